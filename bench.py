@@ -1,0 +1,304 @@
+#!/usr/bin/env python3
+"""Benchmark of the compressed-KV hot path on one MI355X.
+
+Metric: "KV quant GB/s (4-bit, 262K ctx) + CSA sparse-decode tokens/s, 1 GPU".
+
+`value` is the TurboQuant 4-bit encode throughput on BASELINE cfg2 — one full decode KV layer,
+262144 tokens x 1536 (12 heads x 128) bf16, N(0,1) with 2% outlier channels x8, seed 1 — in GB/s of
+algorithmic bytes (805,306,368 read + 201,326,592 codes + 12,582,912 scales = 1,019,215,872 B per
+step), inputs resident in HBM.  One step = one encode of the whole layer (one kernel launch).
+The same line carries, under "secondary", cfg2 decode GB/s, CSA sparse decode tokens/s (cfg5 and
+cfg3), HCA decode tokens/s (cfg4) and the reference microbenchmark shape of sparse_sink_attention.
+
+Timing: W untimed warmup steps, then K steps bracketed by torch.cuda.synchronize() and HIP events
+recorded on the stream the kernels run on (torch's current stream).
+
+cpu_baseline: the CPU oracle (oracle/liboracle.so, a C restatement of turbo_quant.py's encode)
+timed on this host's cores over the cfg2 layer (median of 3 passes).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "deepseek-v4-codebase_amd"))
+
+import torch  # noqa: E402
+
+METRIC = "KV quant GB/s (4-bit, 262K ctx) + CSA sparse-decode tokens/s, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+# cfg2 algorithmic bytes per encode (and per decode)
+T2, H2, D2 = 262144, 12, 128
+N_VEC2 = T2 * H2
+ENC_BYTES = N_VEC2 * (D2 * 2 + D2 // 2 + 4)   # 1,019,215,872
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed(fn, steps: int, warmup: int):
+    """Average ms per call with HIP events on the current stream (bracketed by synchronize)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def cpu_cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
+def bench_encode(args, dev, out):
+    from aetherkv import PolarQuant
+    from aetherkv.synthetic import normal_with_outliers
+
+    log("cfg2: generating 262144x12x128 bf16 (seed 1, 2% outliers x8)")
+    x = normal_with_outliers((T2, H2, D2), 1, device=dev)
+    pq = PolarQuant(4)
+    codes = torch.empty((T2, H2, D2 // 2), dtype=torch.uint8, device=dev)
+    scale = torch.empty((T2, H2, 1), dtype=torch.float32, device=dev)
+    import aetherkv._lib as L
+
+    lib = L.lib()
+    diag = pq._diag(D2, dev)
+    stream = L.stream_of(x)
+    xp, dp, cp, sp = L.ptr(x), L.ptr(diag), L.ptr(codes), L.ptr(scale)
+
+    def enc():
+        L.check(lib.aekv_tq_encode(xp, L.BF16, N_VEC2, D2, 4, dp, cp, sp, stream), "encode")
+
+    ms = timed(enc, args.steps, args.warmup)
+    log(f"cfg2 encode: {ms * 1e3:.1f} us/step, {ENC_BYTES / ms / 1e6:.1f} GB/s")
+    out["encode_ms"] = ms
+    rec = torch.empty((T2, H2, D2), dtype=torch.bfloat16, device=dev)
+    rp = L.ptr(rec)
+
+    def dec():
+        L.check(lib.aekv_tq_decode(cp, sp, N_VEC2, D2, 4, dp, rp, L.BF16, stream), "decode")
+
+    ms_d = timed(dec, args.steps, args.warmup)
+    log(f"cfg2 decode: {ms_d * 1e3:.1f} us/step, {ENC_BYTES / ms_d / 1e6:.1f} GB/s")
+    out["decode_ms"] = ms_d
+    # copy-bandwidth reference (torch copy of the same layer)
+    y = torch.empty_like(x)
+    ms_c = timed(lambda: y.copy_(x), args.steps, args.warmup)
+    out["copy_gbs"] = 2 * x.numel() * 2 / ms_c / 1e6
+    log(f"torch copy of the layer: {out['copy_gbs']:.1f} GB/s")
+    if not args.no_cpu_baseline:
+        out["x_host"] = x.view(torch.int16).cpu()
+    del y, rec
+
+
+def bench_cpu_encode(out):
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    xb = out.pop("x_host").numpy().view(np.uint16)
+    dg = O.diag(42, D2)
+    cores = cpu_cores()
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        O.encode(xb, "bf16", 4, dg, threads=cores)
+        times.append(time.perf_counter() - t)
+    med = sorted(times)[1]
+    log(f"cpu oracle encode (cfg2, {cores} threads): {med:.3f} s, {ENC_BYTES / med / 1e9:.2f} GB/s")
+    return {"value": round(ENC_BYTES / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": "full cfg2 layer (3,145,728 vectors), median of 3 passes of the C oracle encode "
+                      "(oracle/aekv_oracle.c, OpenMP over vectors)"}
+
+
+def make_csa_inputs(dev, B, S, bits, seed, outliers):
+    from aetherkv import PolarQuant
+    from aetherkv.synthetic import normal, normal_with_outliers
+
+    H, D, W, IH, IC = 12, 128, 128, 4, 64
+    pq = PolarQuant(bits)
+    gen = (lambda shape, s: normal_with_outliers(shape, s, device=dev, trailing_dims=1)) if outliers else \
+        (lambda shape, s: normal(shape, s, device=dev))
+    kv_codes, kv_scale = pq.encode(gen((B, S, D), seed))
+    ix_codes, ix_scale = pq.encode(gen((B, S, IC), seed + 1000))
+    torch.cuda.empty_cache()
+    return dict(
+        pq=pq, kv_codes=kv_codes, kv_scale=kv_scale, ix_codes=ix_codes, ix_scale=ix_scale,
+        q=normal((B, 1, H, D), seed + 1, device=dev),
+        index_q=normal((B, IH, IC), seed + 2, dtype=torch.float32, device=dev),
+        index_w=normal((B, IH), seed + 3, dtype=torch.float32, device=dev),
+        win=normal((B, W, D), seed + 4, device=dev),
+        sink=normal((H,), seed + 5, dtype=torch.float32, device=dev),
+    )
+
+
+def bench_csa(args, dev, B, S, bits, seed, outliers, name):
+    from aetherkv.decode import attention_workspace, csa_indexer_topk_quant, indexer_workspace, quant_sink_attention
+
+    log(f"{name}: CSA decode B={B} S={S} {bits}-bit")
+    inp = make_csa_inputs(dev, B, S, bits, seed, outliers)
+    k = 256
+    H, D = 12, 128
+    ws_i = indexer_workspace(B, S, k, dev)
+    ws_a = attention_workspace(B, H, D, k, 128, dev)
+    idx = torch.empty((B, k), dtype=torch.int64, device=dev)
+    out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
+    pq = inp["pq"]
+
+    def index_only():
+        csa_indexer_topk_quant(inp["index_q"], inp["index_w"], inp["ix_codes"], inp["ix_scale"], k, quant=pq,
+                               workspace=ws_i, out=idx)
+
+    def attn_only():
+        quant_sink_attention(inp["q"], inp["kv_codes"], inp["kv_scale"], idx, inp["win"], inp["sink"], D ** -0.5,
+                             quant=pq, workspace=ws_a, out=out)
+
+    def step():
+        index_only()
+        attn_only()
+
+    ms = timed(step, args.steps, args.warmup)
+    ms_i = timed(index_only, args.steps, args.warmup)
+    ms_a = timed(attn_only, args.steps, args.warmup)
+    row_bytes = (D if bits == 8 else D // 2) + 4
+    ix_bytes = (64 if bits == 8 else 32) + 4
+    step_bytes = B * (S * ix_bytes + k * row_bytes + 128 * D * 2 + H * D * 2 * 2)
+    res = {"B": B, "S": S, "bits": bits, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / ms * 1e3, 1),
+           "indexer_ms": round(ms_i, 5), "attention_ms": round(ms_a, 5), "bytes_per_step": step_bytes,
+           "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    log(f"{name}: {ms * 1e3:.1f} us/step ({ms_i * 1e3:.1f} indexer + {ms_a * 1e3:.1f} attention) "
+        f"-> {res['tokens_per_s']:.0f} tok/s, {res['hbm_frac'] * 100:.1f}% of HBM peak")
+    del inp
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_hca(args, dev):
+    from aetherkv import PolarQuant
+    from aetherkv.decode import attention_workspace, quant_sink_attention
+    from aetherkv.synthetic import normal, rope_interleaved
+
+    B, H, D, S, W = 32, 12, 128, 2048, 128
+    log(f"cfg4: HCA decode B={B} S={S} 4-bit")
+    pq = PolarQuant(4)
+    blocks = rope_interleaved(normal((B, S, D), 3, device=dev), torch.arange(S, device=dev) * 128 + 127)
+    codes, scale = pq.encode(blocks)
+    q = normal((B, 1, H, D), 4, device=dev)
+    win = normal((B, W, D), 5, device=dev)
+    sink = normal((H,), 6, dtype=torch.float32, device=dev)
+    ws = attention_workspace(B, H, D, S, W, dev)
+    out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
+    ms = timed(lambda: quant_sink_attention(q, codes, scale, None, win, sink, D ** -0.5, quant=pq, workspace=ws,
+                                            out=out), args.steps, args.warmup)
+    flops = 2 * 2 * B * H * (S + W) * D
+    step_bytes = B * (S * (D // 2 + 4) + W * D * 2 + H * D * 4)
+    res = {"B": B, "S": S, "bits": 4, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / ms * 1e3, 1),
+           "tflops": round(flops / ms / 1e9, 3), "mfma_frac": round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 5),
+           "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    log(f"cfg4: {ms * 1e3:.1f} us/step -> {res['tokens_per_s']:.0f} tok/s")
+    return res
+
+
+def bench_sparse_report_shape(args, dev):
+    from aetherkv import sparse_sink_attention
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(1, 128, 16, 128, device=dev, generator=g).half()
+    kv = torch.randn(1, 8192, 2, 128, device=dev, generator=g).half()
+    topk = torch.randint(0, 8192, (1, 128, 64), device=dev, generator=g, dtype=torch.int32)
+    sink = torch.zeros(16, device=dev).half()
+    ms = timed(lambda: sparse_sink_attention(q, kv, topk, sink, 128 ** -0.5), args.steps, args.warmup)
+    log(f"sparse_sink_attention report shape: {ms * 1e3:.1f} us (reference published 75.9 us)")
+    return {"shape": "fp16 B=1 T=128 H=16 D=128 S=8192 top_k=64", "ms": round(ms, 5), "reference_published_ms": 0.0759}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=["all", "encode", "csa", "hca", "sparse"], default="all")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the sharded design is "
+              "described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+    import aetherkv._lib as L
+
+    if not L.available():
+        print("libaetherkv.so is not built; run `python __graft_entry__.py` first", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    res = {}
+    secondary = {}
+    cpu = None
+    if args.only in ("all", "encode"):
+        bench_encode(args, dev, res)
+        if not args.no_cpu_baseline:
+            cpu = bench_cpu_encode(res)
+        torch.cuda.empty_cache()
+    if args.only in ("all", "csa"):
+        secondary["csa_decode_cfg5"] = bench_csa(args, dev, 64, 65536, 4, 4, True, "cfg5")
+        secondary["csa_decode_cfg3"] = bench_csa(args, dev, 8, 16384, 8, 2, False, "cfg3")
+    if args.only in ("all", "hca"):
+        secondary["hca_decode_cfg4"] = bench_hca(args, dev)
+    if args.only in ("all", "sparse"):
+        secondary["sparse_sink_attention_report_shape"] = bench_sparse_report_shape(args, dev)
+
+    line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic"}
+    if "encode_ms" in res:
+        ms = res["encode_ms"]
+        gbs = ENC_BYTES / ms / 1e6
+        traffic = None
+        pmc = ROOT / "profiles" / "tq_encode_cfg2_traffic.json"
+        if pmc.exists():
+            traffic = json.loads(pmc.read_text()).get("hbm_bytes_per_launch")
+        line.update({
+            "value": round(gbs, 2), "unit": "GB/s", "ms_per_step": round(ms, 5),
+            "config": {"workload": "cfg2: TurboQuant 4-bit encode (WHT + absmax quantise + nibble pack) of one "
+                                   "262144-token x 1536 (12x128) bf16 KV layer, N(0,1) with 2% outlier channels x8, "
+                                   "seed 1", "tokens": T2, "heads": H2, "head_dim": D2, "bits": 4,
+                       "bytes_per_step": ENC_BYTES},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                         "kernel": "tq_forward_kernel<BF16,128,ENC4>"},
+        })
+        secondary["tq_decode_cfg2"] = {"ms": round(res["decode_ms"], 5),
+                                       "GB/s": round(ENC_BYTES / res["decode_ms"] / 1e6, 2),
+                                       "frac": round(ENC_BYTES / res["decode_ms"] / 1e6 / HBM_PEAK_GBS, 4)}
+        secondary["copy_GB/s"] = round(res["copy_gbs"], 1)
+    else:
+        first = next(iter(secondary.values()), {})
+        line.update({"value": first.get("tokens_per_s"), "unit": "tokens/s", "ms_per_step": first.get("ms_per_step"),
+                     "config": {"workload": args.only}})
+    line["cpu_baseline"] = cpu
+    line["secondary"] = secondary
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

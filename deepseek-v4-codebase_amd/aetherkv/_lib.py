@@ -1,0 +1,124 @@
+"""ctypes binding of libaetherkv.so (the C ABI declared in include/aetherkv.h).
+
+Torch tensors enter the ABI only as raw device pointers (``tensor.data_ptr()``), int64 sizes and
+the current HIP stream handle.  A non-zero status becomes ``ValueError`` (AEKV_ERR_VALUE) or
+``RuntimeError`` (everything else) carrying the library's message, matching the reference's
+split between the quantiser's ``ValueError`` (turbo_quant.py:58-59, :98-99) and the extension's
+``TORCH_CHECK`` ``RuntimeError`` (bindings.cpp:5-9).
+
+There is no fallback: if the library is missing every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libaetherkv.so"
+
+# aekv_status
+OK, ERR_VALUE, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_WORKSPACE, ERR_HIP, ERR_UNSUPPORTED = range(8)
+# aekv_dtype
+F32, F16, BF16, I32, I64 = range(5)
+# aekv_index_mode
+INDEX_MODES = {"softplus": 0, "raw": 1, "relu_w": 2}
+
+TORCH_TO_AEKV = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int32: I32, torch.int64: I64}
+
+SYMBOLS = (
+    "aekv_version", "aekv_last_error", "aekv_max_head_dim", "aekv_max_topk", "aekv_tq_diag", "aekv_wht",
+    "aekv_tq_encode", "aekv_tq_decode", "aekv_csa_indexer_workspace_size", "aekv_csa_indexer_topk",
+    "aekv_csa_indexer_topk_quant", "aekv_sparse_sink_attention", "aekv_quant_attention_workspace_size",
+    "aekv_quant_sink_attention", "aekv_hca_compress", "aekv_tiled_prefill_attention",
+)
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class LibraryUnavailable(RuntimeError):
+    pass
+
+
+def available() -> bool:
+    return LIB_PATH.exists()
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise LibraryUnavailable(
+            f"libaetherkv.so not found at {LIB_PATH}; build it with `python -m aetherkv.build` "
+            "(or __graft_entry__.build())")
+    L = ctypes.CDLL(str(LIB_PATH))
+    P, I64_, I32_, SZ, F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t, ctypes.c_float
+    sig = {
+        "aekv_version": ([], ctypes.c_char_p),
+        "aekv_last_error": ([], ctypes.c_char_p),
+        "aekv_max_head_dim": ([], I32_),
+        "aekv_max_topk": ([], I32_),
+        "aekv_tq_diag": ([I64_, I32_, P], ctypes.c_int),
+        "aekv_wht": ([P, I32_, I64_, I32_, P, P], ctypes.c_int),
+        "aekv_tq_encode": ([P, I32_, I64_, I32_, I32_, P, P, P, P], ctypes.c_int),
+        "aekv_tq_decode": ([P, P, I64_, I32_, I32_, P, P, I32_, P], ctypes.c_int),
+        "aekv_csa_indexer_workspace_size": ([I64_, I64_, I32_], SZ),
+        "aekv_csa_indexer_topk": ([P, P, P, P, I64_, I64_, I32_, I32_, I32_, I32_, P, SZ, P, P, P], ctypes.c_int),
+        "aekv_csa_indexer_topk_quant": ([P, P, P, P, P, P, I64_, I64_, I32_, I32_, I32_, I32_, I32_, P, SZ, P, P, P],
+                                        ctypes.c_int),
+        "aekv_sparse_sink_attention": ([P, P, P, I32_, P, I64_, I32_, I64_, I64_, I64_, I64_, I64_, I64_, F, P, P],
+                                       ctypes.c_int),
+        "aekv_quant_attention_workspace_size": ([I64_, I64_, I64_, I64_, I64_], SZ),
+        "aekv_quant_sink_attention": ([P, P, P, P, P, P, P, I64_, I64_, I64_, I64_, I64_, I64_, I32_, F, P, SZ, P, P],
+                                      ctypes.c_int),
+        "aekv_hca_compress": ([P, P, I32_, I64_, I64_, I64_, P, P], ctypes.c_int),
+        "aekv_tiled_prefill_attention": ([P, P, P, I64_, I32_, I64_, I64_, I64_, I64_, I64_, F, I32_, P, P],
+                                         ctypes.c_int),
+    }
+    for name, (argtypes, restype) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == OK:
+        return
+    msg = lib().aekv_last_error().decode("utf-8", "replace") or f"{what} failed with status {rc}"
+    if rc == ERR_VALUE:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_device(name: str, *tensors: Optional[torch.Tensor]) -> None:
+    """The product path runs on HIP devices only; CPU tensors are rejected loudly."""
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(f"{name} must be a HIP device tensor (got {t.device}); aetherkv has no CPU path")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return TORCH_TO_AEKV[t.dtype]
+    except KeyError as exc:
+        raise RuntimeError(f"unsupported dtype {t.dtype}") from exc
+
+
+def aligned(t: torch.Tensor, nbytes: int) -> torch.Tensor:
+    """Contiguous tensor whose data pointer is a multiple of `nbytes` (copies only when needed)."""
+    t = t.contiguous()
+    if t.numel() and t.data_ptr() % nbytes:
+        t = t.clone()
+    return t

@@ -1,0 +1,80 @@
+"""Ahead-of-time build of libaetherkv.so for gfx950 (hipcc, in-tree).
+
+Every source under ``csrc/`` is compiled in parallel with hipcc ``--offload-arch=gfx950`` and linked
+into ``aetherkv/libaetherkv.so`` next to this file, so the library travels with the source tree.
+
+Flags that matter for parity:
+  -ffp-contract=off                              no silent FMA contraction (bit-exact codec)
+  -fhip-fp32-correctly-rounded-divide-sqrt       IEEE division, as torch's fp32 `/`
+  -Xclang -target-feature -Xclang -packed-fp32-ops   no packed-fp32 VALU ops
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent                      # deepseek-v4-codebase_amd/
+CSRC = ROOT / "csrc"
+INCLUDE = ROOT.parent / "include"
+LIB = PKG / "libaetherkv.so"
+OBJ_DIR = ROOT / "_build"
+
+ARCH = os.environ.get("AETHERKV_ARCH", "gfx950")
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm toolchain required to build libaetherkv)")
+
+
+def sources():
+    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+
+
+def _compile(src: Path) -> Path:
+    obj = OBJ_DIR / (src.name + ".o")
+    cmd = [hipcc(), *COMMON_FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
+    return obj
+
+
+def build(verbose: bool = False, jobs: int = 8) -> Path:
+    """Compile every HIP source and link libaetherkv.so (always rebuilds)."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    srcs = sources()
+    with ThreadPoolExecutor(max_workers=min(jobs, len(srcs))) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}", file=sys.stderr)
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)

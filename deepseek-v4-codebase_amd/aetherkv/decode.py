@@ -1,0 +1,163 @@
+"""Quantised compressed-KV decode step on MI355X: CSA indexer + top-k + sparse sink attention, and
+HCA block attention, reading TurboQuant codes directly (no dequantised cache is materialised).
+
+What the reference decode step does (aether_2b/serving.py):
+  CSA  :597-625  dequantise the whole index cache and KV cache (_read_compressed :346-376), score
+                 blocks (einsum -> relu -> x weight -> sum over heads, :618-619), topk(min(256, S)),
+                 gather, concat the bf16 window, attend with the sink (_run_backend :450-467).
+  HCA  :507-522  dequantise every visible block, concat the window, attend with full indices.
+Here each step is two fused HIP stages: the indexer scans the index codes in the rotated domain and
+selects the top-k exactly; the attention kernel gathers the selected code rows, dequantises them in
+registers, attends them together with the window and the per-head sink, and rotates the value sum
+back once per head.
+
+Score rule: ``mode="softplus"`` (aether_2b/modeling.py:609-611, default), ``"raw"`` (the serving
+engine's sum_h w_h relu(q_h.k), serving.py:618-619) or ``"relu_w"`` (csa_indexer_cuda.cu:222-231).
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from .turbo_quant import PolarQuant
+
+
+def _scale_2d(scale: torch.Tensor, B: int, S: int) -> torch.Tensor:
+    s = scale.to(torch.float32).contiguous()
+    if s.numel() != B * S:
+        raise RuntimeError(f"scale must hold B*S = {B * S} values, got shape {tuple(scale.shape)}")
+    return s
+
+
+def indexer_workspace(B: int, S: int, k: int, device) -> torch.Tensor:
+    return torch.empty(_lib.lib().aekv_csa_indexer_workspace_size(B, S, k), dtype=torch.uint8, device=device)
+
+
+def attention_workspace(B: int, H: int, D: int, n_comp: int, W: int, device) -> torch.Tensor:
+    return torch.empty(_lib.lib().aekv_quant_attention_workspace_size(B, H, D, n_comp, W), dtype=torch.uint8,
+                       device=device)
+
+
+def csa_indexer_topk_quant(index_q: torch.Tensor, index_weight: torch.Tensor, key_codes: torch.Tensor,
+                           key_scale: torch.Tensor, k: int, *, quant: PolarQuant,
+                           valid: Optional[torch.Tensor] = None, mode: str = "softplus",
+                           return_scores: bool = False, workspace: Optional[torch.Tensor] = None,
+                           out: Optional[torch.Tensor] = None):
+    """Top-k block indices [B, k] (int64, sorted by score desc then index asc; -1 pads rows whose
+    valid count is below k) over TurboQuant-coded index keys.
+
+    index_q [B, IH, IC] fp32, index_weight [B, IH] fp32 (raw; the rule applies softplus),
+    key_codes [B, S, IC] int8 (8-bit) or [B, S, IC/2] uint8 (4-bit), key_scale [B, S(, 1)] fp32,
+    valid [B] int32 visible block count per row (None: all S).
+    """
+    _lib.require_device("index_q", index_q, index_weight, key_codes, key_scale, valid)
+    if mode not in _lib.INDEX_MODES:
+        raise ValueError(f"mode must be one of {sorted(_lib.INDEX_MODES)}, got {mode!r}")
+    B, IH, IC = index_q.shape
+    S = key_codes.size(1)
+    bits = quant.bits
+    want = torch.int8 if bits == 8 else torch.uint8
+    if key_codes.dtype != want:
+        raise RuntimeError(f"{bits}-bit index codes must be {want}, got {key_codes.dtype}")
+    if key_codes.size(-1) * (1 if bits == 8 else 2) != IC or key_codes.size(0) != B:
+        raise RuntimeError(f"key_codes shape {tuple(key_codes.shape)} does not match index_q {tuple(index_q.shape)}")
+    q = index_q.to(torch.float32).contiguous()
+    w = index_weight.to(torch.float32).contiguous()
+    codes = key_codes.contiguous()
+    sc = _scale_2d(key_scale, B, S)
+    v = None if valid is None else valid.to(torch.int32).contiguous()
+    diag = quant._diag(IC, index_q.device)
+    L = _lib.lib()
+    if out is None:
+        out = torch.empty((B, k), dtype=torch.int64, device=index_q.device)
+    scores = torch.empty((B, k), dtype=torch.float32, device=index_q.device) if return_scores else None
+    if workspace is None:
+        workspace = indexer_workspace(B, S, k, index_q.device)
+    with torch.cuda.device(index_q.device):
+        _lib.check(L.aekv_csa_indexer_topk_quant(
+            _lib.ptr(q), _lib.ptr(w), _lib.ptr(codes), _lib.ptr(sc), _lib.ptr(diag), _lib.ptr(v), B, S, IH, IC, bits,
+            int(k), _lib.INDEX_MODES[mode], _lib.ptr(workspace), workspace.numel(), _lib.ptr(out), _lib.ptr(scores),
+            _lib.stream_of(index_q)), "aekv_csa_indexer_topk_quant")
+    return (out, scores) if return_scores else out
+
+
+def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tensor, sel: Optional[torch.Tensor],
+                         window: Optional[torch.Tensor], sink: torch.Tensor, softmax_scale: float, *,
+                         quant: PolarQuant, workspace: Optional[torch.Tensor] = None,
+                         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode-step sink attention over [dequant(codes[sel]) ; window] with K = V.
+
+    q [B, 1, H, D] or [B, H, D] bf16; codes [B, S, D] int8 | [B, S, D/2] uint8; scale [B, S(, 1)];
+    sel [B, K] int64 block indices (None: all S blocks — HCA); window [B, W, D] bf16 or None;
+    sink [H].  Returns bf16 with q's shape.
+    """
+    _lib.require_device("q", q, codes, scale, sel, window, sink)
+    if q.dtype != torch.bfloat16:
+        raise RuntimeError(f"q must be bfloat16, got {q.dtype}")
+    squeeze = q.dim() == 4
+    q3 = q.reshape(q.size(0), q.size(-2), q.size(-1)) if squeeze else q
+    if squeeze and q.size(1) != 1:
+        raise RuntimeError("quant_sink_attention expects one target token per row")
+    B, H, D = q3.shape
+    S = codes.size(1)
+    bits = quant.bits
+    want = torch.int8 if bits == 8 else torch.uint8
+    if codes.dtype != want:
+        raise RuntimeError(f"{bits}-bit codes must be {want}, got {codes.dtype}")
+    if codes.size(-1) * (1 if bits == 8 else 2) != D or codes.size(0) != B:
+        raise RuntimeError(f"codes shape {tuple(codes.shape)} does not match q {tuple(q.shape)}")
+    qc = q3.contiguous()
+    cc = codes.contiguous()
+    sc = _scale_2d(scale, B, S)
+    s64 = None if sel is None else sel.to(torch.int64).contiguous()
+    K = 0 if s64 is None else s64.size(1)
+    if window is not None and window.numel() > 0:
+        if window.dtype != torch.bfloat16 or window.dim() != 3 or window.size(0) != B or window.size(2) != D:
+            raise RuntimeError(f"window must be bf16 [B, W, D], got {window.dtype} {tuple(window.shape)}")
+        win = window.contiguous()
+        W = win.size(1)
+    else:
+        win, W = None, 0
+    sk = sink.to(torch.float32).reshape(-1).contiguous()
+    if sk.numel() == 1:
+        sk = sk.expand(H).contiguous()
+    if sk.numel() != H:
+        raise RuntimeError("sink must be a scalar or a [num_heads] tensor")
+    diag = quant._diag(D, q.device)
+    n_comp = K if s64 is not None else S
+    if workspace is None:
+        workspace = attention_workspace(B, H, D, n_comp, W, q.device)
+    if out is None:
+        out = torch.empty((B, H, D), dtype=torch.bfloat16, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(_lib.lib().aekv_quant_sink_attention(
+            _lib.ptr(qc), _lib.ptr(cc), _lib.ptr(sc), _lib.ptr(s64), _lib.ptr(win), _lib.ptr(sk), _lib.ptr(diag), B, H,
+            D, S, K, W, bits, float(softmax_scale), _lib.ptr(workspace), workspace.numel(), _lib.ptr(out),
+            _lib.stream_of(q)), "aekv_quant_sink_attention")
+    return out.view(B, 1, H, D) if squeeze else out
+
+
+def csa_decode(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.Tensor, index_codes: torch.Tensor,
+               index_scale: torch.Tensor, kv_codes: torch.Tensor, kv_scale: torch.Tensor,
+               window: Optional[torch.Tensor], sink: torch.Tensor, softmax_scale: float, *, kv_quant: PolarQuant,
+               index_quant: Optional[PolarQuant] = None, top_k: int = 256, mode: str = "softplus",
+               valid: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One CSA decode step (serving.py:597-625): returns (attention output like q, selected [B, k])."""
+    index_quant = index_quant or kv_quant
+    S = kv_codes.size(1)
+    k = min(int(top_k), S)
+    if k == 0:
+        return quant_sink_attention(q, kv_codes, kv_scale, kv_codes.new_zeros((q.size(0), 0), dtype=torch.int64),
+                                    window, sink, softmax_scale, quant=kv_quant), None
+    idx = csa_indexer_topk_quant(index_q, index_weight, index_codes, index_scale, k, quant=index_quant, valid=valid,
+                                 mode=mode)
+    out = quant_sink_attention(q, kv_codes, kv_scale, idx, window, sink, softmax_scale, quant=kv_quant)
+    return out, idx
+
+
+def hca_decode(q: torch.Tensor, kv_codes: torch.Tensor, kv_scale: torch.Tensor, window: Optional[torch.Tensor],
+               sink: torch.Tensor, softmax_scale: float, *, kv_quant: PolarQuant) -> torch.Tensor:
+    """One HCA decode step (serving.py:507-522): all blocks + window."""
+    return quant_sink_attention(q, kv_codes, kv_scale, None, window, sink, softmax_scale, quant=kv_quant)

@@ -1,0 +1,100 @@
+// Shared host/device helpers for libaetherkv (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+
+#include "aetherkv.h"
+
+namespace aekv {
+
+// ---- host-side error reporting -------------------------------------------------------------
+// Stores a thread-local message and returns `status` so call sites can `return fail(...)`.
+int fail(int status, const char* fmt, ...);
+// Checks hipGetLastError() after a launch; returns AEKV_OK or AEKV_ERR_HIP with a message.
+int check_launch(const char* what);
+
+inline bool is_pow2(int64_t d) { return d > 0 && (d & (d - 1)) == 0; }
+inline bool is_aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline size_t dtype_size(int dt) { return dt == AEKV_F32 || dt == AEKV_I32 ? 4 : (dt == AEKV_I64 ? 8 : 2); }
+inline bool is_float_dtype(int dt) { return dt == AEKV_F32 || dt == AEKV_F16 || dt == AEKV_BF16; }
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+// fp32(d ** -0.5): the python double d**-0.5 rounded to fp32, as torch does for `out * (d ** -0.5)`.
+float wht_scale(int d);
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---- device helpers ------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __builtin_bit_cast(float, bits16 << 16); }
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+// Two fp32 -> packed bf16x2 with round-to-nearest-even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// Lane exchange with partner lane ^ HL inside a wave64.  HL 1/2 use DPP quad_perm, 4/8/16 the
+// ds_swizzle xor mode (within 32 lanes), 32 a ds_bpermute.
+template <int HL>
+__device__ __forceinline__ float xor_lane(float v) {
+  int i = __builtin_bit_cast(int, v);
+  if constexpr (HL == 1) {
+    i = __builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (HL == 2) {
+    i = __builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (HL == 4 || HL == 8 || HL == 16) {
+    i = __builtin_amdgcn_ds_swizzle(i, (HL << 10) | 0x1F);         // bitmask mode, xor HL
+  } else {
+    static_assert(HL == 32, "xor_lane: HL must be a power of two below 64");
+    i = __builtin_amdgcn_ds_bpermute(static_cast<int>(((threadIdx.x & 63) ^ 32) << 2), i);
+  }
+  return __builtin_bit_cast(float, i);
+}
+
+__device__ __forceinline__ float xor_lane_rt(float v, int hl) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_ds_bpermute(static_cast<int>(((threadIdx.x & 63) ^ hl) << 2), __builtin_bit_cast(int, v)));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += xor_lane<1>(v);
+  v += xor_lane<2>(v);
+  v += xor_lane<4>(v);
+  v += xor_lane<8>(v);
+  v += xor_lane<16>(v);
+  v += xor_lane<32>(v);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, xor_lane<1>(v));
+  v = fmaxf(v, xor_lane<2>(v));
+  v = fmaxf(v, xor_lane<4>(v));
+  v = fmaxf(v, xor_lane<8>(v));
+  v = fmaxf(v, xor_lane<16>(v));
+  v = fmaxf(v, xor_lane<32>(v));
+  return v;
+}
+
+// fp32 score -> uint32 whose unsigned order equals the float order (-inf smallest).
+__device__ __forceinline__ uint32_t order_key(float s) {
+  uint32_t u = __builtin_bit_cast(uint32_t, s);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float order_key_inv(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __builtin_bit_cast(float, u);
+}
+
+}  // namespace aekv

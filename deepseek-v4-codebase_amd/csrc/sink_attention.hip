@@ -1,0 +1,526 @@
+// Sink attention kernels for gfx950.
+//
+// 1. sparse_attn_kernel — drop-in for sparse_sink_attention (aether_kernels/sparse_attention.py:8-16,
+//    semantics aether_kernels/csrc/sparse_sink_attention_cuda.cu:47-114, oracle
+//    aether_pipeline/serving.py:99-130) and, with dense indices, for tiled_prefill_attention
+//    (aether_kernels/sparse_attention.py:19-42) with the sink counted once as in
+//    aether_2b/modeling.py:158-178.  One wave per (b, t, h); keys streamed in tiles of 64 with an
+//    online softmax; the sink joins the normaliser once at the end.
+// 2. quant_attn_partial_kernel + quant_attn_combine_kernel — one decode token per row over
+//    TurboQuant-compressed shared K=V blocks (selected by the CSA indexer, or all blocks for HCA)
+//    plus a bf16 sliding window (aether_2b/serving.py:507-522, :597-625).  Split-KV: each workgroup
+//    attends one tile of sources for all heads of a row and writes (max, sum, acc); the combine
+//    merges tiles with the sink and rotates the compressed part back once per head:
+//      sum_j p_j K_j = diag * WHT(sum_j p_j scale_j codes_j)   (K_j = diag * WHT(scale_j codes_j)).
+// 3. hca_compress_kernel — softmax over the M window positions and weighted sum
+//    (aether_kernels/sparse_attention.py:70-83; aether_2b/serving.py:495-497).
+#include "aekv_common.h"
+
+namespace aekv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 64;           // keys per online-softmax step in sparse_attn_kernel
+constexpr int kMaxD = 512;
+constexpr int kTileFloats = 8192;   // source tile of quant_attn_partial_kernel (32 KB)
+constexpr float kNegInf = -__builtin_inff();
+
+template <int DT>
+__device__ __forceinline__ float ld(const void* p, int64_t i) {
+  if constexpr (DT == AEKV_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == AEKV_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void st(void* p, int64_t i, float v) {
+  if constexpr (DT == AEKV_F32) static_cast<float*>(p)[i] = v;
+  else if constexpr (DT == AEKV_BF16) static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(pack_bf16x2(v, 0.0f) & 0xffffu);
+  else static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_f16_bits(v));
+}
+
+// ------------------------------------------------------------------------------------------
+// 1. general sparse sink attention
+// ------------------------------------------------------------------------------------------
+template <int DT, int IDX>  // IDX: 0 dense (index = position), 4 int32, 8 int64
+__global__ __launch_bounds__(kThreads) void sparse_attn_kernel(const void* __restrict__ q, const void* __restrict__ kv,
+                                                               const void* __restrict__ idx,
+                                                               const void* __restrict__ sink, int sink_scalar,
+                                                               int64_t rows, int64_t T, int64_t H, int D, int64_t S,
+                                                               int64_t K, float scale, void* __restrict__ out) {
+  __shared__ float qsh[kThreads / 64][kMaxD];
+  __shared__ float psh[kThreads / 64][kTile];
+  __shared__ int64_t ish[kThreads / 64][kTile];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + w;  // (b, t, h) flattened
+  if (row >= rows) return;  // wave-uniform
+  const int64_t h = row % H;
+  const int64_t bt = row / H;
+  const int64_t b = bt / T;
+  for (int d = lane; d < D; d += 64) qsh[w][d] = ld<DT>(q, row * D + d);
+  const float sk = ld<DT>(sink, sink_scalar ? 0 : h);
+  constexpr int kMaxDPL = kMaxD / 64;
+  float acc[kMaxDPL];
+#pragma unroll
+  for (int i = 0; i < kMaxDPL; ++i) acc[i] = 0.0f;
+  float m = kNegInf, l = 0.0f;
+  __builtin_amdgcn_wave_barrier();
+
+  for (int64_t j0 = 0; j0 < K; j0 += kTile) {
+    const int64_t j = j0 + lane;
+    int64_t src = -1;
+    if (j < K) {
+      if constexpr (IDX == 0) src = j;
+      else if constexpr (IDX == 4) src = static_cast<const int32_t*>(idx)[bt * K + j];
+      else src = static_cast<const int64_t*>(idx)[bt * K + j];
+    }
+    float logit = kNegInf;
+    if (src >= 0 && src < S) {
+      const int64_t kbase = ((b * S + src) * 2 + 0) * D;
+      float dot = 0.0f;
+      for (int d = 0; d < D; ++d) dot = fmaf(qsh[w][d], ld<DT>(kv, kbase + d), dot);
+      logit = dot * scale;
+    } else {
+      src = -1;
+    }
+    const float tmax = wave_max(logit);
+    const float mnew = fmaxf(m, tmax);
+    const float p = (src >= 0) ? __expf(logit - mnew) : 0.0f;
+    const float corr = (m == kNegInf) ? 0.0f : __expf(m - mnew);
+    l = l * corr + wave_sum(p);
+#pragma unroll
+    for (int i = 0; i < kMaxDPL; ++i) acc[i] *= corr;
+    m = (mnew == kNegInf) ? m : mnew;
+    psh[w][lane] = p;
+    ish[w][lane] = src;
+    __builtin_amdgcn_wave_barrier();
+    const int nt = static_cast<int>(min<int64_t>(kTile, K - j0));
+    for (int jj = 0; jj < nt; ++jj) {
+      const int64_t s = ish[w][jj];
+      if (s < 0) continue;  // uniform across the wave
+      const float pj = psh[w][jj];
+      const int64_t vbase = ((b * S + s) * 2 + 1) * D;
+#pragma unroll
+      for (int i = 0; i < kMaxDPL; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) acc[i] = fmaf(pj, ld<DT>(kv, vbase + d), acc[i]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // sink joins the normaliser once: M = max(m, sink)
+  const float M = fmaxf(m, sk);
+  const float cm = (m == kNegInf) ? 0.0f : __expf(m - M);
+  const float den = l * cm + __expf(sk - M);
+  const float f = cm / den;
+#pragma unroll
+  for (int i = 0; i < kMaxDPL; ++i) {
+    const int d = lane + 64 * i;
+    if (d < D) st<DT>(out, row * D + d, acc[i] * f);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// 2. quantised decode attention
+// ------------------------------------------------------------------------------------------
+struct QAttnArgs {
+  const uint16_t* q;      // [B, H, D] bf16
+  const uint8_t* codes;   // [B, S, D or D/2]
+  const float* scale;     // [B, S]
+  const int64_t* sel;     // [B, K] or null
+  const uint16_t* win;    // [B, W, D] bf16
+  const float* sink;      // [H]
+  const float* diag;      // [D]
+  int64_t S, K, W;
+  int H, D, bits, ts;     // ts: sources per tile
+  int n_comp_tiles, n_tiles;
+  float sm_scale, wscale;
+  float* part;            // [B, n_tiles, H, D + 2]
+  uint16_t* out;          // [B, H, D] bf16
+};
+
+// q (or WHT(diag*q) when `rotate`) for all heads of row b into qs[H*D] (uses qtmp as scratch).
+__device__ void load_query(const QAttnArgs& a, int64_t b, bool rotate, float* qs, float* qtmp) {
+  const int HD = a.H * a.D;
+  for (int i = threadIdx.x; i < HD; i += kThreads) {
+    float v = bf16_to_f32(a.q[b * HD + i]);
+    if (rotate) v = v * a.diag[i % a.D];
+    qs[i] = v;
+  }
+  __syncthreads();
+  if (!rotate) return;
+  float* src = qs;
+  float* dst = qtmp;
+  const int pairs = HD / 2, half = a.D / 2;
+  for (int hh = 1; hh < a.D; hh <<= 1) {
+    for (int p = threadIdx.x; p < pairs; p += kThreads) {
+      const int head = p / half, r = p % half;
+      const int i = head * a.D + (r / hh) * 2 * hh + (r % hh);
+      const float x = src[i], y = src[i + hh];
+      dst[i] = x + y;
+      dst[i + hh] = x - y;
+    }
+    __syncthreads();
+    float* t = src;
+    src = dst;
+    dst = t;
+  }
+  for (int i = threadIdx.x; i < HD; i += kThreads) qs[i] = src[i] * a.wscale;
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kThreads) void quant_attn_partial_kernel(QAttnArgs a) {
+  extern __shared__ float smem[];
+  const int H = a.H, D = a.D, DP = D + 1, ts = a.ts;
+  float* qs = smem;                       // H*D
+  float* qtmp = qs + H * D;               // H*D
+  float* X = qtmp + H * D;                // ts * (D+1)
+  float* sig = X + ts * DP;               // ts   (scale_j, 1 for window; 0 = invalid)
+  float* P = sig + ts;                    // H * ts
+  float* stat = P + H * ts;               // 2*H  (max, sum)
+
+  const int64_t b = blockIdx.y;
+  const int tile = blockIdx.x;
+  const bool comp = tile < a.n_comp_tiles;
+  const int64_t n_src = comp ? (a.sel ? a.K : a.S) : a.W;
+  const int64_t j0 = static_cast<int64_t>(comp ? tile : tile - a.n_comp_tiles) * ts;
+  const int nt = static_cast<int>(min<int64_t>(ts, n_src - j0));
+
+  load_query(a, b, comp, qs, qtmp);
+
+  // stage the source tile (integer codes for compressed blocks, bf16 values for the window)
+  const int row_bytes = a.bits == 8 ? D : D / 2;
+  for (int e = threadIdx.x; e < nt * D; e += kThreads) {
+    const int jj = e / D, d = e % D;
+    float v;
+    if (comp) {
+      const int64_t s = a.sel ? a.sel[b * a.K + j0 + jj] : j0 + jj;
+      if (s < 0 || s >= a.S) {
+        v = 0.0f;
+      } else {
+        const uint8_t* cp = a.codes + (b * a.S + s) * row_bytes;
+        if (a.bits == 8) {
+          v = static_cast<float>(static_cast<int8_t>(cp[d]));
+        } else {
+          const uint32_t byte = cp[d >> 1];
+          const uint32_t nib = (d & 1) ? (byte >> 4) : (byte & 0x0fu);
+          v = static_cast<float>((static_cast<int>(nib) ^ 8) - 8);
+        }
+      }
+    } else {
+      v = bf16_to_f32(a.win[(b * a.W + j0 + jj) * D + d]);
+    }
+    X[jj * DP + d] = v;
+  }
+  for (int jj = threadIdx.x; jj < nt; jj += kThreads) {
+    float s = 1.0f;
+    if (comp) {
+      const int64_t src = a.sel ? a.sel[b * a.K + j0 + jj] : j0 + jj;
+      s = (src < 0 || src >= a.S) ? 0.0f : a.scale[b * a.S + src];
+    }
+    sig[jj] = s;
+  }
+  __syncthreads();
+
+  // logits
+  for (int p = threadIdx.x; p < H * nt; p += kThreads) {
+    const int h = p / nt, jj = p % nt;
+    const float* qh = qs + h * D;
+    const float* xj = X + jj * DP;
+    float dot = 0.0f;
+    for (int d = 0; d < D; ++d) dot = fmaf(qh[d], xj[d], dot);
+    P[h * ts + jj] = sig[jj] == 0.0f ? kNegInf : (dot * sig[jj]) * a.sm_scale;
+  }
+  __syncthreads();
+
+  // per-head tile softmax (one wave per head, round robin)
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int h = w; h < H; h += kThreads / 64) {
+    float mx = kNegInf;
+    for (int jj = lane; jj < nt; jj += 64) mx = fmaxf(mx, P[h * ts + jj]);
+    mx = wave_max(mx);
+    float sum = 0.0f;
+    for (int jj = lane; jj < nt; jj += 64) {
+      const float l = P[h * ts + jj];
+      const float e = l == kNegInf ? 0.0f : __expf(l - mx);
+      sum += e;
+      P[h * ts + jj] = e * sig[jj];  // fold scale_j into the weight of the code vector
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) {
+      stat[2 * h] = mx;
+      stat[2 * h + 1] = sum;
+    }
+  }
+  __syncthreads();
+
+  // PV
+  float* dst = a.part + ((b * a.n_tiles + tile) * H) * (D + 2);
+  for (int p = threadIdx.x; p < H * D; p += kThreads) {
+    const int h = p / D, d = p % D;
+    const float* ph = P + h * ts;
+    float acc = 0.0f;
+    for (int jj = 0; jj < nt; ++jj) acc = fmaf(ph[jj], X[jj * DP + d], acc);
+    dst[h * (D + 2) + 2 + d] = acc;
+  }
+  for (int h = threadIdx.x; h < H; h += kThreads) {
+    dst[h * (D + 2)] = stat[2 * h];
+    dst[h * (D + 2) + 1] = stat[2 * h + 1];
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void quant_attn_combine_kernel(QAttnArgs a) {
+  extern __shared__ float smem[];
+  const int H = a.H, D = a.D;
+  float* rot = smem;          // H*D
+  float* rtmp = rot + H * D;  // H*D
+  float* win = rtmp + H * D;  // H*D
+  float* fac = win + H * D;   // n_tiles * H   (e^{m_t - M})
+  float* den = fac + a.n_tiles * H;  // H
+  const int64_t b = blockIdx.x;
+  const float* part = a.part + (b * a.n_tiles) * H * (D + 2);
+
+  for (int h = threadIdx.x; h < H; h += kThreads) {
+    const float sk = a.sink[h];
+    float M = sk;
+    for (int t = 0; t < a.n_tiles; ++t) M = fmaxf(M, part[(t * H + h) * (D + 2)]);
+    float L = __expf(sk - M);
+    for (int t = 0; t < a.n_tiles; ++t) {
+      const float mt = part[(t * H + h) * (D + 2)];
+      const float f = mt == kNegInf ? 0.0f : __expf(mt - M);
+      fac[t * H + h] = f;
+      L += f * part[(t * H + h) * (D + 2) + 1];
+    }
+    den[h] = L;
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < H * D; p += kThreads) {
+    const int h = p / D, d = p % D;
+    float r = 0.0f, wv = 0.0f;
+    for (int t = 0; t < a.n_tiles; ++t) {
+      const float v = fac[t * H + h] * part[(t * H + h) * (D + 2) + 2 + d];
+      if (t < a.n_comp_tiles) r += v; else wv += v;
+    }
+    rot[p] = r;
+    win[p] = wv;
+  }
+  __syncthreads();
+  // rotate the compressed part back: diag * WHT(rot)
+  float* src = rot;
+  float* dst = rtmp;
+  const int pairs = H * D / 2, half = D / 2;
+  for (int hh = 1; hh < D; hh <<= 1) {
+    for (int p = threadIdx.x; p < pairs; p += kThreads) {
+      const int head = p / half, r = p % half;
+      const int i = head * D + (r / hh) * 2 * hh + (r % hh);
+      const float x = src[i], y = src[i + hh];
+      dst[i] = x + y;
+      dst[i + hh] = x - y;
+    }
+    __syncthreads();
+    float* t = src;
+    src = dst;
+    dst = t;
+  }
+  for (int p = threadIdx.x; p < H * D; p += kThreads) {
+    const int h = p / D, d = p % D;
+    const float o = ((src[p] * a.wscale) * a.diag[d] + win[p]) / den[h];
+    a.out[b * H * D + p] = static_cast<uint16_t>(pack_bf16x2(o, 0.0f) & 0xffffu);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// 3. hca_compress
+// ------------------------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(kThreads) void hca_compress_kernel(const void* __restrict__ c, const void* __restrict__ z,
+                                                                int64_t B, int64_t M, int64_t D, void* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= B * D) return;
+  const int64_t b = i / D, d = i % D;
+  float mx = kNegInf;
+  for (int64_t m = 0; m < M; ++m) mx = fmaxf(mx, ld<DT>(z, (b * M + m) * D + d));
+  float den = 0.0f, acc = 0.0f;
+  for (int64_t m = 0; m < M; ++m) {
+    const float e = __expf(ld<DT>(z, (b * M + m) * D + d) - mx);
+    den += e;
+    acc = fmaf(e, ld<DT>(c, (b * M + m) * D + d), acc);
+  }
+  st<DT>(out, i, acc / den);
+}
+
+__global__ void zero_u16_kernel(uint16_t* __restrict__ p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// Dynamic LDS above 64 KB must be enabled per kernel; done once per process.
+void allow_big_lds() {
+  static const bool done = [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(quant_attn_partial_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(quant_attn_combine_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    return true;
+  }();
+  (void)done;
+}
+
+template <int DT>
+int launch_sparse(int idx_kind, const void* q, const void* kv, const void* topk, const void* sink, int scalar,
+                  int64_t B, int64_t T, int64_t H, int64_t D, int64_t S, int64_t K, float scale, void* out,
+                  hipStream_t st) {
+  const int64_t rows = B * T * H;
+  const dim3 grid(static_cast<uint32_t>(ceil_div(rows, kThreads / 64)));
+  if (idx_kind == 0)
+    hipLaunchKernelGGL((sparse_attn_kernel<DT, 0>), grid, dim3(kThreads), 0, st, q, kv, topk, sink, scalar, rows, T, H,
+                       static_cast<int>(D), S, K, scale, out);
+  else if (idx_kind == 4)
+    hipLaunchKernelGGL((sparse_attn_kernel<DT, 4>), grid, dim3(kThreads), 0, st, q, kv, topk, sink, scalar, rows, T, H,
+                       static_cast<int>(D), S, K, scale, out);
+  else
+    hipLaunchKernelGGL((sparse_attn_kernel<DT, 8>), grid, dim3(kThreads), 0, st, q, kv, topk, sink, scalar, rows, T, H,
+                       static_cast<int>(D), S, K, scale, out);
+  return AEKV_OK;
+}
+
+int sparse_common(const void* q, const void* kv, const void* topk, int idx_kind, const void* sink, int64_t sink_numel,
+                  int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D, int64_t S, int64_t K, float scale,
+                  void* out, void* stream, const char* who) {
+  if (!is_float_dtype(dtype)) return fail(AEKV_ERR_DTYPE, "%s: dtype %d is not f32/f16/bf16", who, dtype);
+  if (B < 0 || T < 0 || H < 0 || D < 0 || S < 0 || K < 0) return fail(AEKV_ERR_SHAPE, "%s: negative size", who);
+  if (D > kMaxD) return fail(AEKV_ERR_UNSUPPORTED, "%s: head_dim %lld exceeds %d", who, (long long)D, kMaxD);
+  if (sink_numel != 1 && sink_numel != H)
+    return fail(AEKV_ERR_SHAPE, "sink must be a scalar or a [num_heads] tensor");
+  const int64_t rows = B * T * H;
+  if (rows == 0 || D == 0) return AEKV_OK;
+  if (ceil_div(rows, kThreads / 64) > 0x7fffffffLL) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many rows", who);
+  if (!q || !sink || !out || (K > 0 && (!kv || (idx_kind != 0 && !topk))))
+    return fail(AEKV_ERR_VALUE, "%s: null pointer", who);
+  const hipStream_t st = as_stream(stream);
+  const int scalar = sink_numel == 1 ? 1 : 0;
+  if (dtype == AEKV_F32) launch_sparse<AEKV_F32>(idx_kind, q, kv, topk, sink, scalar, B, T, H, D, S, K, scale, out, st);
+  else if (dtype == AEKV_F16) launch_sparse<AEKV_F16>(idx_kind, q, kv, topk, sink, scalar, B, T, H, D, S, K, scale, out, st);
+  else launch_sparse<AEKV_BF16>(idx_kind, q, kv, topk, sink, scalar, B, T, H, D, S, K, scale, out, st);
+  return check_launch(who);
+}
+
+struct QLayout {
+  int ts, n_comp_tiles, n_tiles;
+  size_t part_bytes;
+};
+
+QLayout qlayout(int64_t B, int64_t H, int64_t D, int64_t n_comp, int64_t W) {
+  QLayout l;
+  int ts = static_cast<int>(kTileFloats / (D > 0 ? D : 1));
+  if (ts > 256) ts = 256;
+  if (ts < 1) ts = 1;
+  l.ts = ts;
+  l.n_comp_tiles = static_cast<int>(ceil_div(n_comp, ts));
+  l.n_tiles = l.n_comp_tiles + static_cast<int>(ceil_div(W, ts));
+  l.part_bytes = align_up(static_cast<size_t>(B) * l.n_tiles * H * (D + 2) * 4, 256);
+  return l;
+}
+
+}  // namespace
+}  // namespace aekv
+
+using namespace aekv;
+
+extern "C" int aekv_sparse_sink_attention(const void* q, const void* kv, const void* topk, int32_t idx_dtype,
+                                          const void* sink, int64_t sink_numel, int32_t dtype, int64_t B, int64_t T,
+                                          int64_t H, int64_t D, int64_t S, int64_t K, float softmax_scale, void* out,
+                                          void* stream) {
+  if (idx_dtype != AEKV_I32 && idx_dtype != AEKV_I64) return fail(AEKV_ERR_DTYPE, "topk_indices must be int32 or int64");
+  return sparse_common(q, kv, topk, idx_dtype == AEKV_I32 ? 4 : 8, sink, sink_numel, dtype, B, T, H, D, S, K,
+                       softmax_scale, out, stream, "aekv_sparse_sink_attention");
+}
+
+extern "C" int aekv_tiled_prefill_attention(const void* q, const void* kv, const void* sink, int64_t sink_numel,
+                                            int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D, int64_t S,
+                                            float softmax_scale, int32_t tile_size, void* out, void* stream) {
+  if (tile_size <= 0) return fail(AEKV_ERR_VALUE, "tile_size must be positive");
+  return sparse_common(q, kv, nullptr, 0, sink, sink_numel, dtype, B, T, H, D, S, S, softmax_scale, out, stream,
+                       "aekv_tiled_prefill_attention");
+}
+
+extern "C" size_t aekv_quant_attention_workspace_size(int64_t B, int64_t H, int64_t D, int64_t n_comp, int64_t W) {
+  if (B <= 0 || H <= 0 || D <= 0) return 256;
+  return qlayout(B, H, D, n_comp, W).part_bytes;
+}
+
+extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const float* scale, const int64_t* sel,
+                                         const void* window, const float* sink, const float* diag, int64_t B, int64_t H,
+                                         int64_t D, int64_t S, int64_t K, int64_t W, int32_t bits, float softmax_scale,
+                                         void* ws, size_t ws_bytes, void* out, void* stream) {
+  const char* who = "aekv_quant_sink_attention";
+  if (bits != 4 && bits != 8) return fail(AEKV_ERR_VALUE, "bits must be 4 or 8, got %d", bits);
+  if (!is_pow2(D)) return fail(AEKV_ERR_VALUE, "WHT requires last dim to be a power of 2, got %lld", (long long)D);
+  if (D < 2 || D > 256) return fail(AEKV_ERR_UNSUPPORTED, "%s: head_dim %lld outside [2, 256]", who, (long long)D);
+  if (B < 0 || H <= 0 || S < 0 || K < 0 || W < 0) return fail(AEKV_ERR_SHAPE, "%s: bad sizes", who);
+  if (H * D > 4096) return fail(AEKV_ERR_UNSUPPORTED, "%s: H*D=%lld exceeds 4096", who, (long long)(H * D));
+  if (B > 65535) return fail(AEKV_ERR_UNSUPPORTED, "%s: B exceeds 65535", who);
+  const int64_t n_comp = sel ? K : S;
+  const QLayout l = qlayout(B, H, D, n_comp, W);
+  if (B == 0) return AEKV_OK;
+  if (!q || !sink || !diag || !out || (n_comp > 0 && (!codes || !scale)) || (W > 0 && !window))
+    return fail(AEKV_ERR_VALUE, "%s: null pointer", who);
+  if (l.n_tiles == 0) {
+    // no sources: every weight is zero -> out = 0 (serving.py:451-452)
+    const int64_t n16 = B * H * D;
+    hipLaunchKernelGGL(zero_u16_kernel, dim3(static_cast<uint32_t>(ceil_div(n16, kThreads))), dim3(kThreads), 0,
+                       as_stream(stream), static_cast<uint16_t*>(out), n16);
+    return check_launch(who);
+  }
+  if (!ws || ws_bytes < l.part_bytes)
+    return fail(AEKV_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who, l.part_bytes, ws_bytes);
+  if (l.n_tiles > 65535) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many source tiles", who);
+  QAttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.codes = static_cast<const uint8_t*>(codes);
+  a.scale = scale;
+  a.sel = sel;
+  a.win = static_cast<const uint16_t*>(window);
+  a.sink = sink;
+  a.diag = diag;
+  a.S = S;
+  a.K = K;
+  a.W = W;
+  a.H = static_cast<int>(H);
+  a.D = static_cast<int>(D);
+  a.bits = bits;
+  a.ts = l.ts;
+  a.n_comp_tiles = l.n_comp_tiles;
+  a.n_tiles = l.n_tiles;
+  a.sm_scale = softmax_scale;
+  a.wscale = wht_scale(static_cast<int>(D));
+  a.part = static_cast<float*>(ws);
+  a.out = static_cast<uint16_t*>(out);
+  const hipStream_t st = as_stream(stream);
+  allow_big_lds();
+  const size_t sm1 = sizeof(float) * (2 * H * D + static_cast<size_t>(l.ts) * (D + 1) + l.ts + H * l.ts + 2 * H);
+  if (sm1 > 160 * 1024) return fail(AEKV_ERR_UNSUPPORTED, "%s: source tile does not fit in LDS", who);
+  hipLaunchKernelGGL(quant_attn_partial_kernel, dim3(static_cast<uint32_t>(l.n_tiles), static_cast<uint32_t>(B)),
+                     dim3(kThreads), sm1, st, a);
+  if (int rc = check_launch(who)) return rc;
+  const size_t sm2 = sizeof(float) * (3 * H * D + static_cast<size_t>(l.n_tiles) * H + H);
+  if (sm2 > 160 * 1024) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many tiles for the combine", who);
+  hipLaunchKernelGGL(quant_attn_combine_kernel, dim3(static_cast<uint32_t>(B)), dim3(kThreads), sm2, st, a);
+  return check_launch(who);
+}
+
+extern "C" int aekv_hca_compress(const void* c, const void* z, int32_t dtype, int64_t B, int64_t M, int64_t D, void* out,
+                                 void* stream) {
+  const char* who = "aekv_hca_compress";
+  if (!is_float_dtype(dtype)) return fail(AEKV_ERR_DTYPE, "%s: dtype %d is not f32/f16/bf16", who, dtype);
+  if (B < 0 || M < 0 || D < 0) return fail(AEKV_ERR_SHAPE, "%s: negative size", who);
+  if (B * D == 0) return AEKV_OK;
+  if (M == 0) return fail(AEKV_ERR_SHAPE, "%s: empty compression window", who);
+  if (!c || !z || !out) return fail(AEKV_ERR_VALUE, "%s: null pointer", who);
+  const dim3 grid(static_cast<uint32_t>(ceil_div(B * D, kThreads)));
+  const hipStream_t st = as_stream(stream);
+  if (dtype == AEKV_F32) hipLaunchKernelGGL(hca_compress_kernel<AEKV_F32>, grid, dim3(kThreads), 0, st, c, z, B, M, D, out);
+  else if (dtype == AEKV_F16) hipLaunchKernelGGL(hca_compress_kernel<AEKV_F16>, grid, dim3(kThreads), 0, st, c, z, B, M, D, out);
+  else hipLaunchKernelGGL(hca_compress_kernel<AEKV_BF16>, grid, dim3(kThreads), 0, st, c, z, B, M, D, out);
+  return check_launch(who);
+}

@@ -1,0 +1,164 @@
+/*
+ * aetherkv.h — C ABI of libaetherkv.so, the MI355X (gfx950) compressed-KV hot path.
+ *
+ * Every entry point:
+ *   - is extern "C", takes plain device pointers, int64 sizes and a hipStream_t passed as void*;
+ *   - validates every argument on the host BEFORE any launch (so argument errors are testable
+ *     without a GPU) and returns an aekv_status; the message of the last failure on the calling
+ *     thread is returned by aekv_last_error();
+ *   - never allocates device memory: scratch space is passed in (`ws`, `ws_bytes`) and its size
+ *     is returned by the matching *_workspace_size() query;
+ *   - enqueues its kernels on `stream` and returns without synchronising.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository root):
+ *   aekv_wht                         aether_2b/turbo_quant.py:49-76             _wht(x)
+ *   aekv_tq_diag                     aether_2b/turbo_quant.py:111-121           PolarQuant._diag(d, device)
+ *   aekv_tq_encode                   aether_2b/turbo_quant.py:127-166           PolarQuant.encode(x)
+ *   aekv_tq_decode                   aether_2b/turbo_quant.py:168-211           PolarQuant.decode(data, scale, out_dtype)
+ *   aekv_csa_indexer_topk            aether_kernels/sparse_attention.py:45-67   csa_indexer_topk(...)
+ *                                    (binding aether_kernels/csrc/bindings.cpp:88-101)
+ *   aekv_csa_indexer_topk_quant      aether_2b/serving.py:606-621 (indexer over the quantised index cache)
+ *   aekv_sparse_sink_attention       aether_kernels/sparse_attention.py:8-16    sparse_sink_attention(...)
+ *                                    (binding aether_kernels/csrc/bindings.cpp:21-46)
+ *   aekv_quant_sink_attention        aether_2b/serving.py:507-525 (HCA) and :597-625 (CSA): dequantise,
+ *                                    gather, concat window, aether_pipeline/serving.py:99-130 attention
+ *   aekv_hca_compress                aether_kernels/sparse_attention.py:70-83   hca_compress(...)
+ *   aekv_tiled_prefill_attention     aether_kernels/sparse_attention.py:19-42   tiled_prefill_attention(...)
+ */
+#ifndef AETHERKV_H_
+#define AETHERKV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------------------- */
+typedef enum {
+  AEKV_OK = 0,
+  AEKV_ERR_VALUE = 1,       /* bad value (bits, non-power-of-two dim, k, ...)  -> ValueError   */
+  AEKV_ERR_SHAPE = 2,       /* inconsistent shapes / ranks                     -> RuntimeError */
+  AEKV_ERR_DTYPE = 3,       /* unsupported dtype                               -> RuntimeError */
+  AEKV_ERR_ALIGN = 4,       /* pointer not aligned as documented               -> RuntimeError */
+  AEKV_ERR_WORKSPACE = 5,   /* ws NULL or ws_bytes smaller than the query      -> RuntimeError */
+  AEKV_ERR_HIP = 6,         /* a HIP launch/runtime call failed                -> RuntimeError */
+  AEKV_ERR_UNSUPPORTED = 7  /* size outside what the kernels support           -> RuntimeError */
+} aekv_status;
+
+/* ---- element types ----------------------------------------------------------------------- */
+typedef enum {
+  AEKV_F32 = 0,
+  AEKV_F16 = 1,
+  AEKV_BF16 = 2,
+  AEKV_I32 = 3,
+  AEKV_I64 = 4
+} aekv_dtype;
+
+/* Indexer score rules.  The reference has three (file:line of each):
+ *   AEKV_IDX_SOFTPLUS : sum_h softplus(w_h) * relu(q_h . k_j)   aether_2b/modeling.py:609-611, :521-523
+ *   AEKV_IDX_RAW      : sum_h w_h * relu(q_h . k_j)             aether_2b/serving.py:618-619
+ *   AEKV_IDX_RELU_W   : sum_h max(w_h, 0) * (q_h . k_j)         aether_kernels/csrc/csa_indexer_cuda.cu:222-231 */
+typedef enum {
+  AEKV_IDX_SOFTPLUS = 0,
+  AEKV_IDX_RAW = 1,
+  AEKV_IDX_RELU_W = 2
+} aekv_index_mode;
+
+/* ---- library ----------------------------------------------------------------------------- */
+const char* aekv_version(void);
+/* Message of the last non-OK status returned on the calling thread ("" if none). */
+const char* aekv_last_error(void);
+/* Largest supported values (compile-time limits of the kernels). */
+int32_t aekv_max_head_dim(void);   /* power-of-two vector length limit for the codec (512)   */
+int32_t aekv_max_topk(void);       /* largest k accepted by the indexer select (2048)         */
+
+/* ---- TurboQuant codec -------------------------------------------------------------------- */
+/* Rademacher diagonal of PolarQuant(seed)._diag(d): MT19937 seeded with seed*10007+d, one
+ * 32-bit draw per element, r = (draw & 0xFFFFFF) * 2^-24, diag = r > 0.5 ? +1 : -1.
+ * Host memory out[d].  (turbo_quant.py:111-121; torch.rand's CPU generator is MT19937.) */
+int aekv_tq_diag(int64_t seed, int32_t d, float* out_host);
+
+/* Normalised Walsh-Hadamard transform of n_vec rows of length d (power of two, 1..512):
+ * x (x_dtype f32/f16/bf16) -> out fp32, butterfly stages h = 1,2,..,d/2 in order, then * fp32(d^-0.5).
+ * x must be aligned to min(d,8)*sizeof(x_dtype) bytes, out to min(d,8)*4. */
+int aekv_wht(const void* x, int32_t x_dtype, int64_t n_vec, int32_t d, float* out, void* stream);
+
+/* Encode: rot = WHT(x * diag); m = max(max|rot|, 1e-8); scale = m / Q; codes = clamp(rne(rot/m*Q))
+ * with Q = 127 (bits 8: int8 codes [n_vec, d]) or Q = 7 (bits 4: uint8 [n_vec, d/2], element 2i in
+ * the low nibble, 2i+1 in the high nibble, two's complement).  scale fp32 [n_vec].
+ * diag: device fp32 [d] of +-1.  Bit-exact with turbo_quant.py:127-166. */
+int aekv_tq_encode(const void* x, int32_t x_dtype, int64_t n_vec, int32_t d, int32_t bits,
+                   const float* diag, void* codes, float* scale, void* stream);
+
+/* Decode: rot = codes * scale; out = WHT(rot) * diag, rounded to out_dtype (f32/f16/bf16, RNE).
+ * Bit-exact with turbo_quant.py:168-211. */
+int aekv_tq_decode(const void* codes, const float* scale, int64_t n_vec, int32_t d, int32_t bits,
+                   const float* diag, void* out, int32_t out_dtype, void* stream);
+
+/* ---- CSA indexer + top-k ----------------------------------------------------------------- */
+/* Scores score[b,j] = sum_h act(w[b,h]) * rho(q[b,h,:] . k[b,j,:]) (act/rho from `mode`) for
+ * j < valid[b] (valid == NULL: all S), and returns the k best per row under the total order
+ * (score descending, index ascending), sorted in that order, as int64 out_idx[B, k].  Rows with
+ * valid[b] < k are padded with -1.  out_score[B, k] (fp32, nullable) receives the scores.
+ *
+ * aekv_csa_indexer_topk: fp32 keys index_kv[B, S, IC] (drop-in for csa_indexer_topk).
+ * aekv_csa_indexer_topk_quant: keys are TurboQuant codes key_codes[B, S, IC or IC/2] with
+ *   key_scale[B, S]; k_j = decode(codes_j, scale_j) in fp32.  The scan runs in the rotated domain:
+ *   q.k_j = scale_j * (WHT(diag*q) . codes_j). */
+size_t aekv_csa_indexer_workspace_size(int64_t B, int64_t S, int32_t k);
+int aekv_csa_indexer_topk(const float* index_q, const float* index_kv, const float* index_weight,
+                          const int32_t* valid, int64_t B, int64_t S, int32_t IH, int32_t IC,
+                          int32_t k, int32_t mode, void* ws, size_t ws_bytes,
+                          int64_t* out_idx, float* out_score, void* stream);
+int aekv_csa_indexer_topk_quant(const float* index_q, const float* index_weight,
+                                const void* key_codes, const float* key_scale, const float* diag,
+                                const int32_t* valid, int64_t B, int64_t S, int32_t IH, int32_t IC,
+                                int32_t bits, int32_t k, int32_t mode, void* ws, size_t ws_bytes,
+                                int64_t* out_idx, float* out_score, void* stream);
+
+/* ---- attention ----------------------------------------------------------------------------- */
+/* Drop-in sparse sink attention (sparse_sink_attention_cuda.cu semantics, oracle
+ * aether_pipeline/serving.py:99-130):
+ *   q [B,T,H,D], kv [B,S,2,D] (K = kv[:,:,0], V = kv[:,:,1]), topk [B,T,K] (idx_dtype I32/I64),
+ *   sink: sink_numel == 1 (scalar) or H, same dtype as q.  Index outside [0,S) is skipped.
+ *   out[b,t,h] = sum_j e^{l_j-M} V[idx_j] / (sum_j e^{l_j-M} + e^{sink_h-M}),
+ *   l_j = scale * q.K[idx_j], M = max(max_j l_j, sink_h).  dtype F32/F16/BF16, D <= 512. */
+int aekv_sparse_sink_attention(const void* q, const void* kv, const void* topk, int32_t idx_dtype,
+                               const void* sink, int64_t sink_numel, int32_t dtype,
+                               int64_t B, int64_t T, int64_t H, int64_t D, int64_t S, int64_t K,
+                               float softmax_scale, void* out, void* stream);
+
+/* Sink attention of one bf16 query token per row over TurboQuant-compressed shared K=V blocks plus
+ * a bf16 sliding window (the serving engine's decode step, dequantise + gather + concat + attend
+ * fused):
+ *   q [B,H,D] bf16; codes [B,S,D or D/2] + scale [B,S]; sel [B,K] int64 block indices
+ *   (sel == NULL: all S blocks in order, i.e. HCA; entries outside [0,S) are skipped);
+ *   window [B,W,D] bf16 (W may be 0); sink fp32 [H]; out [B,H,D] bf16.
+ *   Sources = [dequant(blocks[sel]), window]; K = V = source (aether_2b/serving.py:52-53).
+ * The compressed sources stay in the rotated domain: logits use WHT(diag*q), the value sum is
+ * rotated back once per (row, head). */
+size_t aekv_quant_attention_workspace_size(int64_t B, int64_t H, int64_t D, int64_t n_comp,
+                                           int64_t W);
+int aekv_quant_sink_attention(const void* q, const void* codes, const float* scale,
+                              const int64_t* sel, const void* window, const float* sink,
+                              const float* diag, int64_t B, int64_t H, int64_t D, int64_t S,
+                              int64_t K, int64_t W, int32_t bits, float softmax_scale,
+                              void* ws, size_t ws_bytes, void* out, void* stream);
+
+/* hca_compress drop-in: out[b,d] = sum_m softmax_m(z[b,:,d]) * c[b,m,d], c/z [B,M,D], dtype
+ * F32/F16/BF16, out [B,D] same dtype (hca_compress_cuda.cu:18-68; serving.py:495-497). */
+int aekv_hca_compress(const void* c, const void* z, int32_t dtype, int64_t B, int64_t M, int64_t D,
+                      void* out, void* stream);
+
+/* tiled_prefill_attention drop-in: sink attention of every target over all S sources,
+ * oracle aether_2b/modeling.py:158-178 (sink counted once in the normaliser). */
+int aekv_tiled_prefill_attention(const void* q, const void* kv, const void* sink, int64_t sink_numel,
+                                 int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D, int64_t S,
+                                 float softmax_scale, int32_t tile_size, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AETHERKV_H_ */

@@ -1,0 +1,187 @@
+"""C ABI and host-side logic of libaetherkv — CPU only, no kernel launches.
+
+Every entry point validates its arguments on the host before launching anything, so each error
+path is exercised here with fake (never dereferenced) pointers.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import aetherkv
+import aetherkv._lib as L
+from conftest import ROOT
+
+FAKE = ctypes.c_void_p(0x10000)        # never dereferenced: validation fails or n == 0 first
+FAKE_ODD = ctypes.c_void_p(0x10001)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not L.available():
+        pytest.fail("libaetherkv.so is not built (run __graft_entry__.build())")
+    return L.lib()
+
+
+def header_functions():
+    text = (ROOT / "include" / "aetherkv.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|int32_t|const char\*)\s+(aekv_\w+)\(", text, flags=re.M)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = header_functions()
+    assert len(names) >= 16
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(L.SYMBOLS)
+
+
+def test_version_and_limits(lib):
+    assert b"gfx950" in lib.aekv_version()
+    assert lib.aekv_max_head_dim() == 512
+    assert lib.aekv_max_topk() == 2048
+
+
+@pytest.mark.parametrize("seed,d", [(42, 128), (42, 64), (7, 16), (0, 512)])
+def test_host_diag_matches_torch_generator(lib, seed, d):
+    out = np.empty(d, np.float32)
+    assert lib.aekv_tq_diag(seed, d, out.ctypes.data_as(ctypes.c_void_p)) == L.OK
+    g = torch.Generator()
+    g.manual_seed(seed * 10007 + d)
+    r = torch.rand(d, generator=g)
+    np.testing.assert_array_equal(out, torch.where(r > 0.5, 1.0, -1.0).numpy())
+
+
+def _err(lib):
+    return lib.aekv_last_error().decode()
+
+
+def test_encode_argument_errors(lib):
+    rc = lib.aekv_tq_encode(FAKE, L.BF16, 4, 128, 3, FAKE, FAKE, FAKE, None)
+    assert rc == L.ERR_VALUE and "bits must be 4 or 8" in _err(lib)
+    rc = lib.aekv_tq_encode(FAKE, L.BF16, 4, 96, 8, FAKE, FAKE, FAKE, None)
+    assert rc == L.ERR_VALUE and "power of 2" in _err(lib)
+    rc = lib.aekv_tq_encode(FAKE, L.BF16, 4, 1024, 8, FAKE, FAKE, FAKE, None)
+    assert rc == L.ERR_UNSUPPORTED
+    rc = lib.aekv_tq_encode(FAKE, L.I32, 4, 128, 8, FAKE, FAKE, FAKE, None)
+    assert rc == L.ERR_DTYPE
+    rc = lib.aekv_tq_encode(FAKE_ODD, L.BF16, 4, 128, 8, FAKE, FAKE, FAKE, None)
+    assert rc == L.ERR_ALIGN
+    rc = lib.aekv_tq_encode(None, L.BF16, 4, 128, 8, FAKE, FAKE, FAKE, None)
+    assert rc == L.ERR_VALUE
+    rc = lib.aekv_tq_encode(FAKE, L.BF16, 1, 1, 4, FAKE, FAKE, FAKE, None)
+    assert rc == L.ERR_VALUE and "even" in _err(lib)
+    # empty input succeeds without launching anything
+    assert lib.aekv_tq_encode(None, L.BF16, 0, 128, 4, None, None, None, None) == L.OK
+
+
+def test_decode_and_wht_argument_errors(lib):
+    assert lib.aekv_tq_decode(FAKE, FAKE, 4, 128, 5, FAKE, FAKE, L.BF16, None) == L.ERR_VALUE
+    assert lib.aekv_tq_decode(FAKE, FAKE, 4, 128, 4, FAKE, FAKE, L.I64, None) == L.ERR_DTYPE
+    assert lib.aekv_tq_decode(FAKE, FAKE, 4, 128, 4, FAKE, FAKE_ODD, L.BF16, None) == L.ERR_ALIGN
+    assert lib.aekv_tq_decode(None, None, 0, 128, 4, None, None, L.BF16, None) == L.OK
+    assert lib.aekv_wht(FAKE, L.F32, 4, 12, FAKE, None) == L.ERR_VALUE
+    assert lib.aekv_wht(None, L.F32, 0, 16, None, None) == L.OK
+
+
+def test_indexer_argument_errors(lib):
+    ws_need = lib.aekv_csa_indexer_workspace_size(8, 16384, 256)
+    assert ws_need >= 8 * 4 * 256 * 8
+    rc = lib.aekv_csa_indexer_topk(FAKE, FAKE, FAKE, None, 8, 16384, 4, 64, 0, 0, FAKE, ws_need, FAKE, None, None)
+    assert rc == L.ERR_VALUE and "k must be positive" in _err(lib)
+    rc = lib.aekv_csa_indexer_topk(FAKE, FAKE, FAKE, None, 8, 16384, 4, 64, 4096, 0, FAKE, ws_need, FAKE, None, None)
+    assert rc == L.ERR_UNSUPPORTED
+    rc = lib.aekv_csa_indexer_topk(FAKE, FAKE, FAKE, None, 8, 16384, 4, 64, 256, 0, FAKE, ws_need - 1, FAKE, None, None)
+    assert rc == L.ERR_WORKSPACE
+    rc = lib.aekv_csa_indexer_topk(FAKE, FAKE, FAKE, None, 8, 16384, 4, 64, 256, 9, FAKE, ws_need, FAKE, None, None)
+    assert rc == L.ERR_VALUE
+    rc = lib.aekv_csa_indexer_topk_quant(FAKE, FAKE, FAKE, FAKE, FAKE, None, 8, 16384, 4, 64, 6, 256, 0, FAKE, ws_need,
+                                         FAKE, None, None)
+    assert rc == L.ERR_VALUE and "bits must be 4 or 8" in _err(lib)
+    rc = lib.aekv_csa_indexer_topk_quant(FAKE, FAKE, FAKE, FAKE, FAKE, None, 8, 16384, 4, 48, 8, 256, 0, FAKE, ws_need,
+                                         FAKE, None, None)
+    assert rc == L.ERR_VALUE and "power of 2" in _err(lib)
+    assert lib.aekv_csa_indexer_topk(None, None, None, None, 0, 10, 4, 64, 4, 0, None, 0, None, None, None) == L.OK
+
+
+def test_attention_argument_errors(lib):
+    rc = lib.aekv_sparse_sink_attention(FAKE, FAKE, FAKE, L.F32, FAKE, 1, L.BF16, 1, 1, 4, 128, 8, 4, 0.1, FAKE, None)
+    assert rc == L.ERR_DTYPE and "int32 or int64" in _err(lib)
+    rc = lib.aekv_sparse_sink_attention(FAKE, FAKE, FAKE, L.I64, FAKE, 3, L.BF16, 1, 1, 4, 128, 8, 4, 0.1, FAKE, None)
+    assert rc == L.ERR_SHAPE and "sink" in _err(lib)
+    rc = lib.aekv_sparse_sink_attention(FAKE, FAKE, FAKE, L.I64, FAKE, 1, L.BF16, 1, 1, 4, 1024, 8, 4, 0.1, FAKE, None)
+    assert rc == L.ERR_UNSUPPORTED
+    assert lib.aekv_sparse_sink_attention(None, None, None, L.I64, None, 1, L.BF16, 0, 1, 4, 128, 8, 4, 0.1, None,
+                                          None) == L.OK
+    assert lib.aekv_tiled_prefill_attention(FAKE, FAKE, FAKE, 1, L.BF16, 1, 1, 4, 128, 8, 0.1, 0, FAKE, None) == L.ERR_VALUE
+    need = lib.aekv_quant_attention_workspace_size(64, 12, 128, 256, 128)
+    assert need >= 64 * 6 * 12 * 130 * 4
+    rc = lib.aekv_quant_sink_attention(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 64, 12, 128, 65536, 256, 128, 4, 0.1,
+                                       FAKE, need - 1, FAKE, None)
+    assert rc == L.ERR_WORKSPACE
+    rc = lib.aekv_quant_sink_attention(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 64, 12, 96, 65536, 256, 128, 4, 0.1,
+                                       FAKE, need, FAKE, None)
+    assert rc == L.ERR_VALUE
+    rc = lib.aekv_hca_compress(FAKE, FAKE, L.BF16, 2, 0, 16, FAKE, None)
+    assert rc == L.ERR_SHAPE
+
+
+# ---- python surface (host validation, no device) ---------------------------------------------
+def test_polarquant_rejects_bad_bits():
+    with pytest.raises(ValueError, match="bits must be 4 or 8"):
+        aetherkv.PolarQuant(bits=3)
+
+
+def test_wht_rejects_non_power_of_two_before_device():
+    with pytest.raises(ValueError, match="power of 2"):
+        aetherkv._wht(torch.randn(3, 12))
+
+
+def test_no_cpu_fallback():
+    pq = aetherkv.PolarQuant(bits=8)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        pq.encode(torch.randn(2, 128, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="HIP device"):
+        aetherkv._wht(torch.randn(2, 16))
+
+
+def test_polarquant_diag_cached_and_matches_torch():
+    pq = aetherkv.PolarQuant(bits=4)
+    d1 = pq._diag(128, torch.device("cpu"))
+    assert pq._diag(128, torch.device("cpu")) is d1
+    g = torch.Generator()
+    g.manual_seed(42 * 10007 + 128)
+    assert torch.equal(d1, torch.where(torch.rand(128, generator=g) > 0.5, 1.0, -1.0))
+
+
+def test_sparse_wrappers_reject_cpu_tensors_like_reference():
+    q = torch.randn(1, 1, 2, 8)
+    kv = torch.randn(1, 4, 2, 8)
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        aetherkv.sparse_sink_attention(q, kv, torch.zeros(1, 1, 2, dtype=torch.long), torch.zeros(2), 0.5)
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        aetherkv.csa_indexer_topk(torch.randn(1, 2, 8), torch.randn(1, 5, 8), torch.randn(1, 2), 2)
+
+
+def test_loader_environment_keys_and_consistency():
+    # reference tests/test_cuda_loader.py:12-33
+    env = aetherkv.cuda_build_environment()
+    assert set(env) == {"torch_cuda_built", "torch_cuda_available", "cuda_home", "nvcc", "conda_target_include",
+                        "conda_target_lib", "cuda_runtime_lib"}
+    from aetherkv.backends import CudaSparseAttentionBackend
+
+    backend = CudaSparseAttentionBackend()
+    reason = aetherkv.cuda_extension_unavailable_reason(require_device=True)
+    assert backend.available() is (reason is None)
+    assert backend.availability_error() == reason
+    assert backend.name() == "hip_extension"
+
+
+def test_loader_returns_kernel_namespace():
+    ext = aetherkv.load_aether_cuda_kernels()
+    for n in ("sparse_sink_attention", "tiled_prefill_attention", "csa_indexer_topk", "hca_compress"):
+        assert callable(getattr(ext, n))

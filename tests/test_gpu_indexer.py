@@ -1,0 +1,113 @@
+"""GPU parity of the CSA indexer + top-k (fp32 drop-in and quantised keys) against the oracle.
+
+Bar: the selected set equals the oracle's exact-math top-k, except for indices whose oracle score
+is within the fp32 rounding bound of the k-th score (see topk_check.py); output sorted by score,
+padded with -1 beyond the visible count; exact ties resolve to the lower index.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from aetherkv import PolarQuant, csa_indexer_topk
+from aetherkv.decode import csa_indexer_topk_quant
+from aetherkv.synthetic import normal, normal_with_outliers
+from topk_check import assert_topk_matches, score_error_bound
+
+pytestmark = pytest.mark.gpu
+
+
+def w_act(w: np.ndarray, mode: str) -> np.ndarray:
+    w = w.astype(np.float64)
+    if mode == "softplus":
+        return np.where(w > 20, w, np.log1p(np.exp(np.minimum(w, 20))))
+    return np.maximum(w, 0) if mode == "relu_w" else w
+
+
+@pytest.mark.parametrize("mode", ["softplus", "raw", "relu_w"])
+@pytest.mark.parametrize("S,k", [(1, 1), (7, 7), (300, 16), (5000, 256), (9000, 2048), (4096, 256)])
+def test_fp32_indexer_matches_oracle(dev, mode, S, k):
+    B, IH, IC = 3, 4, 64
+    g = torch.Generator().manual_seed(S * 3 + k)
+    q = torch.randn(B, IH, IC, generator=g)
+    kv = torch.randn(B, S, IC, generator=g)
+    w = torch.randn(B, IH, generator=g) * 2
+    idx = csa_indexer_topk(q.to(dev), kv.to(dev), w.to(dev), k, mode=mode).cpu().numpy()
+    assert idx.shape == (B, k) and idx.dtype == np.int64
+    scores = O.index_scores(q.numpy(), w.numpy(), kv.numpy(), mode=mode)
+    tol = score_error_bound(q.numpy(), w_act(w.numpy(), mode), kv.numpy())
+    assert_topk_matches(idx, scores, k, tol)
+
+
+def test_fp32_indexer_reference_contract(dev):
+    # k must be in [1, S] (csa_indexer_cuda.cu:272); output int64 [B, k]
+    q = torch.randn(1, 2, 8, device=dev)
+    kv = torch.randn(1, 5, 8, device=dev)
+    w = torch.randn(1, 2, device=dev)
+    with pytest.raises(RuntimeError, match=r"k must be in \[1, S\]"):
+        csa_indexer_topk(q, kv, w, 6)
+    assert csa_indexer_topk(q, kv, w, 5).shape == (1, 5)
+
+
+def test_exact_ties_pick_lowest_indices(dev):
+    B, S, IH, IC = 2, 9000, 2, 16
+    q = torch.randn(B, IH, IC)
+    kv = torch.randn(1, 1, IC).expand(B, S, IC).contiguous()   # every key identical -> all scores tie
+    w = torch.ones(B, IH)
+    idx = csa_indexer_topk(q.to(dev), kv.to(dev), w.to(dev), 300).cpu().numpy()
+    np.testing.assert_array_equal(idx, np.tile(np.arange(300), (B, 1)))
+
+
+def _quant_case(dev, B, S, IH, IC, bits, seed, outliers=False, mode="softplus", k=256, valid=None):
+    pq = PolarQuant(bits)
+    keys = (normal_with_outliers((B, S, IC), seed, dtype=torch.bfloat16, trailing_dims=1) if outliers
+            else normal((B, S, IC), seed, dtype=torch.bfloat16)).to(dev)
+    codes, scale = pq.encode(keys)
+    q = normal((B, IH, IC), seed + 100, dtype=torch.float32).to(dev)
+    w = normal((B, IH), seed + 200, dtype=torch.float32).to(dev)
+    vt = None if valid is None else torch.tensor(valid, dtype=torch.int32, device=dev)
+    idx, sc = csa_indexer_topk_quant(q, w, codes, scale, k, quant=pq, valid=vt, mode=mode, return_scores=True)
+    # oracle: keys dequantised in fp32 (turbo_quant.py decode), exact-math scores
+    dg = O.diag(42, IC)
+    keys_f32 = O.decode(codes.cpu().numpy(), scale.cpu().numpy(), bits, dg, "f32")
+    qn, wn = q.cpu().numpy(), w.cpu().numpy()
+    scores = O.index_scores(qn, wn, keys_f32, valid=None if valid is None else np.array(valid, np.int32), mode=mode)
+    tol = score_error_bound(qn, w_act(wn, mode), keys_f32, extra_rel=16 * math.log2(IC) * 2.0 ** -24)
+    subs = assert_topk_matches(idx.cpu().numpy(), scores, k, tol, None if valid is None else np.array(valid))
+    # returned scores agree with the oracle's within the bound
+    ii = idx.cpu().numpy()
+    ok = ii >= 0
+    bi = np.nonzero(ok)
+    ref = scores[bi[0], ii[ok]]
+    assert np.all(np.abs(sc.cpu().numpy()[ok] - ref) <= 2 * tol[bi[0], ii[ok]] + 1e-30)
+    return subs
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("mode", ["softplus", "raw", "relu_w"])
+def test_quant_indexer_matches_oracle(dev, bits, mode):
+    _quant_case(dev, 3, 6000, 4, 64, bits, 10 + bits, mode=mode)
+
+
+def test_quant_indexer_ragged_valid_and_padding(dev):
+    _quant_case(dev, 4, 5000, 4, 64, 4, 21, valid=[5000, 2500, 0, 3], k=16)
+
+
+def test_quant_indexer_small_dims(dev):
+    # tiny-model shapes of the reference tests (indexer_head_dim=8, 2 heads)
+    _quant_case(dev, 2, 37, 2, 8, 8, 31, k=4)
+    _quant_case(dev, 2, 37, 2, 8, 4, 32, k=37)
+
+
+def test_config3_indexer_8bit(dev):
+    # BASELINE cfg3: B=8, 16384 blocks, 4 index heads x 64, 8-bit keys, softplus weights, top-256
+    _quant_case(dev, 8, 16384, 4, 64, 8, 2)
+
+
+def test_config5_indexer_4bit_rows(dev):
+    # BASELINE cfg5 at full S (65536 blocks, 4-bit, outliers) on 2 of the 64 rows
+    _quant_case(dev, 2, 65536, 4, 64, 4, 4, outliers=True)
