@@ -7,9 +7,9 @@ What the reference decode step does (aether_2b/serving.py):
                  gather, concat the bf16 window, attend with the sink (_run_backend :450-467).
   HCA  :507-522  dequantise every visible block, concat the window, attend with full indices.
 Here each step is two fused HIP stages: the indexer scans the index codes in the rotated domain and
-selects the top-k exactly; the attention kernel gathers the selected code rows, dequantises them in
-registers, attends them together with the window and the per-head sink, and rotates the value sum
-back once per head.
+selects the top-k exactly; the attention kernel gathers the selected code rows, dequantises them on
+load to the same bf16 values PolarQuant.decode produces, and attends them together with the window
+and the per-head sink (split over source tiles, merged with the sink counted once).
 
 Score rule: ``mode="softplus"`` (aether_2b/modeling.py:609-611, default), ``"raw"`` (the serving
 engine's sum_h w_h relu(q_h.k), serving.py:618-619) or ``"relu_w"`` (csa_indexer_cuda.cu:222-231).
@@ -112,7 +112,7 @@ def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tens
     cc = codes.contiguous()
     sc = _scale_2d(scale, B, S)
     s64 = None if sel is None else sel.to(torch.int64).contiguous()
-    K = 0 if s64 is None else s64.size(1)
+    K = -1 if s64 is None else s64.size(1)  # n_sel < 0: every block (HCA)
     if window is not None and window.numel() > 0:
         if window.dtype != torch.bfloat16 or window.dim() != 3 or window.size(0) != B or window.size(2) != D:
             raise RuntimeError(f"window must be bf16 [B, W, D], got {window.dtype} {tuple(window.shape)}")
@@ -126,7 +126,7 @@ def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tens
     if sk.numel() != H:
         raise RuntimeError("sink must be a scalar or a [num_heads] tensor")
     diag = quant._diag(D, q.device)
-    n_comp = K if s64 is not None else S
+    n_comp = K if K >= 0 else S
     if workspace is None:
         workspace = attention_workspace(B, H, D, n_comp, W, q.device)
     if out is None:

@@ -9,12 +9,15 @@
 // 2. quant_attn_partial_kernel + quant_attn_combine_kernel — one decode token per row over
 //    TurboQuant-compressed shared K=V blocks (selected by the CSA indexer, or all blocks for HCA)
 //    plus a bf16 sliding window (aether_2b/serving.py:507-522, :597-625).  Split-KV: each workgroup
-//    attends one tile of sources for all heads of a row and writes (max, sum, acc); the combine
-//    merges tiles with the sink and rotates the compressed part back once per head:
-//      sum_j p_j K_j = diag * WHT(sum_j p_j scale_j codes_j)   (K_j = diag * WHT(scale_j codes_j)).
+//    gathers one tile of sources, dequantises the code rows on load to the same bf16 values
+//    PolarQuant.decode produces, attends them for all heads of the row and writes (max, sum, acc);
+//    the combine merges the tiles with the sink counted once.
 // 3. hca_compress_kernel — softmax over the M window positions and weighted sum
 //    (aether_kernels/sparse_attention.py:70-83; aether_2b/serving.py:495-497).
-#include "aekv_common.h"
+#include <mutex>
+#include <unordered_set>
+
+#include "tq_device.h"
 
 namespace aekv {
 namespace {
@@ -132,52 +135,33 @@ struct QAttnArgs {
   const float* sink;      // [H]
   const float* diag;      // [D]
   int64_t S, K, W;
-  int H, D, bits, ts;     // ts: sources per tile
+  int H, ts;              // ts: sources per tile
   int n_comp_tiles, n_tiles;
   float sm_scale, wscale;
   float* part;            // [B, n_tiles, H, D + 2]
   uint16_t* out;          // [B, H, D] bf16
 };
 
-// q (or WHT(diag*q) when `rotate`) for all heads of row b into qs[H*D] (uses qtmp as scratch).
-__device__ void load_query(const QAttnArgs& a, int64_t b, bool rotate, float* qs, float* qtmp) {
-  const int HD = a.H * a.D;
-  for (int i = threadIdx.x; i < HD; i += kThreads) {
-    float v = bf16_to_f32(a.q[b * HD + i]);
-    if (rotate) v = v * a.diag[i % a.D];
-    qs[i] = v;
-  }
-  __syncthreads();
-  if (!rotate) return;
-  float* src = qs;
-  float* dst = qtmp;
-  const int pairs = HD / 2, half = a.D / 2;
-  for (int hh = 1; hh < a.D; hh <<= 1) {
-    for (int p = threadIdx.x; p < pairs; p += kThreads) {
-      const int head = p / half, r = p % half;
-      const int i = head * a.D + (r / hh) * 2 * hh + (r % hh);
-      const float x = src[i], y = src[i + hh];
-      dst[i] = x + y;
-      dst[i + hh] = x - y;
-    }
-    __syncthreads();
-    float* t = src;
-    src = dst;
-    dst = t;
-  }
-  for (int i = threadIdx.x; i < HD; i += kThreads) qs[i] = src[i] * a.wscale;
-  __syncthreads();
+__device__ __forceinline__ float round_bf16(float v) {
+  return bf16_to_f32(pack_bf16x2(v, 0.0f) & 0xffffu);
 }
 
+// One workgroup = one tile of `ts` sources of one row, all heads.  Compressed sources are gathered
+// by index and dequantised on load exactly as PolarQuant.decode(..., bf16) (the engine attends the
+// bf16 dequantised cache, serving.py:346-376), window sources are the bf16 rows as stored.
+template <int BITS, int D>
 __global__ __launch_bounds__(kThreads) void quant_attn_partial_kernel(QAttnArgs a) {
+  constexpr int EPL = D < 8 ? D : 8;
+  constexpr int LPV = D / EPL;
+  constexpr int VPW = 64 / LPV;
+  constexpr int DP = D + 1;  // padded LDS row: conflict-free column walks
   extern __shared__ float smem[];
-  const int H = a.H, D = a.D, DP = D + 1, ts = a.ts;
-  float* qs = smem;                       // H*D
-  float* qtmp = qs + H * D;               // H*D
-  float* X = qtmp + H * D;                // ts * (D+1)
-  float* sig = X + ts * DP;               // ts   (scale_j, 1 for window; 0 = invalid)
-  float* P = sig + ts;                    // H * ts
-  float* stat = P + H * ts;               // 2*H  (max, sum)
+  const int H = a.H, ts = a.ts;
+  float* qs = smem;         // H*D
+  float* X = qs + H * D;    // ts*DP
+  float* okf = X + ts * DP; // ts (1 = source present, 0 = skipped index)
+  float* P = okf + ts;      // H*ts
+  float* stat = P + H * ts; // 2H (tile max, tile sum)
 
   const int64_t b = blockIdx.y;
   const int tile = blockIdx.x;
@@ -185,56 +169,51 @@ __global__ __launch_bounds__(kThreads) void quant_attn_partial_kernel(QAttnArgs 
   const int64_t n_src = comp ? (a.sel ? a.K : a.S) : a.W;
   const int64_t j0 = static_cast<int64_t>(comp ? tile : tile - a.n_comp_tiles) * ts;
   const int nt = static_cast<int>(min<int64_t>(ts, n_src - j0));
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 
-  load_query(a, b, comp, qs, qtmp);
+  for (int i = threadIdx.x; i < H * D; i += kThreads) qs[i] = bf16_to_f32(a.q[b * H * D + i]);
 
-  // stage the source tile (integer codes for compressed blocks, bf16 values for the window)
-  const int row_bytes = a.bits == 8 ? D : D / 2;
-  for (int e = threadIdx.x; e < nt * D; e += kThreads) {
-    const int jj = e / D, d = e % D;
-    float v;
-    if (comp) {
-      const int64_t s = a.sel ? a.sel[b * a.K + j0 + jj] : j0 + jj;
-      if (s < 0 || s >= a.S) {
-        v = 0.0f;
-      } else {
-        const uint8_t* cp = a.codes + (b * a.S + s) * row_bytes;
-        if (a.bits == 8) {
-          v = static_cast<float>(static_cast<int8_t>(cp[d]));
-        } else {
-          const uint32_t byte = cp[d >> 1];
-          const uint32_t nib = (d & 1) ? (byte >> 4) : (byte & 0x0fu);
-          v = static_cast<float>((static_cast<int>(nib) ^ 8) - 8);
-        }
+  if (comp) {
+    constexpr int RB = BITS == 8 ? D : D / 2;
+    const int sub = lane % LPV, slot = lane / LPV;
+    float dg[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) dg[e] = a.diag[sub * EPL + e];
+    for (int r0 = w * VPW; r0 < nt; r0 += (kThreads / 64) * VPW) {
+      const int jj = r0 + slot;
+      int64_t s = -1;
+      if (jj < nt) s = a.sel ? a.sel[b * a.K + j0 + jj] : j0 + jj;
+      const bool valid = jj < nt && s >= 0 && s < a.S;  // uniform within a lane group (one row)
+      if (valid) {
+        float v[EPL];
+        decode_lane<BITS, D>(a.codes + (b * a.S + s) * RB, a.scale[b * a.S + s], sub, dg, a.wscale, v);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) X[jj * DP + sub * EPL + e] = round_bf16(v[e]);
       }
-    } else {
-      v = bf16_to_f32(a.win[(b * a.W + j0 + jj) * D + d]);
+      if (jj < nt && sub == 0) okf[jj] = valid ? 1.0f : 0.0f;
     }
-    X[jj * DP + d] = v;
-  }
-  for (int jj = threadIdx.x; jj < nt; jj += kThreads) {
-    float s = 1.0f;
-    if (comp) {
-      const int64_t src = a.sel ? a.sel[b * a.K + j0 + jj] : j0 + jj;
-      s = (src < 0 || src >= a.S) ? 0.0f : a.scale[b * a.S + src];
+  } else {
+    for (int e = threadIdx.x; e < nt * D; e += kThreads) {
+      const int jj = e / D, d = e % D;
+      X[jj * DP + d] = bf16_to_f32(a.win[(b * a.W + j0 + jj) * D + d]);
     }
-    sig[jj] = s;
+    for (int jj = threadIdx.x; jj < nt; jj += kThreads) okf[jj] = 1.0f;
   }
   __syncthreads();
 
-  // logits
+  // logits l = scale * q.K
   for (int p = threadIdx.x; p < H * nt; p += kThreads) {
     const int h = p / nt, jj = p % nt;
     const float* qh = qs + h * D;
     const float* xj = X + jj * DP;
     float dot = 0.0f;
+#pragma unroll 8
     for (int d = 0; d < D; ++d) dot = fmaf(qh[d], xj[d], dot);
-    P[h * ts + jj] = sig[jj] == 0.0f ? kNegInf : (dot * sig[jj]) * a.sm_scale;
+    P[h * ts + jj] = okf[jj] == 0.0f ? kNegInf : dot * a.sm_scale;
   }
   __syncthreads();
 
   // per-head tile softmax (one wave per head, round robin)
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int h = w; h < H; h += kThreads / 64) {
     float mx = kNegInf;
     for (int jj = lane; jj < nt; jj += 64) mx = fmaxf(mx, P[h * ts + jj]);
@@ -244,7 +223,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_partial_kernel(QAttnArgs 
       const float l = P[h * ts + jj];
       const float e = l == kNegInf ? 0.0f : __expf(l - mx);
       sum += e;
-      P[h * ts + jj] = e * sig[jj];  // fold scale_j into the weight of the code vector
+      P[h * ts + jj] = e;
     }
     sum = wave_sum(sum);
     if (lane == 0) {
@@ -254,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_partial_kernel(QAttnArgs 
   }
   __syncthreads();
 
-  // PV
+  // PV (K = V: the same staged rows)
   float* dst = a.part + ((b * a.n_tiles + tile) * H) * (D + 2);
   for (int p = threadIdx.x; p < H * D; p += kThreads) {
     const int h = p / D, d = p % D;
@@ -269,17 +248,15 @@ __global__ __launch_bounds__(kThreads) void quant_attn_partial_kernel(QAttnArgs 
   }
 }
 
-__global__ __launch_bounds__(kThreads) void quant_attn_combine_kernel(QAttnArgs a) {
+// Merge the tiles of one row: M = max(sink, tile maxima), L = e^{sink-M} + sum_t e^{m_t-M} l_t,
+// out = sum_t e^{m_t-M} acc_t / L  (the sink counted once, aether_pipeline/serving.py:125-129).
+__global__ __launch_bounds__(kThreads) void quant_attn_combine_kernel(QAttnArgs a, int D) {
   extern __shared__ float smem[];
-  const int H = a.H, D = a.D;
-  float* rot = smem;          // H*D
-  float* rtmp = rot + H * D;  // H*D
-  float* win = rtmp + H * D;  // H*D
-  float* fac = win + H * D;   // n_tiles * H   (e^{m_t - M})
+  const int H = a.H;
+  float* fac = smem;                 // n_tiles * H
   float* den = fac + a.n_tiles * H;  // H
   const int64_t b = blockIdx.x;
   const float* part = a.part + (b * a.n_tiles) * H * (D + 2);
-
   for (int h = threadIdx.x; h < H; h += kThreads) {
     const float sk = a.sink[h];
     float M = sk;
@@ -296,36 +273,26 @@ __global__ __launch_bounds__(kThreads) void quant_attn_combine_kernel(QAttnArgs 
   __syncthreads();
   for (int p = threadIdx.x; p < H * D; p += kThreads) {
     const int h = p / D, d = p % D;
-    float r = 0.0f, wv = 0.0f;
-    for (int t = 0; t < a.n_tiles; ++t) {
-      const float v = fac[t * H + h] * part[(t * H + h) * (D + 2) + 2 + d];
-      if (t < a.n_comp_tiles) r += v; else wv += v;
-    }
-    rot[p] = r;
-    win[p] = wv;
+    float o = 0.0f;
+    for (int t = 0; t < a.n_tiles; ++t) o = fmaf(fac[t * H + h], part[(t * H + h) * (D + 2) + 2 + d], o);
+    a.out[b * H * D + p] = static_cast<uint16_t>(pack_bf16x2(o / den[h], 0.0f) & 0xffffu);
   }
-  __syncthreads();
-  // rotate the compressed part back: diag * WHT(rot)
-  float* src = rot;
-  float* dst = rtmp;
-  const int pairs = H * D / 2, half = D / 2;
-  for (int hh = 1; hh < D; hh <<= 1) {
-    for (int p = threadIdx.x; p < pairs; p += kThreads) {
-      const int head = p / half, r = p % half;
-      const int i = head * D + (r / hh) * 2 * hh + (r % hh);
-      const float x = src[i], y = src[i + hh];
-      dst[i] = x + y;
-      dst[i + hh] = x - y;
-    }
-    __syncthreads();
-    float* t = src;
-    src = dst;
-    dst = t;
-  }
-  for (int p = threadIdx.x; p < H * D; p += kThreads) {
-    const int h = p / D, d = p % D;
-    const float o = ((src[p] * a.wscale) * a.diag[d] + win[p]) / den[h];
-    a.out[b * H * D + p] = static_cast<uint16_t>(pack_bf16x2(o, 0.0f) & 0xffffu);
+}
+
+typedef void (*qattn_fn)(QAttnArgs);
+
+template <int BITS>
+qattn_fn pick_qattn(int D) {
+  switch (D) {
+    case 2: return quant_attn_partial_kernel<BITS, 2>;
+    case 4: return quant_attn_partial_kernel<BITS, 4>;
+    case 8: return quant_attn_partial_kernel<BITS, 8>;
+    case 16: return quant_attn_partial_kernel<BITS, 16>;
+    case 32: return quant_attn_partial_kernel<BITS, 32>;
+    case 64: return quant_attn_partial_kernel<BITS, 64>;
+    case 128: return quant_attn_partial_kernel<BITS, 128>;
+    case 256: return quant_attn_partial_kernel<BITS, 256>;
+    default: return nullptr;
   }
 }
 
@@ -354,16 +321,13 @@ __global__ void zero_u16_kernel(uint16_t* __restrict__ p, int64_t n) {
   if (i < n) p[i] = 0;
 }
 
-// Dynamic LDS above 64 KB must be enabled per kernel; done once per process.
-void allow_big_lds() {
-  static const bool done = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(quant_attn_partial_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(quant_attn_combine_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    return true;
-  }();
-  (void)done;
+// Dynamic LDS above 64 KB must be enabled per kernel; the attribute is set on every launch path
+// (idempotent and cheap).
+void allow_big_lds(const void* fn) {
+  static std::mutex mu;
+  static std::unordered_set<const void*> done;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.insert(fn).second) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
 }
 
 template <int DT>
@@ -451,19 +415,22 @@ extern "C" size_t aekv_quant_attention_workspace_size(int64_t B, int64_t H, int6
 
 extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const float* scale, const int64_t* sel,
                                          const void* window, const float* sink, const float* diag, int64_t B, int64_t H,
-                                         int64_t D, int64_t S, int64_t K, int64_t W, int32_t bits, float softmax_scale,
+                                         int64_t D, int64_t S, int64_t n_sel, int64_t W, int32_t bits, float softmax_scale,
                                          void* ws, size_t ws_bytes, void* out, void* stream) {
   const char* who = "aekv_quant_sink_attention";
   if (bits != 4 && bits != 8) return fail(AEKV_ERR_VALUE, "bits must be 4 or 8, got %d", bits);
   if (!is_pow2(D)) return fail(AEKV_ERR_VALUE, "WHT requires last dim to be a power of 2, got %lld", (long long)D);
   if (D < 2 || D > 256) return fail(AEKV_ERR_UNSUPPORTED, "%s: head_dim %lld outside [2, 256]", who, (long long)D);
-  if (B < 0 || H <= 0 || S < 0 || K < 0 || W < 0) return fail(AEKV_ERR_SHAPE, "%s: bad sizes", who);
+  if (B < 0 || H <= 0 || S < 0 || W < 0) return fail(AEKV_ERR_SHAPE, "%s: bad sizes", who);
   if (H * D > 4096) return fail(AEKV_ERR_UNSUPPORTED, "%s: H*D=%lld exceeds 4096", who, (long long)(H * D));
   if (B > 65535) return fail(AEKV_ERR_UNSUPPORTED, "%s: B exceeds 65535", who);
-  const int64_t n_comp = sel ? K : S;
+  const bool all_blocks = n_sel < 0;  // HCA: every block in order
+  const int64_t K = all_blocks ? 0 : n_sel;
+  const int64_t n_comp = all_blocks ? S : K;
   const QLayout l = qlayout(B, H, D, n_comp, W);
   if (B == 0) return AEKV_OK;
-  if (!q || !sink || !diag || !out || (n_comp > 0 && (!codes || !scale)) || (W > 0 && !window))
+  if (!q || !sink || !diag || !out || (n_comp > 0 && (!codes || !scale)) || (W > 0 && !window) ||
+      (K > 0 && !sel))
     return fail(AEKV_ERR_VALUE, "%s: null pointer", who);
   if (l.n_tiles == 0) {
     // no sources: every weight is zero -> out = 0 (serving.py:451-452)
@@ -479,7 +446,7 @@ extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const
   a.q = static_cast<const uint16_t*>(q);
   a.codes = static_cast<const uint8_t*>(codes);
   a.scale = scale;
-  a.sel = sel;
+  a.sel = all_blocks ? nullptr : sel;
   a.win = static_cast<const uint16_t*>(window);
   a.sink = sink;
   a.diag = diag;
@@ -487,8 +454,6 @@ extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const
   a.K = K;
   a.W = W;
   a.H = static_cast<int>(H);
-  a.D = static_cast<int>(D);
-  a.bits = bits;
   a.ts = l.ts;
   a.n_comp_tiles = l.n_comp_tiles;
   a.n_tiles = l.n_tiles;
@@ -497,15 +462,17 @@ extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const
   a.part = static_cast<float*>(ws);
   a.out = static_cast<uint16_t*>(out);
   const hipStream_t st = as_stream(stream);
-  allow_big_lds();
-  const size_t sm1 = sizeof(float) * (2 * H * D + static_cast<size_t>(l.ts) * (D + 1) + l.ts + H * l.ts + 2 * H);
+  qattn_fn fn = bits == 8 ? pick_qattn<8>(static_cast<int>(D)) : pick_qattn<4>(static_cast<int>(D));
+  allow_big_lds(reinterpret_cast<const void*>(fn));
+  const size_t sm1 = sizeof(float) * (H * D + static_cast<size_t>(l.ts) * (D + 1) + l.ts + H * l.ts + 2 * H);
   if (sm1 > 160 * 1024) return fail(AEKV_ERR_UNSUPPORTED, "%s: source tile does not fit in LDS", who);
-  hipLaunchKernelGGL(quant_attn_partial_kernel, dim3(static_cast<uint32_t>(l.n_tiles), static_cast<uint32_t>(B)),
-                     dim3(kThreads), sm1, st, a);
+  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(l.n_tiles), static_cast<uint32_t>(B)), dim3(kThreads), sm1, st, a);
   if (int rc = check_launch(who)) return rc;
-  const size_t sm2 = sizeof(float) * (3 * H * D + static_cast<size_t>(l.n_tiles) * H + H);
+  const size_t sm2 = sizeof(float) * (static_cast<size_t>(l.n_tiles) * H + H);
   if (sm2 > 160 * 1024) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many tiles for the combine", who);
-  hipLaunchKernelGGL(quant_attn_combine_kernel, dim3(static_cast<uint32_t>(B)), dim3(kThreads), sm2, st, a);
+  allow_big_lds(reinterpret_cast<const void*>(quant_attn_combine_kernel));
+  hipLaunchKernelGGL(quant_attn_combine_kernel, dim3(static_cast<uint32_t>(B)), dim3(kThreads), sm2, st, a,
+                     static_cast<int>(D));
   return check_launch(who);
 }
 

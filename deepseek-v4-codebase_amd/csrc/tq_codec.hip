@@ -12,106 +12,13 @@
 // lane l with lane l ^ (h/EPL) (DPP for 1/2, ds_swizzle for 4/8/16, ds_bpermute for 32).  The
 // butterfly result for the lane holding the upper element is partner - mine, for the lower one
 // mine + partner; both are one fmaf(mine, +-1, partner).
-#include "aekv_common.h"
+#include "tq_device.h"
 
 namespace aekv {
 namespace {
 
 constexpr int kThreads = 256;
 enum { kModeWht = 0, kModeEnc4 = 4, kModeEnc8 = 8 };
-
-template <int N>
-struct alignas(N) Bytes {
-  uint8_t b[N];
-};
-
-// Load EPL elements of type dtype (F32/F16/BF16) starting at element offset `off`.
-template <int DT, int EPL>
-__device__ __forceinline__ void load_elems(const void* base, int64_t off, bool ok, float (&a)[EPL]) {
-  constexpr int ES = DT == AEKV_F32 ? 4 : 2;
-  constexpr int NB = ES * EPL;
-  if (!ok) {
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) a[e] = 0.0f;
-    return;
-  }
-  const uint8_t* p = static_cast<const uint8_t*>(base) + off * ES;
-  if constexpr (NB <= 16) {
-    Bytes<NB> raw = *reinterpret_cast<const Bytes<NB>*>(p);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      if constexpr (DT == AEKV_F32) {
-        uint32_t u;
-        __builtin_memcpy(&u, raw.b + 4 * e, 4);
-        a[e] = __builtin_bit_cast(float, u);
-      } else {
-        uint16_t u;
-        __builtin_memcpy(&u, raw.b + 2 * e, 2);
-        a[e] = DT == AEKV_BF16 ? bf16_to_f32(u) : f16_to_f32(u);
-      }
-    }
-  } else {  // fp32, EPL == 8: two 16-byte loads
-    Bytes<16> r0 = reinterpret_cast<const Bytes<16>*>(p)[0];
-    Bytes<16> r1 = reinterpret_cast<const Bytes<16>*>(p)[1];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      uint32_t u0, u1;
-      __builtin_memcpy(&u0, r0.b + 4 * e, 4);
-      __builtin_memcpy(&u1, r1.b + 4 * e, 4);
-      a[e] = __builtin_bit_cast(float, u0);
-      a[e + 4] = __builtin_bit_cast(float, u1);
-    }
-  }
-}
-
-template <int HL, int EPL>
-__device__ __forceinline__ void cross_stage(float (&a)[EPL], int sub) {
-  const float s = (sub & HL) ? -1.0f : 1.0f;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    const float p = xor_lane<HL>(a[e]);
-    a[e] = fmaf(a[e], s, p);  // lower lane: a + p ; upper lane: p - a   (product exact)
-  }
-}
-
-// Butterfly stages of a D-point transform spread over LPV lanes x EPL elements.
-template <int D, int EPL>
-__device__ __forceinline__ void wht_butterflies(float (&a)[EPL], int sub) {
-  constexpr int LPV = D / EPL;
-#pragma unroll
-  for (int h = 1; h < EPL; h <<= 1) {
-#pragma unroll
-    for (int blk = 0; blk < EPL; blk += 2 * h) {
-#pragma unroll
-      for (int i = 0; i < h; ++i) {
-        const float x = a[blk + i], y = a[blk + h + i];
-        a[blk + i] = x + y;
-        a[blk + h + i] = x - y;
-      }
-    }
-  }
-  if constexpr (LPV > 1) cross_stage<1>(a, sub);
-  if constexpr (LPV > 2) cross_stage<2>(a, sub);
-  if constexpr (LPV > 4) cross_stage<4>(a, sub);
-  if constexpr (LPV > 8) cross_stage<8>(a, sub);
-  if constexpr (LPV > 16) cross_stage<16>(a, sub);
-  if constexpr (LPV > 32) cross_stage<32>(a, sub);
-}
-
-template <int D, int EPL>
-__device__ __forceinline__ float group_absmax(const float (&a)[EPL]) {
-  constexpr int LPV = D / EPL;
-  float m = 0.0f;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) m = fmaxf(m, fabsf(a[e]));
-  if constexpr (LPV > 1) m = fmaxf(m, xor_lane<1>(m));
-  if constexpr (LPV > 2) m = fmaxf(m, xor_lane<2>(m));
-  if constexpr (LPV > 4) m = fmaxf(m, xor_lane<4>(m));
-  if constexpr (LPV > 8) m = fmaxf(m, xor_lane<8>(m));
-  if constexpr (LPV > 16) m = fmaxf(m, xor_lane<16>(m));
-  if constexpr (LPV > 32) m = fmaxf(m, xor_lane<32>(m));
-  return m;
-}
 
 // Forward kernel: WHT (fp32 out), or encode to 8/4-bit codes + fp32 scale.
 template <int DT, int D, int MODE>
@@ -195,7 +102,6 @@ __global__ __launch_bounds__(kThreads) void tq_decode_kernel(const void* __restr
   constexpr int EPL = D < 8 ? D : 8;
   constexpr int LPV = D / EPL;
   constexpr int VPW = 64 / LPV;
-  constexpr int NB = BITS == 8 ? EPL : EPL / 2;  // code bytes per lane
   const int lane = threadIdx.x & 63;
   const int sub = lane % LPV;
   const int slot = lane / LPV;
@@ -210,28 +116,9 @@ __global__ __launch_bounds__(kThreads) void tq_decode_kernel(const void* __restr
     const int64_t v = base + slot;
     const bool ok = v < n_vec;
     float a[EPL];
-    if (ok) {
-      const float s = scale[v];
-      const uint8_t* p = static_cast<const uint8_t*>(codes) + v * (BITS == 8 ? D : D / 2) + sub * NB;
-      Bytes<NB> w = *reinterpret_cast<const Bytes<NB>*>(p);
-#pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        if constexpr (BITS == 8) {
-          a[i] = static_cast<float>(static_cast<int8_t>(w.b[i])) * s;
-        } else {
-          const int lo = (static_cast<int>(w.b[i] & 0x0f) ^ 8) - 8;  // sign-extend nibble
-          const int hi = (static_cast<int>(w.b[i] >> 4) ^ 8) - 8;
-          a[2 * i] = static_cast<float>(lo) * s;
-          a[2 * i + 1] = static_cast<float>(hi) * s;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) a[e] = 0.0f;
-    }
-    wht_butterflies<D, EPL>(a, sub);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) a[e] = (a[e] * c) * dg[e];  // _wht(...) * diag
+    // inactive lanes decode row 0 so every lane joins the cross-lane butterflies
+    const int64_t vr = ok ? v : 0;
+    decode_lane<BITS, D>(static_cast<const uint8_t*>(codes) + vr * (BITS == 8 ? D : D / 2), scale[vr], sub, dg, c, a);
     if (ok) {
       uint8_t* o = static_cast<uint8_t*>(out) + (v * D + sub * EPL) * (ODT == AEKV_F32 ? 4 : 2);
       if constexpr (ODT == AEKV_F32) {

@@ -1,0 +1,133 @@
+// Device-side building blocks of the TurboQuant codec, shared by the codec kernels and by the
+// attention kernels that dequantise KV codes on load.
+//
+// Layout: a D-element vector is spread over LPV = D/EPL lanes with EPL = min(D, 8) consecutive
+// elements per lane.  Butterfly stages h < EPL run inside a lane; stage h >= EPL pairs lane l with
+// lane l ^ (h/EPL).  Every fp32 operation of aether_2b/turbo_quant.py:49-211 is performed once, in
+// the reference's order, so results are bit-exact (the library is built with -ffp-contract=off).
+#pragma once
+
+#include "aekv_common.h"
+
+namespace aekv {
+
+template <int N>
+struct alignas(N) Bytes {
+  uint8_t b[N];
+};
+
+// Load EPL elements of type dtype (F32/F16/BF16) starting at element offset `off`.
+template <int DT, int EPL>
+__device__ __forceinline__ void load_elems(const void* base, int64_t off, bool ok, float (&a)[EPL]) {
+  constexpr int ES = DT == AEKV_F32 ? 4 : 2;
+  constexpr int NB = ES * EPL;
+  if (!ok) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) a[e] = 0.0f;
+    return;
+  }
+  const uint8_t* p = static_cast<const uint8_t*>(base) + off * ES;
+  if constexpr (NB <= 16) {
+    Bytes<NB> raw = *reinterpret_cast<const Bytes<NB>*>(p);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      if constexpr (DT == AEKV_F32) {
+        uint32_t u;
+        __builtin_memcpy(&u, raw.b + 4 * e, 4);
+        a[e] = __builtin_bit_cast(float, u);
+      } else {
+        uint16_t u;
+        __builtin_memcpy(&u, raw.b + 2 * e, 2);
+        a[e] = DT == AEKV_BF16 ? bf16_to_f32(u) : f16_to_f32(u);
+      }
+    }
+  } else {  // fp32, EPL == 8: two 16-byte loads
+    Bytes<16> r0 = reinterpret_cast<const Bytes<16>*>(p)[0];
+    Bytes<16> r1 = reinterpret_cast<const Bytes<16>*>(p)[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t u0, u1;
+      __builtin_memcpy(&u0, r0.b + 4 * e, 4);
+      __builtin_memcpy(&u1, r1.b + 4 * e, 4);
+      a[e] = __builtin_bit_cast(float, u0);
+      a[e + 4] = __builtin_bit_cast(float, u1);
+    }
+  }
+}
+
+template <int HL, int EPL>
+__device__ __forceinline__ void cross_stage(float (&a)[EPL], int sub) {
+  const float s = (sub & HL) ? -1.0f : 1.0f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float p = xor_lane<HL>(a[e]);
+    a[e] = fmaf(a[e], s, p);  // lower lane: a + p ; upper lane: p - a   (product exact)
+  }
+}
+
+// Butterfly stages of a D-point transform spread over LPV lanes x EPL elements.
+template <int D, int EPL>
+__device__ __forceinline__ void wht_butterflies(float (&a)[EPL], int sub) {
+  constexpr int LPV = D / EPL;
+#pragma unroll
+  for (int h = 1; h < EPL; h <<= 1) {
+#pragma unroll
+    for (int blk = 0; blk < EPL; blk += 2 * h) {
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const float x = a[blk + i], y = a[blk + h + i];
+        a[blk + i] = x + y;
+        a[blk + h + i] = x - y;
+      }
+    }
+  }
+  if constexpr (LPV > 1) cross_stage<1>(a, sub);
+  if constexpr (LPV > 2) cross_stage<2>(a, sub);
+  if constexpr (LPV > 4) cross_stage<4>(a, sub);
+  if constexpr (LPV > 8) cross_stage<8>(a, sub);
+  if constexpr (LPV > 16) cross_stage<16>(a, sub);
+  if constexpr (LPV > 32) cross_stage<32>(a, sub);
+}
+
+template <int D, int EPL>
+__device__ __forceinline__ float group_absmax(const float (&a)[EPL]) {
+  constexpr int LPV = D / EPL;
+  float m = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) m = fmaxf(m, fabsf(a[e]));
+  if constexpr (LPV > 1) m = fmaxf(m, xor_lane<1>(m));
+  if constexpr (LPV > 2) m = fmaxf(m, xor_lane<2>(m));
+  if constexpr (LPV > 4) m = fmaxf(m, xor_lane<4>(m));
+  if constexpr (LPV > 8) m = fmaxf(m, xor_lane<8>(m));
+  if constexpr (LPV > 16) m = fmaxf(m, xor_lane<16>(m));
+  if constexpr (LPV > 32) m = fmaxf(m, xor_lane<32>(m));
+  return m;
+}
+
+
+// Dequantise the EPL elements of one vector held by this lane: codes * scale -> WHT -> * c -> * diag
+// (turbo_quant.py:187-211).  `row` points at the vector's code bytes.
+template <int BITS, int D>
+__device__ __forceinline__ void decode_lane(const uint8_t* __restrict__ row, float s, int sub,
+                                            const float (&dg)[(D < 8 ? D : 8)], float c,
+                                            float (&a)[(D < 8 ? D : 8)]) {
+  constexpr int EPL = D < 8 ? D : 8;
+  constexpr int NB = BITS == 8 ? EPL : EPL / 2;
+  Bytes<NB> w = *reinterpret_cast<const Bytes<NB>*>(row + sub * NB);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    if constexpr (BITS == 8) {
+      a[i] = static_cast<float>(static_cast<int8_t>(w.b[i])) * s;
+    } else {
+      const int lo = (static_cast<int>(w.b[i] & 0x0f) ^ 8) - 8;  // sign-extend nibble
+      const int hi = (static_cast<int>(w.b[i] >> 4) ^ 8) - 8;
+      a[2 * i] = static_cast<float>(lo) * s;
+      a[2 * i + 1] = static_cast<float>(hi) * s;
+    }
+  }
+  wht_butterflies<D, EPL>(a, sub);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) a[e] = (a[e] * c) * dg[e];
+}
+
+}  // namespace aekv

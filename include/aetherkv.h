@@ -133,18 +133,18 @@ int aekv_sparse_sink_attention(const void* q, const void* kv, const void* topk, 
 /* Sink attention of one bf16 query token per row over TurboQuant-compressed shared K=V blocks plus
  * a bf16 sliding window (the serving engine's decode step, dequantise + gather + concat + attend
  * fused):
- *   q [B,H,D] bf16; codes [B,S,D or D/2] + scale [B,S]; sel [B,K] int64 block indices
- *   (sel == NULL: all S blocks in order, i.e. HCA; entries outside [0,S) are skipped);
+ *   q [B,H,D] bf16; codes [B,S,D or D/2] + scale [B,S]; sel [B,n_sel] int64 block indices
+ *   (n_sel < 0: all S blocks in order, i.e. HCA, sel ignored; entries outside [0,S) are skipped);
  *   window [B,W,D] bf16 (W may be 0); sink fp32 [H]; out [B,H,D] bf16.
  *   Sources = [dequant(blocks[sel]), window]; K = V = source (aether_2b/serving.py:52-53).
- * The compressed sources stay in the rotated domain: logits use WHT(diag*q), the value sum is
- * rotated back once per (row, head). */
+ * Gathered code rows are dequantised on load to exactly the bf16 values PolarQuant.decode returns
+ * (the engine attends its bf16 dequantised cache); logits and the value sum accumulate in fp32. */
 size_t aekv_quant_attention_workspace_size(int64_t B, int64_t H, int64_t D, int64_t n_comp,
                                            int64_t W);
 int aekv_quant_sink_attention(const void* q, const void* codes, const float* scale,
                               const int64_t* sel, const void* window, const float* sink,
                               const float* diag, int64_t B, int64_t H, int64_t D, int64_t S,
-                              int64_t K, int64_t W, int32_t bits, float softmax_scale,
+                              int64_t n_sel, int64_t W, int32_t bits, float softmax_scale,
                               void* ws, size_t ws_bytes, void* out, void* stream);
 
 /* hca_compress drop-in: out[b,d] = sum_m softmax_m(z[b,:,d]) * c[b,m,d], c/z [B,M,D], dtype

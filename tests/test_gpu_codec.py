@@ -75,7 +75,7 @@ def test_wht_bit_exact(dev, d, dt):
     np.testing.assert_array_equal(got, O.wht(host_bits(x, dt), dt))
     # self-inverse (reference test_wht_self_inverse)
     if dt == "f32":
-        np.testing.assert_allclose(_wht(_wht(x.to(dev))).cpu().numpy(), x.numpy(), atol=1e-5)
+        np.testing.assert_allclose(_wht(_wht(x.to(dev))).cpu().numpy(), x.numpy(), rtol=1e-6, atol=1e-5)
 
 
 def test_config1_8bit_round_trip_bit_exact(dev):
