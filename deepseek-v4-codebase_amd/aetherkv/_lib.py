@@ -31,7 +31,7 @@ SYMBOLS = (
     "aekv_version", "aekv_last_error", "aekv_max_head_dim", "aekv_max_topk", "aekv_tq_diag", "aekv_wht",
     "aekv_tq_encode", "aekv_tq_decode", "aekv_csa_indexer_workspace_size", "aekv_csa_indexer_topk",
     "aekv_csa_indexer_topk_quant", "aekv_sparse_sink_attention", "aekv_quant_attention_workspace_size",
-    "aekv_quant_sink_attention", "aekv_hca_compress", "aekv_tiled_prefill_attention",
+    "aekv_quant_sink_attention", "aekv_hca_compress", "aekv_tiled_prefill_attention", "aekv_set_generic_kernels",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -60,6 +60,7 @@ def lib() -> ctypes.CDLL:
         "aekv_last_error": ([], ctypes.c_char_p),
         "aekv_max_head_dim": ([], I32_),
         "aekv_max_topk": ([], I32_),
+        "aekv_set_generic_kernels": ([ctypes.c_int], ctypes.c_int),
         "aekv_tq_diag": ([I64_, I32_, P], ctypes.c_int),
         "aekv_wht": ([P, I32_, I64_, I32_, P, P], ctypes.c_int),
         "aekv_tq_encode": ([P, I32_, I64_, I32_, I32_, P, P, P, P], ctypes.c_int),

@@ -253,6 +253,9 @@ extern "C" int aekv_tq_encode(const void* x, int32_t x_dtype, int64_t n_vec, int
   const size_t out_al = bits == 8 ? epl : epl / 2;
   if (!is_aligned(x, in_al) || !is_aligned(codes, out_al) || !is_aligned(scale, 4) || !is_aligned(diag, 4))
     return fail(AEKV_ERR_ALIGN, "aekv_tq_encode: misaligned pointer (x needs %zu, codes %zu bytes)", in_al, out_al);
+  if (bits == 4 && d == 128 && x_dtype == AEKV_BF16 && use_specialised_codec() &&
+      launch_encode4_d128_bf16(x, n_vec, diag, wht_scale(d), codes, scale, as_stream(stream)))
+    return check_launch("aekv_tq_encode");
   fwd_fn fn = bits == 8 ? pick_fwd_dt<kModeEnc8>(x_dtype, d) : pick_fwd_dt<kModeEnc4>(x_dtype, d);
   hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(grid_for(n_vec, d))), dim3(kThreads), 0, as_stream(stream), x,
                      n_vec, diag, wht_scale(d), codes, scale);

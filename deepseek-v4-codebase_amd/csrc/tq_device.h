@@ -130,4 +130,11 @@ __device__ __forceinline__ void decode_lane(const uint8_t* __restrict__ row, flo
   for (int e = 0; e < EPL; ++e) a[e] = (a[e] * c) * dg[e];
 }
 
+// Specialised production-shape kernels (tq_encode_d128.hip).  Each returns false (and launches
+// nothing) when its alignment requirements are not met, so the caller falls back to the generic
+// kernel.  AETHERKV_CODEC=generic in the environment forces the generic kernels (testing aid).
+bool launch_encode4_d128_bf16(const void* x, int64_t n_vec, const float* diag, float c, void* codes, float* scale,
+                              hipStream_t st);
+bool use_specialised_codec();
+
 }  // namespace aekv

@@ -73,6 +73,11 @@ const char* aekv_last_error(void);
 /* Largest supported values (compile-time limits of the kernels). */
 int32_t aekv_max_head_dim(void);   /* power-of-two vector length limit for the codec (512)   */
 int32_t aekv_max_topk(void);       /* largest k accepted by the indexer select (2048)         */
+/* Kernel selection (no reference counterpart; a testing and A/B aid): 1 = use only the generic
+ * kernels, 0 = also use the kernels specialised for the production shape (default, unless the
+ * environment sets AETHERKV_CODEC=generic).  Both produce identical results.  Returns the
+ * previous setting. */
+int aekv_set_generic_kernels(int generic_only);
 
 /* ---- TurboQuant codec -------------------------------------------------------------------- */
 /* Rademacher diagonal of PolarQuant(seed)._diag(d): MT19937 seeded with seed*10007+d, one

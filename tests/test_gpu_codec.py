@@ -73,9 +73,10 @@ def test_wht_bit_exact(dev, d, dt):
     x = special_rows(300, d, TDT[dt]) if d >= 8 else torch.randn(300, d).to(TDT[dt])
     got = _wht(x.to(dev)).cpu().numpy()
     np.testing.assert_array_equal(got, O.wht(host_bits(x, dt), dt))
-    # self-inverse (reference test_wht_self_inverse)
+    # self-inverse on the N(0,1) rows (reference test_wht_self_inverse: randn, atol 1e-5)
     if dt == "f32":
-        np.testing.assert_allclose(_wht(_wht(x.to(dev))).cpu().numpy(), x.numpy(), rtol=1e-6, atol=1e-5)
+        xs = x[5:]
+        np.testing.assert_allclose(_wht(_wht(xs.to(dev))).cpu().numpy(), xs.numpy(), atol=1e-5)
 
 
 def test_config1_8bit_round_trip_bit_exact(dev):
@@ -120,6 +121,50 @@ def test_config2_4bit_full_layer_properties(dev):
     # quality: reference 4-bit threshold (cosine > 0.99 on Gaussian rows)
     cos = torch.nn.functional.cosine_similarity(x.float().view(-1, D), rec.float().view(-1, D), dim=-1)
     assert float(cos.mean()) > 0.99
+
+
+def near_tie_rows(n: int, seed: int) -> torch.Tensor:
+    """bf16 rows whose rotated values sit on or next to quantiser ties: x*diag = a*e_0 + b*e_j gives
+    raw butterflies a +- b, so raw/max*7 hits k + 1/2 for (a+b, a-b) = (14, 1), (14, 3), (254, 1) ..."""
+    g = torch.Generator().manual_seed(seed)
+    dg = torch.from_numpy(O.diag(42, 128))
+    x = torch.zeros(n, 128)
+    pairs = [(7.5, 6.5), (8.5, 5.5), (9.5, 4.5), (127.5, 126.5), (3.5, 3.0), (1.0, 0.0), (0.75, 0.25)]
+    for i in range(n):
+        a, b = pairs[i % len(pairs)]
+        j = int(torch.randint(1, 128, (1,), generator=g))
+        s = float(torch.randn(1, generator=g).sign())
+        x[i, 0] = a * s
+        x[i, j] = b * s * (1 if i % 2 else -1)
+        if i % 3 == 0:
+            x[i, (j + 5) % 127 + 1] += 0.5
+    return (x * dg).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_encode_near_tie_rows_bit_exact(dev, bits):
+    x = near_tie_rows(4001, 17)
+    want_c, want_s = O.encode(bf16_bits(x), "bf16", bits, O.diag(42, 128))
+    pq = PolarQuant(bits)
+    codes, scale = pq.encode(x.to(dev))
+    np.testing.assert_array_equal(codes.cpu().numpy(), want_c)
+    np.testing.assert_array_equal(scale.cpu().numpy(), want_s)
+
+
+def test_specialised_and_generic_encode_agree(dev):
+    import aetherkv._lib as L
+
+    x = normal_with_outliers((3001, 128), 5, trailing_dims=1).to(dev)
+    pq = PolarQuant(4)
+    prev = L.lib().aekv_set_generic_kernels(1)
+    try:
+        cg, sg = pq.encode(x)
+    finally:
+        L.lib().aekv_set_generic_kernels(prev)
+    cs, ss = pq.encode(x)
+    assert torch.equal(cg, cs) and torch.equal(sg, ss)
+    want_c, want_s = O.encode(bf16_bits(x), "bf16", 4, O.diag(42, 128))
+    np.testing.assert_array_equal(cs.cpu().numpy(), want_c)
 
 
 def test_empty_and_misaligned_inputs(dev):
