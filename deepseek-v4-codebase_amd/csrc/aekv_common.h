@@ -27,6 +27,14 @@ float wht_scale(int d);
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Matrix-core indexer for quantised keys (csa_indexer_mfma.hip).
+bool mfma_indexer_supported(int IH, int IC, int k, int64_t S);
+size_t mfma_indexer_workspace(int64_t B, int64_t S, int32_t k);
+int launch_mfma_indexer(const float* q, const float* w, const void* codes, const float* kscale, const float* diag,
+                        const int32_t* valid, int64_t B, int64_t S, int IH, int IC, int bits, int k, int mode, void* ws,
+                        int64_t* out_idx, float* out_score, hipStream_t st, const char* who);
+bool use_specialised_codec();
+
 // ---- device helpers ------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __builtin_bit_cast(float, bits16 << 16); }
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {

@@ -17,6 +17,8 @@
 // Quantised keys are scanned in the rotated domain: q.k_j = scale_j * (WHT(diag*q) . codes_j)
 // (the WHT is orthogonal and symmetric; turbo_quant.py:208-209), and since scale_j > 0,
 // relu(scale_j * x) = scale_j * relu(x).
+#include <algorithm>
+
 #include "aekv_common.h"
 
 namespace aekv {
@@ -340,9 +342,9 @@ int validate_common(const float* q, const float* w, int64_t B, int64_t S, int32_
     return fail(AEKV_ERR_UNSUPPORTED, "%s: S=%lld exceeds %d", who, (long long)S, kChunk * 1024);
   if (B > 65535) return fail(AEKV_ERR_UNSUPPORTED, "%s: B=%lld exceeds 65535", who, (long long)B);
   if (B > 0 && (!q || !w || !out_idx)) return fail(AEKV_ERR_VALUE, "%s: null pointer", who);
-  const WsLayout l = ws_layout(B, S, k);
-  if (B > 0 && (!ws || ws_bytes < l.total))
-    return fail(AEKV_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who, l.total, ws_bytes);
+  const size_t need = std::max(ws_layout(B, S, k).total, mfma_indexer_workspace(B, S, k));
+  if (B > 0 && (!ws || ws_bytes < need))
+    return fail(AEKV_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who, need, ws_bytes);
   if (ws && !is_aligned(ws, 256)) return fail(AEKV_ERR_ALIGN, "%s: workspace must be 256-byte aligned", who);
   return AEKV_OK;
 }
@@ -374,7 +376,7 @@ using namespace aekv;
 
 extern "C" size_t aekv_csa_indexer_workspace_size(int64_t B, int64_t S, int32_t k) {
   if (B <= 0 || k <= 0) return 256;
-  return ws_layout(B, S, k).total;
+  return std::max(ws_layout(B, S, k).total, mfma_indexer_workspace(B, S, k));
 }
 
 extern "C" int aekv_csa_indexer_topk(const float* index_q, const float* index_kv, const float* index_weight,
@@ -420,5 +422,8 @@ extern "C" int aekv_csa_indexer_topk_quant(const float* index_q, const float* in
   a.IC = IC;
   a.k = k;
   a.mode = mode;
+  if (use_specialised_codec() && mfma_indexer_supported(IH, IC, k, S))
+    return launch_mfma_indexer(index_q, index_weight, key_codes, key_scale, diag, valid, B, S, IH, IC, bits, k, mode, ws,
+                               out_idx, out_score, as_stream(stream), who);
   return launch_indexer(bits == 8 ? kKeyQ8 : kKeyQ4, a, B, S, ws, out_idx, out_score, as_stream(stream), who);
 }

@@ -184,13 +184,17 @@ __global__ __launch_bounds__(kThreads) void quant_attn_partial_kernel(QAttnArgs 
       int64_t s = -1;
       if (jj < nt) s = a.sel ? a.sel[b * a.K + j0 + jj] : j0 + jj;
       const bool valid = jj < nt && s >= 0 && s < a.S;  // uniform within a lane group (one row)
-      if (valid) {
+      if (jj < nt) {
+        // A skipped index still gets a zero row: the PV pass multiplies every staged row by its
+        // (zero) probability, and 0 * stale LDS contents could be NaN.
         float v[EPL];
-        decode_lane<BITS, D>(a.codes + (b * a.S + s) * RB, a.scale[b * a.S + s], sub, dg, a.wscale, v);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[e] = 0.0f;
+        if (valid) decode_lane<BITS, D>(a.codes + (b * a.S + s) * RB, a.scale[b * a.S + s], sub, dg, a.wscale, v);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) X[jj * DP + sub * EPL + e] = round_bf16(v[e]);
+        if (sub == 0) okf[jj] = valid ? 1.0f : 0.0f;
       }
-      if (jj < nt && sub == 0) okf[jj] = valid ? 1.0f : 0.0f;
     }
   } else {
     for (int e = threadIdx.x; e < nt * D; e += kThreads) {

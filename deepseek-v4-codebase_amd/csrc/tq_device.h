@@ -135,6 +135,5 @@ __device__ __forceinline__ void decode_lane(const uint8_t* __restrict__ row, flo
 // kernel.  AETHERKV_CODEC=generic in the environment forces the generic kernels (testing aid).
 bool launch_encode4_d128_bf16(const void* x, int64_t n_vec, const float* diag, float c, void* codes, float* scale,
                               hipStream_t st);
-bool use_specialised_codec();
 
 }  // namespace aekv

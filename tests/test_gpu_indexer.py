@@ -111,3 +111,23 @@ def test_config3_indexer_8bit(dev):
 def test_config5_indexer_4bit_rows(dev):
     # BASELINE cfg5 at full S (65536 blocks, 4-bit, outliers) on 2 of the 64 rows
     _quant_case(dev, 2, 65536, 4, 64, 4, 4, outliers=True)
+
+
+@pytest.fixture(params=["matrix", "generic"])
+def indexer_path(request):
+    """Run a case on the matrix-core indexer (default) and again on the generic VALU indexer."""
+    from aetherkv import _lib as L
+    prev = L.lib().aekv_set_generic_kernels(1 if request.param == "generic" else 0)
+    yield request.param
+    L.lib().aekv_set_generic_kernels(prev)
+
+
+@pytest.mark.parametrize("B,S,IH,IC,bits,k,valid,mode", [
+    (2, 1, 4, 64, 4, 8, None, "softplus"),                         # one key, k > S: -1 padding
+    (2, 100, 4, 64, 8, 256, [100, 17], "raw"),                     # k > visible keys
+    (3, 20000, 16, 128, 4, 1024, [20000, 8193, 2049], "relu_w"),   # 4 row blocks, largest k
+    (2, 9000, 3, 128, 8, 1, None, "softplus"),                     # heads not a multiple of 4, k = 1
+    (2, 70000, 8, 64, 4, 512, [70000, 16385], "softplus"),         # many chunks, ragged tail
+])
+def test_quant_indexer_shapes_both_paths(dev, indexer_path, B, S, IH, IC, bits, k, valid, mode):
+    _quant_case(dev, B, S, IH, IC, bits, 50 + S % 97, mode=mode, k=k, valid=valid)
