@@ -1,9 +1,9 @@
 #!/usr/bin/env python3
 """Benchmark of the compressed-KV hot path on one MI355X.
 
-Metric (BASELINE.json): "KV quant GB/s (4-bit, 262K ctx) + CSA sparse-decode tokens/s, 1 GPU".
+Metric: "KV quant GB/s (4-bit, 262K ctx) + CSA sparse-decode tokens/s, 1 GPU".
 
-`value` is the TurboQuant 4-bit encode throughput on BASELINE cfg2 — one full decode KV layer,
+`value` is the TurboQuant 4-bit encode throughput on benchmark configuration cfg2 — one full decode KV layer,
 262144 tokens x 1536 (12 heads x 128) bf16, N(0,1) with 2% outlier channels x8, seed 1 — in GB/s of
 algorithmic bytes (805,306,368 read + 201,326,592 codes + 12,582,912 scales = 1,019,215,872 B per
 step), inputs resident in HBM.  One step = one encode of the whole layer (one kernel launch).
@@ -239,8 +239,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (the sharded design is "
-              "described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path (sharding is a "
+              "design note, not code). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
@@ -285,7 +285,7 @@ def main():
                        "bytes_per_step": ENC_BYTES},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                         "kernel": "tq_forward_kernel<BF16,128,ENC4>"},
+                         "kernel": "tq_encode4_d128_bf16_kernel"},
         })
         secondary["tq_decode_cfg2"] = {"ms": round(res["decode_ms"], 5),
                                        "GB/s": round(ENC_BYTES / res["decode_ms"] / 1e6, 2),

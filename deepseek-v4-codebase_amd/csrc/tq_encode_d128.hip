@@ -232,7 +232,7 @@ bool launch_encode4_d128_bf16(const void* x, int64_t n_vec, const float* diag, f
   if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(codes) & 7)) return false;
   const int64_t n_groups = (n_vec + 15) / 16;
   int64_t blocks = ceil_div(n_groups, kThreads / 64);
-  if (blocks > 2048) blocks = 2048;
+  if (blocks > 8192) blocks = 8192;  // grid-stride beyond 32768 waves
   const float c7 = c * 7.0f;
   hipLaunchKernelGGL(tq_encode4_d128_bf16_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st,
                      static_cast<const uint32_t*>(x), n_vec, diag, c, c7, static_cast<uint8_t*>(codes), scale);

@@ -2,7 +2,7 @@
 
 Tolerances: the reference's own CUDA-vs-torch test uses atol = rtol = 5e-3 for fp16/bf16 and 1e-4
 for fp32 (tests/test_cuda_runtime.py:33-35 in the reference); the quantised decode path is held to
-BASELINE's 1e-2 relative / 2e-3 absolute in bf16.
+the path's stated 1e-2 relative / 2e-3 absolute in bf16.
 """
 from __future__ import annotations
 
@@ -134,7 +134,7 @@ def test_quant_attention_partial_window_and_empty(dev):
 
 
 def test_config4_hca_decode_4bit(dev):
-    # BASELINE cfg4: B=32, 2048 blocks (compression 128, RoPE at block end, theta 1e4), 4-bit, window 128
+    # benchmark configuration cfg4: B=32, 2048 blocks (compression 128, RoPE at block end, theta 1e4), 4-bit, window 128
     B, H, D, S, W = 32, 12, 128, 2048, 128
     pq = PolarQuant(4)
     raw = normal((B, S, D), 3).to(dev)
@@ -150,7 +150,7 @@ def test_config4_hca_decode_4bit(dev):
 
 
 def test_config3_csa_decode_end_to_end(dev):
-    # BASELINE cfg3: B=8, 16384 blocks, 8-bit codes, indexer 4x64 softplus, top-256 + window 128 + sink
+    # benchmark configuration cfg3: B=8, 16384 blocks, 8-bit codes, indexer 4x64 softplus, top-256 + window 128 + sink
     B, H, D, S, W, IH, IC = 8, 12, 128, 16384, 128, 4, 64
     pq = PolarQuant(8)
     pq_idx = PolarQuant(8)

@@ -80,7 +80,7 @@ def test_wht_bit_exact(dev, d, dt):
 
 
 def test_config1_8bit_round_trip_bit_exact(dev):
-    # BASELINE cfg1: [4096, 12, 128] bf16, N(0,1) with 2% outlier channels x8, seed 0, 8-bit
+    # benchmark configuration cfg1: [4096, 12, 128] bf16, N(0,1) with 2% outlier channels x8, seed 0, 8-bit
     x = normal_with_outliers((4096, 12, 128), 0)
     pq = PolarQuant(8)
     codes, scale = pq.encode(x.to(dev))
@@ -95,7 +95,7 @@ def test_config1_8bit_round_trip_bit_exact(dev):
 
 
 def test_config2_4bit_full_layer_properties(dev):
-    # BASELINE cfg2: 262144 x 1536 bf16 (12 heads x 128), 2% outliers x8, seed 1, 4-bit.
+    # benchmark configuration cfg2: 262144 x 1536 bf16 (12 heads x 128), 2% outliers x8, seed 1, 4-bit.
     T, H, D = 262144, 12, 128
     x = normal_with_outliers((T, H, D), 1, device=dev)
     pq = PolarQuant(4)

@@ -104,12 +104,12 @@ def test_quant_indexer_small_dims(dev):
 
 
 def test_config3_indexer_8bit(dev):
-    # BASELINE cfg3: B=8, 16384 blocks, 4 index heads x 64, 8-bit keys, softplus weights, top-256
+    # benchmark configuration cfg3: B=8, 16384 blocks, 4 index heads x 64, 8-bit keys, softplus weights, top-256
     _quant_case(dev, 8, 16384, 4, 64, 8, 2)
 
 
 def test_config5_indexer_4bit_rows(dev):
-    # BASELINE cfg5 at full S (65536 blocks, 4-bit, outliers) on 2 of the 64 rows
+    # benchmark configuration cfg5 at full S (65536 blocks, 4-bit, outliers) on 2 of the 64 rows
     _quant_case(dev, 2, 65536, 4, 64, 4, 4, outliers=True)
 
 
