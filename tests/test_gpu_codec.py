@@ -109,15 +109,15 @@ def test_config2_4bit_full_layer_properties(dev):
     sx = lambda v: torch.where(v >= 8, v - 16, v)
     rowmax = torch.maximum(sx(lo).abs().amax(-1), sx(hi).abs().amax(-1))
     assert bool((rowmax == 7).all())                                  # the max element maps to +-7
-    # bit-exact on a sample of rows spread over the whole layer
-    rows = torch.cat([torch.arange(0, 2048), torch.arange(2048, T, 977)]).to(dev)
-    xs = x[rows]
+    # bit-exact over the whole layer (the oracle's OpenMP encode takes well under a second)
     dg = O.diag(42, D)
-    want_c, want_s = O.encode(bf16_bits(xs), "bf16", 4, dg)
-    np.testing.assert_array_equal(codes[rows].cpu().numpy(), want_c)
-    np.testing.assert_array_equal(scale[rows].cpu().numpy(), want_s)
+    want_c, want_s = O.encode(bf16_bits(x), "bf16", 4, dg)
+    np.testing.assert_array_equal(codes.cpu().numpy(), want_c)
+    np.testing.assert_array_equal(scale.cpu().numpy(), want_s)
     rec = pq.decode(codes, scale)
-    np.testing.assert_array_equal(bf16_bits(rec[rows]), O.decode(want_c, want_s, 4, dg, "bf16"))
+    rows = torch.cat([torch.arange(0, 2048), torch.arange(2048, T, 977)]).to(dev)
+    np.testing.assert_array_equal(bf16_bits(rec[rows]), O.decode(want_c[rows.cpu().numpy()], want_s[rows.cpu().numpy()], 4, dg, "bf16"))
+    del want_c, want_s
     # quality: reference 4-bit threshold (cosine > 0.99 on Gaussian rows)
     cos = torch.nn.functional.cosine_similarity(x.float().view(-1, D), rec.float().view(-1, D), dim=-1)
     assert float(cos.mean()) > 0.99
