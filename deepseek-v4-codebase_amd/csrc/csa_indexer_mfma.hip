@@ -1,5 +1,5 @@
 // CSA lightning indexer over TurboQuant-coded index keys on the gfx950 matrix cores, with an
-// exact top-k that needs no atomics.
+// exact radix top-k.
 //
 // Reference: aether_2b/modeling.py:604-616 and aether_2b/serving.py:606-621 (score rules, top-k);
 // the keys are PolarQuant codes (turbo_quant.py:127-211).
@@ -14,24 +14,35 @@
 // over heads across lane groups and multiplied by scale_j.  The only approximation is r (relative
 // ~2^-27 of max|q~_h|) and three fp32 roundings, i.e. fp32-level scores.
 //
-// Selection.  A wave owns 2048 consecutive keys, 32 per lane (slot s, lane l <-> key base+64s+l),
-// as order-preserving uint32 keys (invalid keys = 0, below every finite score).  The k-th largest
-// key T is found by a 32-step binary search whose counts are ballot popcounts; the wave then
-// compacts keys > T and the first (k - #>T) keys == T in index order (ballot + mbcnt), which is the
-// top-k under (score desc, index asc).  A merge kernel repeats this over the candidates of a row
-// (in rounds of 2048 carrying the current best k), and sorts the final k.  Because the order is
-// total, every element of the row's top-k is in its wave's top-k, so the result is exact.
+// Kernels (one stream, in order):
+//   prep   (one workgroup per row)  rotates the query, splits the digits, writes the lanes' A
+//          fragments and combine constants to the workspace, clears the row's histogram.
+//   score  (wide grid)  scores every visible key, stores its order-preserving uint32 key, and
+//          counts keys per bin of the key's top 12 bits (LDS histogram, flushed with atomics).
+//   cand   (wide grid)  finds the bin t1 holding the k-th largest key from the row histogram and
+//          appends every key in bins >= t1 (key, index) to the row's candidate list.
+//   final  (one workgroup per row)  two more radix levels (bits 19..8, 7..0, LDS histograms)
+//          over the candidates give the k-th largest key T; keys > T and the lowest-index keys
+//          == T are taken and placed by rank under (key desc, index asc).  If the bins >= t1
+//          hold more keys than the candidate list can take (many equal keys), the same levels
+//          run over all of the row's stored keys, read in index order.
+// Both routes return the top-k under the total order (score desc, index asc).
+#include <algorithm>
+
 #include "aekv_common.h"
 
 namespace aekv {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kSlots = 32;                    // keys per lane in a wave's selection window
-constexpr int kWaveKeys = 64 * kSlots;        // 2048
-constexpr int kChunkKeys = 4 * kWaveKeys;     // keys per workgroup
+constexpr int kSelThreads = 1024;
+constexpr int kHistBins = 4096;      // top 12 bits of the order key
+constexpr int kCandCap = 4096;       // candidate list per row (fast route)
 constexpr int kMaxMfmaK = 1024;
-constexpr int kMaxLists = 2048;               // wave chunks per row (S <= 4M keys)
+constexpr int kMaxNrb = 4;           // row blocks of 4 heads (IH <= 16)
+constexpr int kMaxKs = 2;            // k-steps of 64 (IC <= 128)
+constexpr int kCandChunk = 8192;     // keys per workgroup of the candidate kernel
+constexpr int64_t kMaxKeys = int64_t(1) << 30;
 
 typedef __attribute__((ext_vector_type(4))) int i32x4_t;
 
@@ -39,65 +50,6 @@ __device__ __forceinline__ float softplus_f32(float x) { return x > 20.0f ? x : 
 
 __device__ __forceinline__ int mbcnt64(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
-}
-
-__device__ __forceinline__ int popc64(uint64_t m) { return __builtin_popcountll(m); }
-
-// k-th largest (k >= 1) of the wave's 64*SLOTS keys (binary search on the value, 32 steps).
-template <int SLOTS>
-__device__ __forceinline__ uint32_t wave_kth(const uint32_t (&key)[SLOTS], int k) {
-  uint32_t T = 0;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t tc = T | (1u << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) cnt += popc64(__builtin_amdgcn_ballot_w64(key[s] >= tc));
-    if (cnt >= k) T = tc;
-  }
-  return T;
-}
-
-// Writes the top-k (k <= #keys > 0) of the wave's keys in index order of (slot, lane), first those
-// > T then those == T; idx(s) gives the lane's element index for slot s.  Returns the count.
-template <int SLOTS, typename IdxFn>
-__device__ __forceinline__ int wave_compact(const uint32_t (&key)[SLOTS], uint32_t T, int k, IdxFn idx,
-                                            uint32_t* out_key, int32_t* out_idx) {
-  int n_gt = 0;
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) n_gt += popc64(__builtin_amdgcn_ballot_w64(key[s] > T));
-  int pos_gt = 0, pos_eq = n_gt;
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) {
-    const uint64_t m_gt = __builtin_amdgcn_ballot_w64(key[s] > T);
-    const uint64_t m_eq = __builtin_amdgcn_ballot_w64(key[s] == T);
-    if (key[s] > T) {
-      const int p = pos_gt + mbcnt64(m_gt);
-      out_key[p] = key[s];
-      out_idx[p] = idx(s);
-    } else if (key[s] == T) {
-      const int p = pos_eq + mbcnt64(m_eq);
-      if (p < k) {
-        out_key[p] = key[s];
-        out_idx[p] = idx(s);
-      }
-    }
-    pos_gt += popc64(m_gt);
-    pos_eq += popc64(m_eq);
-  }
-  return k;
-}
-
-// Top-k of the wave's keys, keys equal to 0 never selected.  Returns the count written.
-template <int SLOTS, typename IdxFn>
-__device__ __forceinline__ int wave_topk(const uint32_t (&key)[SLOTS], int k, IdxFn idx, uint32_t* out_key,
-                                         int32_t* out_idx) {
-  int n_valid = 0;
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) n_valid += popc64(__builtin_amdgcn_ballot_w64(key[s] != 0u));
-  const int kk = min(k, n_valid);
-  if (kk == 0) return 0;
-  const uint32_t T = wave_kth<SLOTS>(key, kk);
-  return wave_compact<SLOTS>(key, T, kk, idx, out_key, out_idx);
 }
 
 struct MfmaIdxArgs {
@@ -108,12 +60,44 @@ struct MfmaIdxArgs {
   const float* diag;     // [IC]
   const int32_t* valid;  // [B] or null
   int64_t S;
-  int IH, k, mode, n_wchunks;  // n_wchunks: 2048-key wave chunks per row
+  int IH, k, mode;
+  int gpw;               // slot groups per wave in the score kernel
   float wscale;
-  uint32_t* cand_key;    // [B, n_wchunks, k]
-  int32_t* cand_idx;     // [B, n_wchunks, k]
-  int32_t* cand_cnt;     // [B, n_wchunks]
+  i32x4_t* frag;         // [B][kMaxNrb][kMaxKs][64]  A fragments per lane
+  float4* fcomb;         // [B][kMaxNrb][64]          digit factors x weight
+  float2* bounds;        // [B][kMaxNrb][64]          relu clamp bounds
+  uint32_t* keys;        // [B][S]                    order keys of visible keys
+  uint32_t* hist;        // [B][kHistBins]
+  uint32_t* cand_cnt;    // [B]
+  uint2* cand;           // [B][kCandCap]             (key, index)
 };
+
+struct WsLayout {
+  size_t frag, fcomb, bounds, keys, hist, cnt, cand, total;
+};
+
+WsLayout layout(int64_t B, int64_t S) {
+  WsLayout l{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += align_up(bytes, 256);
+    return at;
+  };
+  l.frag = take(static_cast<size_t>(B) * kMaxNrb * kMaxKs * 64 * sizeof(i32x4_t));
+  l.fcomb = take(static_cast<size_t>(B) * kMaxNrb * 64 * sizeof(float4));
+  l.bounds = take(static_cast<size_t>(B) * kMaxNrb * 64 * sizeof(float2));
+  l.keys = take(static_cast<size_t>(B) * static_cast<size_t>(S) * 4);
+  l.hist = take(static_cast<size_t>(B) * kHistBins * 4);
+  l.cnt = take(static_cast<size_t>(B) * 4);
+  l.cand = take(static_cast<size_t>(B) * kCandCap * sizeof(uint2));
+  l.total = o;
+  return l;
+}
+
+__device__ __forceinline__ int64_t visible(const MfmaIdxArgs& a, int b) {
+  return a.valid ? min<int64_t>(a.S, max(0, a.valid[b])) : a.S;
+}
 
 // digit position -> index c of the key element for lane group g, byte position p of k-step ks
 template <int BITS>
@@ -128,344 +112,535 @@ __device__ __forceinline__ int cmap(int ks, int g, int p) {
   }
 }
 
-template <int BITS, int IC, int NRB>
-__global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a) {
-  constexpr int KS = IC / 64;          // k-steps of 64
-  constexpr int RB = BITS == 8 ? IC : IC / 2;
-  __shared__ float qs[16 * IC];
-  __shared__ float qs2[16 * IC];
-  __shared__ int8_t dig[4][16][IC];
-  __shared__ float hf[16][4];          // per head: digit factors S * 2^-7d (/16 for 4-bit) * weight
-  __shared__ float hb[16][2];          // per head: clamp bounds
-  // per wave: candidate keys [0, kMaxMfmaK) and indices [kMaxMfmaK, 2 kMaxMfmaK); the whole
-  // 2048-word row also stages the slot keys before the selection
-  __shared__ uint32_t wbuf[4][2 * kMaxMfmaK];
-  static_assert(2 * kMaxMfmaK == kWaveKeys, "slot staging must fill exactly one wave buffer");
+// Threshold search over a histogram: the largest bin t with sum_{u >= t} h[u] >= need, and
+// above = sum_{u > t} h[u] (1 <= need <= sum of all bins).  Thread `tid` of NT owns the PER
+// contiguous bins [PER*tid, PER*tid + PER), loaded as 16-byte vectors (global or LDS).
+template <int PER>
+__device__ __forceinline__ void load_bins(const uint32_t* h, int tid, uint32_t (&v)[PER]) {
+  static_assert(PER % 4 == 0, "bins are loaded 4 at a time");
+  const uint4* p = reinterpret_cast<const uint4*>(h + PER * tid);
+#pragma unroll
+  for (int i = 0; i < PER / 4; ++i) {
+    const uint4 x = p[i];
+    v[4 * i] = x.x;
+    v[4 * i + 1] = x.y;
+    v[4 * i + 2] = x.z;
+    v[4 * i + 3] = x.w;
+  }
+}
 
-  const int b = blockIdx.y;
+// Inclusive suffix sum over the lanes of a wave (lane 63 holds the highest bins).
+__device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_down(x, off, 64);
+    if (lane + off < 64) x += y;
+  }
+  return x;
+}
+
+// The lane whose bins hold the crossing walks them from the top.
+template <int PER>
+__device__ __forceinline__ void walk_bins(const uint32_t (&v)[PER], int tid, uint32_t excl, uint32_t need,
+                                          uint32_t* s_res) {
+  uint32_t c = excl;
+  bool done = false;
+#pragma unroll
+  for (int i = PER - 1; i >= 0; --i) {
+    if (!done && c + v[i] >= need) {
+      s_res[0] = static_cast<uint32_t>(PER * tid + i);
+      s_res[1] = c;
+      done = true;
+    }
+    c += v[i];
+  }
+}
+
+// Block-wide (NT threads, NT * PER bins).  Every thread returns the result.  s_tot holds NT/64
+// words, s_res 2; both may be reused after the call.
+template <int NT, int PER>
+__device__ void block_threshold(const uint32_t* h, uint32_t need, uint32_t* s_tot, uint32_t* s_res, uint32_t& t_out,
+                                uint32_t& above_out) {
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t v[PER];
+  load_bins<PER>(h, tid, v);
+  uint32_t sum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) sum += v[i];
+  const uint32_t suf = wave_suffix_sum(sum);
+  if (lane == 0) s_tot[wv] = suf;
+  __syncthreads();
+  uint32_t higher = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < NW; ++w2) higher += w2 > wv ? s_tot[w2] : 0u;
+  const uint32_t incl = higher + suf, excl = incl - sum;
+  if (excl < need && incl >= need) walk_bins<PER>(v, tid, excl, need, s_res);  // exactly one thread
+  __syncthreads();
+  t_out = s_res[0];
+  above_out = s_res[1];
+  __syncthreads();
+}
+
+// Wave-only variant over 64 * PER bins (called by one whole wave); the result lands in s_res.
+template <int PER>
+__device__ void wave_threshold(const uint32_t* h, uint32_t need, uint32_t* s_res) {
+  const int lane = threadIdx.x & 63;
+  uint32_t v[PER];
+  load_bins<PER>(h, lane, v);
+  uint32_t sum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) sum += v[i];
+  const uint32_t incl = wave_suffix_sum(sum), excl = incl - sum;
+  if (excl < need && incl >= need) walk_bins<PER>(v, lane, excl, need, s_res);
+}
+
+// ---- prep: query rotation, digits, A fragments; clears the row's histogram and count ----------
+template <int BITS, int IC>
+__global__ __launch_bounds__(kThreads) void idx_mfma_prep_kernel(MfmaIdxArgs a) {
+  constexpr int KS = IC / 64;
+  __shared__ int8_t dig[4][16][IC];
+  __shared__ float hf[16][4];  // per head: digit factors S * 2^-7d (/16 for 4-bit) * weight
+  __shared__ float hb[16][2];  // per head: clamp bounds
+  const int b = blockIdx.x;
   const int IH = a.IH;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
-  const int64_t S = a.S;
-  const int64_t nv = a.valid ? min<int64_t>(S, max(0, a.valid[b])) : S;
 
-  // ---- query rotation and digits (once per workgroup) ----
-  for (int i = threadIdx.x; i < 16 * IC; i += kThreads) {
-    const int h = i / IC, c = i % IC;
-    qs[i] = h < IH ? a.q[(static_cast<int64_t>(b) * IH + h) * IC + c] * a.diag[c] : 0.0f;
-  }
-  __syncthreads();
   {
-    float* src = qs;
-    float* dst = qs2;
-    for (int hh = 1; hh < IC; hh <<= 1) {
-      for (int p = threadIdx.x; p < 16 * IC / 2; p += kThreads) {
-        const int head = p / (IC / 2), r = p % (IC / 2);
-        const int i = head * IC + (r / hh) * 2 * hh + (r % hh);
-        const float x = src[i], y = src[i + hh];
-        dst[i] = x + y;
-        dst[i + hh] = x - y;
-      }
-      __syncthreads();
-      float* t = src;
-      src = dst;
-      dst = t;
-    }
-    if (src != qs)
-      for (int i = threadIdx.x; i < 16 * IC; i += kThreads) qs[i] = src[i];
-    __syncthreads();
+    uint4* hz = reinterpret_cast<uint4*>(a.hist + static_cast<int64_t>(b) * kHistBins);
+    for (int i = threadIdx.x; i < kHistBins / 4; i += kThreads) hz[i] = make_uint4(0u, 0u, 0u, 0u);
   }
-  if (wv == 0) {
-    // one wave: per head, step S_h = 2^(e-6) from max|q~_h| = m * 2^e (m in [0.5, 1))
-    for (int h = 0; h < 16; ++h) {
-      float mx = 0.0f;
-      for (int c = lane; c < IC; c += 64) mx = fmaxf(mx, fabsf(qs[h * IC + c] * a.wscale));
-      mx = wave_max(mx);
-      int e = 0;
-      (void)frexpf(mx, &e);
-      const float step = mx > 0.0f ? ldexpf(1.0f, e - 6) : 1.0f;
-      for (int c = lane; c < IC; c += 64) {
-        float r = qs[h * IC + c] * a.wscale;  // q~ = _wht(diag * q)
+  if (threadIdx.x == 0) a.cand_cnt[b] = 0u;
+
+  // wave wv handles heads wv, wv+4, wv+8, wv+12; lane l holds elements l + 64e of the head.
+  // q~ = _wht(diag * q): stages h = 1..32 pair lanes (xor_lane), stage 64 pairs e = 0 and 1.
+  constexpr int EPL = IC / 64;
+  for (int h = wv; h < 16; h += 4) {
+    float v[EPL];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const float sd = ldexpf(step, -7 * d);
-          const float di = rintf(r / sd);  // exact quotient by a power of two
-          r = fmaf(-di, sd, r);            // exact residual
-          dig[d][h][c] = static_cast<int8_t>(di);
+    for (int e = 0; e < EPL; ++e) {
+      const int c = lane + 64 * e;
+      v[e] = h < IH ? a.q[(static_cast<int64_t>(b) * IH + h) * IC + c] * a.diag[c] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float x = v[e];
+      x = fmaf(x, (lane & 1) ? -1.0f : 1.0f, xor_lane<1>(x));    // lower lane: x + p, upper: p - x
+      x = fmaf(x, (lane & 2) ? -1.0f : 1.0f, xor_lane<2>(x));
+      x = fmaf(x, (lane & 4) ? -1.0f : 1.0f, xor_lane<4>(x));
+      x = fmaf(x, (lane & 8) ? -1.0f : 1.0f, xor_lane<8>(x));
+      x = fmaf(x, (lane & 16) ? -1.0f : 1.0f, xor_lane<16>(x));
+      x = fmaf(x, (lane & 32) ? -1.0f : 1.0f, xor_lane<32>(x));
+      v[e] = x;
+    }
+    if constexpr (EPL == 2) {
+      const float x = v[0], y = v[1];
+      v[0] = x + y;
+      v[1] = x - y;
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      v[e] = v[e] * a.wscale;
+      mx = fmaxf(mx, fabsf(v[e]));
+    }
+    mx = wave_max(mx);
+    // step S_h = 2^(e-6) from max|q~_h| = m * 2^e (m in [0.5, 1)); e >= -90 keeps every digit
+    // step and its reciprocal normal
+    int ex = 0;
+    (void)frexpf(mx, &ex);
+    ex = ex < -90 ? -90 : ex;
+    const float step = mx > 0.0f ? ldexpf(1.0f, ex - 6) : 1.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float r = v[e];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const float sd = ldexpf(step, -7 * d);
+        const float di = rintf(r * (1.0f / sd));  // exact: 1/sd is a power of two
+        r = fmaf(-di, sd, r);                      // exact residual
+        dig[d][h][lane + 64 * e] = static_cast<int8_t>(di);
+      }
+    }
+    if (lane == 0) {
+      float wa = 0.0f, lo = -__builtin_inff(), hi = __builtin_inff();
+      if (h < IH) {
+        const float wr = a.w[static_cast<int64_t>(b) * IH + h];
+        if (a.mode == AEKV_IDX_SOFTPLUS) {
+          wa = softplus_f32(wr);
+          lo = 0.0f;
+        } else if (a.mode == AEKV_IDX_RAW) {
+          wa = wr;
+          if (wr >= 0.0f) lo = 0.0f; else hi = 0.0f;  // relu(dot)*w = clamp(dot*w) toward 0
+        } else {
+          wa = fmaxf(wr, 0.0f);                       // relu on the weight only
         }
       }
-      if (lane == 0) {
-        float wa = 0.0f, lo = -__builtin_inff(), hi = __builtin_inff();
-        if (h < IH) {
-          const float wr = a.w[static_cast<int64_t>(b) * IH + h];
-          if (a.mode == AEKV_IDX_SOFTPLUS) {
-            wa = softplus_f32(wr);
-            lo = 0.0f;
-          } else if (a.mode == AEKV_IDX_RAW) {
-            wa = wr;
-            if (wr >= 0.0f) lo = 0.0f; else hi = 0.0f;  // relu(dot)*w = clamp(dot*w) toward 0
-          } else {
-            wa = fmaxf(wr, 0.0f);                       // relu on the weight only
-          }
-        }
-        const float unit = BITS == 4 ? 1.0f / 16.0f : 1.0f;
+      const float unit = BITS == 4 ? 1.0f / 16.0f : 1.0f;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) hf[h][d] = ldexpf(step, -7 * d) * unit * wa;
-        hb[h][0] = lo;
-        hb[h][1] = hi;
-      }
+      for (int d = 0; d < 4; ++d) hf[h][d] = ldexpf(step, -7 * d) * unit * wa;
+      hb[h][0] = lo;
+      hb[h][1] = hi;
     }
   }
   __syncthreads();
 
-  // A operands (digits) and combine constants for this lane
+  // wave wv writes row block rb = wv (heads 4rb..4rb+3): A rows = 4 heads x 4 digits
+  const int rb = wv;
+  const int row = lane & 15;
+  const int h = 4 * rb + (row >> 2), d = row & 3;
+  const int64_t fb = static_cast<int64_t>(b) * kMaxNrb + rb;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    i32x4_t A;
+#pragma unroll
+    for (int dw = 0; dw < 4; ++dw) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int by = 0; by < 4; ++by) {
+        const int c = cmap<BITS>(ks, g, 4 * dw + by);
+        word |= (static_cast<uint32_t>(static_cast<uint8_t>(dig[d][h][c])) << (8 * by));
+      }
+      A[dw] = static_cast<int>(word);
+    }
+    a.frag[(fb * kMaxKs + ks) * 64 + lane] = A;
+  }
+  const int ho = 4 * rb + g;  // output rows 4g..4g+3 = head 4rb+g, digits 0..3
+  a.fcomb[fb * 64 + lane] = make_float4(hf[ho][0], hf[ho][1], hf[ho][2], hf[ho][3]);
+  a.bounds[fb * 64 + lane] = make_float2(hb[ho][0], hb[ho][1]);
+}
+
+// ---- score: keys -> order keys + histogram of their top 12 bits --------------------------------
+// A wave scores groups of SPW slots of 64 keys; lane l keeps key base + 64s + l of slot s.  All
+// loads of a group are issued before its matrix work.
+template <int BITS, int IC, int NRB>
+__global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a) {
+  constexpr int KS = IC / 64;
+  constexpr int RB = BITS == 8 ? IC : IC / 2;        // code bytes per key
+  constexpr int SPW = RB <= 32 ? 4 : (RB <= 64 ? 2 : 1);
+  constexpr int LW = BITS == 8 ? 4 : 2;               // dwords per lane per k-step
+  __shared__ uint32_t hist[kHistBins];
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
+  const int64_t S = a.S;
+  const int64_t nv = visible(a, b);
+
+  for (int i = threadIdx.x; i < kHistBins; i += kThreads) hist[i] = 0u;
   i32x4_t A[NRB][KS];
   float f[NRB][4], lo[NRB], hi[NRB];
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb) {
-    const int row = lane & 15;
-    const int h = 4 * rb + (row >> 2), d = row & 3;
+    const int64_t fb = static_cast<int64_t>(b) * kMaxNrb + rb;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-      for (int dw = 0; dw < 4; ++dw) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int by = 0; by < 4; ++by) {
-          const int c = cmap<BITS>(ks, g, 4 * dw + by);
-          word |= (static_cast<uint32_t>(static_cast<uint8_t>(dig[d][h][c])) << (8 * by));
-        }
-        A[rb][ks][dw] = static_cast<int>(word);
-      }
-    }
-    const int ho = 4 * rb + g;  // output rows 4g..4g+3 = head 4rb+g, digits 0..3
-#pragma unroll
-    for (int d2 = 0; d2 < 4; ++d2) f[rb][d2] = hf[ho][d2];
-    lo[rb] = hb[ho][0];
-    hi[rb] = hb[ho][1];
+    for (int ks = 0; ks < KS; ++ks) A[rb][ks] = a.frag[(fb * kMaxKs + ks) * 64 + lane];
+    const float4 fc = a.fcomb[fb * 64 + lane];
+    f[rb][0] = fc.x;
+    f[rb][1] = fc.y;
+    f[rb][2] = fc.z;
+    f[rb][3] = fc.w;
+    const float2 bd = a.bounds[fb * 64 + lane];
+    lo[rb] = bd.x;
+    hi[rb] = bd.y;
   }
+  __syncthreads();
 
-  // ---- scoring: this wave's 2048 keys ----
-  const int64_t kb = static_cast<int64_t>(blockIdx.x) * kChunkKeys + static_cast<int64_t>(wv) * kWaveKeys;
   const uint8_t* crow = a.codes + static_cast<int64_t>(b) * S * RB;
   const float* srow = a.kscale + static_cast<int64_t>(b) * S;
-  // slot keys are staged in this wave's candidate buffer (ck/ci as one 2048-word array) and read
-  // back into registers before the selection overwrites it
-  uint32_t* sk = &wbuf[wv][0];
-  uint32_t* ck = &wbuf[wv][0];
-  int32_t* ci = reinterpret_cast<int32_t*>(&wbuf[wv][kMaxMfmaK]);
+  uint32_t* krow = a.keys + static_cast<int64_t>(b) * S;
+  constexpr int64_t kGroupKeys = SPW * 64;
+  const int64_t wave_base = (static_cast<int64_t>(blockIdx.x) * 4 + wv) * a.gpw * kGroupKeys;
 #pragma unroll 1
-  for (int s = 0; s < kSlots; ++s) {
-    uint32_t kq[4];
+  for (int gi = 0; gi < a.gpw; ++gi) {
+    const int64_t kb = wave_base + gi * kGroupKeys;
+    if (kb >= nv) break;  // wave-uniform
+    uint32_t raw[SPW][4][KS][LW];
+    float scl[SPW];
 #pragma unroll
-    for (int tq = 0; tq < 4; ++tq) {
-      const int64_t j = kb + 64 * s + 16 * tq + (lane & 15);
-      const bool okj = j < nv;
-      const int64_t jr = okj ? j : 0;
-      i32x4_t acc[NRB];
+    for (int s = 0; s < SPW; ++s) {
 #pragma unroll
-      for (int rb = 0; rb < NRB; ++rb) acc[rb] = i32x4_t{0, 0, 0, 0};
+      for (int tq = 0; tq < 4; ++tq) {
+        const int64_t j = kb + 64 * s + 16 * tq + (lane & 15);
+        const int64_t jr = j < nv ? j : 0;  // nv >= 1 here; rows past nv are scored and dropped
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        i32x4_t B;
-        if constexpr (BITS == 8) {
-          const uint4 v = okj ? *reinterpret_cast<const uint4*>(crow + jr * RB + 64 * ks + 16 * g) : make_uint4(0, 0, 0, 0);
-          B = i32x4_t{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
-        } else {
-          const uint2 v = okj ? *reinterpret_cast<const uint2*>(crow + jr * RB + 32 * ks + 8 * g) : make_uint2(0, 0);
-          B = i32x4_t{static_cast<int>((v.x << 4) & 0xF0F0F0F0u), static_cast<int>(v.x & 0xF0F0F0F0u),
-                      static_cast<int>((v.y << 4) & 0xF0F0F0F0u), static_cast<int>(v.y & 0xF0F0F0F0u)};
+        for (int ks = 0; ks < KS; ++ks) {
+          if constexpr (BITS == 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(crow + jr * RB + 64 * ks + 16 * g);
+            raw[s][tq][ks][0] = v.x;
+            raw[s][tq][ks][1] = v.y;
+            raw[s][tq][ks][2] = v.z;
+            raw[s][tq][ks][3] = v.w;
+          } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(crow + jr * RB + 32 * ks + 8 * g);
+            raw[s][tq][ks][0] = v.x;
+            raw[s][tq][ks][1] = v.y;
+          }
         }
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb][ks], B, acc[rb], 0, 0, 0);
       }
-      float t = 0.0f;
-#pragma unroll
-      for (int rb = 0; rb < NRB; ++rb) {
-        float v = static_cast<float>(acc[rb][0]) * f[rb][0];
-        v = fmaf(static_cast<float>(acc[rb][1]), f[rb][1], v);
-        v = fmaf(static_cast<float>(acc[rb][2]), f[rb][2], v);
-        v = fmaf(static_cast<float>(acc[rb][3]), f[rb][3], v);
-        t += __builtin_amdgcn_fmed3f(v, lo[rb], hi[rb]);
-      }
-      t += xor_lane<16>(t);  // sum over the four head groups
-      t += xor_lane<32>(t);
-      const float sc = t * srow[jr];
-      kq[tq] = okj ? order_key(sc) : 0u;
+      const int64_t jo = kb + 64 * s + lane;
+      scl[s] = srow[jo < nv ? jo : 0];
     }
-    const uint32_t mine = g == 0 ? kq[0] : (g == 1 ? kq[1] : (g == 2 ? kq[2] : kq[3]));
-    sk[64 * s + lane] = mine;  // slot s of lane l at 64s + l
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      float tq_t[4];
+#pragma unroll
+      for (int tq = 0; tq < 4; ++tq) {
+        i32x4_t acc[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) acc[rb] = i32x4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          i32x4_t Bop;
+          if constexpr (BITS == 8) {
+            Bop = i32x4_t{static_cast<int>(raw[s][tq][ks][0]), static_cast<int>(raw[s][tq][ks][1]),
+                          static_cast<int>(raw[s][tq][ks][2]), static_cast<int>(raw[s][tq][ks][3])};
+          } else {
+            const uint32_t x = raw[s][tq][ks][0], y = raw[s][tq][ks][1];
+            Bop = i32x4_t{static_cast<int>((x << 4) & 0xF0F0F0F0u), static_cast<int>(x & 0xF0F0F0F0u),
+                          static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
+          }
+#pragma unroll
+          for (int rb = 0; rb < NRB; ++rb) acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb][ks], Bop, acc[rb], 0, 0, 0);
+        }
+        float t = 0.0f;
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+          float v = static_cast<float>(acc[rb][0]) * f[rb][0];
+          v = fmaf(static_cast<float>(acc[rb][1]), f[rb][1], v);
+          v = fmaf(static_cast<float>(acc[rb][2]), f[rb][2], v);
+          v = fmaf(static_cast<float>(acc[rb][3]), f[rb][3], v);
+          t += __builtin_amdgcn_fmed3f(v, lo[rb], hi[rb]);
+        }
+        t += xor_lane<16>(t);  // sum over the four head groups
+        t += xor_lane<32>(t);
+        tq_t[tq] = t;
+      }
+      // lane l keeps key kb + 64s + l, i.e. tq = l / 16
+      const float mine = g == 0 ? tq_t[0] : (g == 1 ? tq_t[1] : (g == 2 ? tq_t[2] : tq_t[3]));
+      const int64_t jo = kb + 64 * s + lane;
+      if (jo < nv) {
+        const uint32_t key = order_key(mine * scl[s]);
+        krow[jo] = key;
+        atomicAdd(&hist[key >> 20], 1u);
+      }
+    }
   }
-  __builtin_amdgcn_wave_barrier();
-  uint32_t key[kSlots];
-#pragma unroll
-  for (int s = 0; s < kSlots; ++s) key[s] = sk[64 * s + lane];
-  __builtin_amdgcn_wave_barrier();
-
-  // ---- per-wave exact top-k ----
-  const int cnt = wave_topk<kSlots>(key, a.k, [&](int s) { return static_cast<int32_t>(kb + 64 * s + lane); }, ck, ci);
-  __builtin_amdgcn_wave_barrier();
-  const int64_t wchunk = static_cast<int64_t>(blockIdx.x) * 4 + wv;
-  if (wchunk < a.n_wchunks) {
-    const int64_t base = (static_cast<int64_t>(b) * a.n_wchunks + wchunk) * a.k;
-    for (int i = lane; i < cnt; i += 64) {
-      a.cand_key[base + i] = ck[i];
-      a.cand_idx[base + i] = ci[i];
-    }
-    if (lane == 0) a.cand_cnt[static_cast<int64_t>(b) * a.n_wchunks + wchunk] = cnt;
+  __syncthreads();
+  uint32_t* gh = a.hist + static_cast<int64_t>(b) * kHistBins;
+  for (int i = threadIdx.x; i < kHistBins; i += kThreads) {
+    const uint32_t c = hist[i];
+    if (c) atomicAdd(&gh[i], c);
   }
 }
 
-// Merges the candidates get(e), e in [0, n), into the wave's held best (hk/hi, `held` entries) in
-// rounds: the slots hold the current best followed by as many new candidates as fit.  Candidate
-// order is index order for equal keys, so the result is the top-k under (key desc, index asc).
-// Needs k <= kMaxMfmaK (< kWaveKeys) so every round consumes new candidates.
-template <typename Get>
-__device__ int wave_merge_rounds(int held, int n, int k, Get get, uint32_t* hk, int32_t* hi, uint32_t* stk,
-                                 int32_t* sti) {
-  const int lane = threadIdx.x & 63;
-  int pos = 0;
-  while (pos < n) {
-    const int take = min(n - pos, kWaveKeys - held);
-    // stage the round in LDS: [0, held) current best, [held, held + take) new, rest empty
-#pragma unroll 1
-    for (int e = lane; e < kWaveKeys; e += 64) {
-      uint32_t kv = 0u;
-      int32_t iv = 0;
-      if (e < held) {
-        kv = hk[e];
-        iv = hi[e];
-      } else if (e < held + take) {
-        get(pos + e - held, kv, iv);
-      }
-      stk[e] = kv;
-      sti[e] = iv;
-    }
-    __builtin_amdgcn_wave_barrier();
-    uint32_t key[kSlots];
-    int32_t idx[kSlots];
-#pragma unroll
-    for (int s = 0; s < kSlots; ++s) {
-      key[s] = stk[64 * s + lane];
-      idx[s] = sti[64 * s + lane];
-    }
-    __builtin_amdgcn_wave_barrier();  // every lane has read the round before hk/hi are overwritten
-    held = wave_topk<kSlots>(key, k, [&](int s) { return idx[s]; }, hk, hi);
-    __builtin_amdgcn_wave_barrier();
-    pos += take;
-  }
-  return held;
-}
-
-// Row merge: top-k of the row's candidates (n_wchunks lists of <= k each) -> sorted int64 indices.
-__global__ __launch_bounds__(kThreads) void idx_mfma_merge_kernel(const uint32_t* __restrict__ cand_key,
-                                                                  const int32_t* __restrict__ cand_idx,
-                                                                  const int32_t* __restrict__ cand_cnt, int n_wchunks,
-                                                                  int k, int64_t* __restrict__ out_idx,
-                                                                  float* __restrict__ out_score) {
-  __shared__ uint32_t hk[4][kMaxMfmaK];
-  __shared__ int32_t hi[4][kMaxMfmaK];
-  __shared__ uint32_t fk[kMaxMfmaK];
-  __shared__ int32_t fi[kMaxMfmaK];
-  __shared__ int held_w[4];
-  __shared__ int pref[kMaxLists + 1];
-  __shared__ uint64_t srt[kMaxMfmaK];
-  __shared__ uint32_t stk[4][kWaveKeys];
-  __shared__ int32_t sti[4][kWaveKeys];
-  const int b = blockIdx.x;
+// ---- cand: keys in bins >= t1 -> the row's candidate list ----------------------------------------
+// Each wave reads its 2048 keys (8 steps of 4 coalesced 64-key loads) before reserving its slots
+// with one atomic.
+__global__ __launch_bounds__(kThreads) void idx_mfma_cand_kernel(MfmaIdxArgs a) {
+  constexpr int kWaveSpan = kCandChunk / 4;
+  constexpr int kSteps = kWaveSpan / 256;
+  __shared__ uint32_t s_tot[kThreads / 64];
+  __shared__ uint32_t s_res[2];
+  const int b = blockIdx.y;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint32_t* ckr = cand_key + static_cast<int64_t>(b) * n_wchunks * k;
-  const int32_t* cir = cand_idx + static_cast<int64_t>(b) * n_wchunks * k;
-  const int32_t* ccr = cand_cnt + static_cast<int64_t>(b) * n_wchunks;
-
-  // prefix of list counts (exclusive), computed by one wave in blocks of 64
-  if (wv == 0) {
-    int run = 0;
-    for (int l0 = 0; l0 < n_wchunks; l0 += 64) {
-      const int l = l0 + lane;
-      const int c = l < n_wchunks ? ccr[l] : 0;
-      int incl = c;
-      for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += y;
+  const int64_t nv = visible(a, b);
+  const uint32_t kk = static_cast<uint32_t>(min<int64_t>(a.k, nv));
+  const int64_t j0 = static_cast<int64_t>(blockIdx.x) * kCandChunk;
+  if (kk == 0 || j0 >= nv) return;  // workgroup-uniform
+  const uint32_t* gh = a.hist + static_cast<int64_t>(b) * kHistBins;
+  uint32_t t1, above;
+  block_threshold<kThreads, kHistBins / kThreads>(gh, kk, s_tot, s_res, t1, above);
+  if (above + gh[t1] > static_cast<uint32_t>(kCandCap)) return;  // the final kernel selects from all keys
+  const uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.S;
+  uint2* crow = a.cand + static_cast<int64_t>(b) * kCandCap;
+  const int64_t j1 = min<int64_t>(nv, j0 + kCandChunk);
+  const int64_t wb = j0 + static_cast<int64_t>(wv) * kWaveSpan;
+  uint32_t key[kSteps][4];
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t j = wb + 256 * st + 64 * u + lane;
+      key[st][u] = j < j1 ? krow[j] : 0u;
+    }
+  int n = 0;
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t j = wb + 256 * st + 64 * u + lane;
+      n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(j < j1 && (key[st][u] >> 20) >= t1));
+    }
+  if (n == 0) return;  // wave-uniform, no barrier follows
+  uint32_t run = 0;
+  if (lane == 0) run = atomicAdd(&a.cand_cnt[b], static_cast<uint32_t>(n));
+  run = __builtin_amdgcn_readfirstlane(run);
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t j = wb + 256 * st + 64 * u + lane;
+      const bool take = j < j1 && (key[st][u] >> 20) >= t1;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(take);
+      if (take) {
+        const uint32_t p = run + static_cast<uint32_t>(mbcnt64(m));
+        if (p < static_cast<uint32_t>(kCandCap)) crow[p] = make_uint2(key[st][u], static_cast<uint32_t>(j));
       }
-      if (l < n_wchunks) pref[l] = run + incl - c;
-      run += __shfl(incl, 63, 64);
+      run += static_cast<uint32_t>(__builtin_popcountll(m));
     }
-    if (lane == 0) pref[n_wchunks] = run;
+}
+
+// ---- final: exact top-k of a row, sorted ------------------------------------------------------
+__device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
+  // ascending order of (~key, idx) == key descending, index ascending
+  return (static_cast<uint64_t>(~key) << 32) | idx;
+}
+
+// Radix levels 2 and 3 (bits 19..8, then 7..0) below the level-1 bin t1 narrow the threshold to
+// the k-th largest key T; the row's keys > T are taken with the lowest-index keys == T, and the
+// kk selected words are placed by rank.  Fast route: the keys are the candidates (every key in
+// bins >= t1, in LDS); exact route: all visible keys of the row, read in index order.
+__global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs a, int64_t* __restrict__ out_idx,
+                                                                     float* __restrict__ out_score) {
+  constexpr int NW = kSelThreads / 64;
+  __shared__ uint32_t ck[kCandCap];
+  __shared__ uint32_t ci[kCandCap];
+  __shared__ __align__(16) uint32_t h[kHistBins];
+  __shared__ uint64_t sel[kMaxMfmaK];
+  __shared__ uint32_t s_tot[NW], s_res[2], s_cnt[2], s_wave_eq[NW];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t nv = visible(a, b);
+  const int k = a.k;
+  const uint32_t kk = static_cast<uint32_t>(min<int64_t>(k, nv));
+  int64_t* orow = out_idx + static_cast<int64_t>(b) * k;
+  float* srow = out_score ? out_score + static_cast<int64_t>(b) * k : nullptr;
+  for (int i = static_cast<int>(kk) + tid; i < k; i += kSelThreads) {
+    orow[i] = -1;
+    if (srow) srow[i] = -__builtin_inff();
+  }
+  if (kk == 0) return;
+  const uint32_t* gh = a.hist + static_cast<int64_t>(b) * kHistBins;
+  uint32_t t1, above1;
+  block_threshold<kSelThreads, kHistBins / kSelThreads>(gh, kk, s_tot, s_res, t1, above1);
+  const bool fast = above1 + gh[t1] <= static_cast<uint32_t>(kCandCap);
+  const uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.S;
+  int n = 0;
+  if (fast) {
+    n = static_cast<int>(min<uint32_t>(a.cand_cnt[b], kCandCap));
+    const uint2* crow = a.cand + static_cast<int64_t>(b) * kCandCap;
+    for (int i = tid; i < n; i += kSelThreads) {
+      const uint2 c = crow[i];
+      ck[i] = c.x;
+      ci[i] = c.y;
+    }
+  }
+  uint32_t need = kk - above1;  // >= 1 keys still to take at or below bin t1
+  uint32_t prefix = t1;
+  int shift = 20;
+#pragma unroll 1
+  for (int lvl = 0; lvl < 2; ++lvl) {
+    const int wbits = lvl == 0 ? 12 : 8;
+    const int nb = 1 << wbits;
+    const int nshift = shift - wbits;
+    const uint32_t mask = static_cast<uint32_t>(nb - 1);
+    for (int i = tid; i < nb; i += kSelThreads) h[i] = 0u;
+    __syncthreads();
+    if (fast) {
+      for (int i = tid; i < n; i += kSelThreads) {
+        const uint32_t key = ck[i];
+        if ((key >> shift) == prefix) atomicAdd(&h[(key >> nshift) & mask], 1u);
+      }
+    } else {
+      for (int64_t j = tid; j < nv; j += kSelThreads) {
+        const uint32_t key = krow[j];
+        if ((key >> shift) == prefix) atomicAdd(&h[(key >> nshift) & mask], 1u);
+      }
+    }
+    __syncthreads();
+    uint32_t t, ab;
+    if (lvl == 0) {
+      block_threshold<kSelThreads, kHistBins / kSelThreads>(h, need, s_tot, s_res, t, ab);
+    } else {
+      if (wv == 0) wave_threshold<4>(h, need, s_res);  // 256 bins
+      __syncthreads();
+      t = s_res[0];
+      ab = s_res[1];
+    }
+    need -= ab;
+    prefix = (prefix << wbits) | t;
+    shift = nshift;
+  }
+  const uint32_t T = prefix;          // the k-th largest key
+  const uint32_t n_eq = h[T & 0xFFu]; // keys == T
+  const uint32_t n_gt = kk - need;    // keys > T; `need` keys == T are taken, lowest index first
+  if (tid == 0) {
+    s_cnt[0] = 0u;
+    s_cnt[1] = 0u;
   }
   __syncthreads();
-
-  // stage 1: wave wv reduces lists [l_lo, l_hi) to its best k
-  const int per = (n_wchunks + 3) / 4;
-  const int l_lo = min(n_wchunks, wv * per), l_hi = min(n_wchunks, l_lo + per);
-  const int p_lo = pref[l_lo], p_hi = pref[l_hi];
-  auto get1 = [&](int e, uint32_t& key, int32_t& idx) {
-    const int P = p_lo + e;
-    int lo = l_lo, hi2 = l_hi - 1;  // last list with pref <= P
-    while (lo < hi2) {
-      const int mid = (lo + hi2 + 1) >> 1;
-      if (pref[mid] <= P) lo = mid; else hi2 = mid - 1;
-    }
-    const int64_t src = static_cast<int64_t>(lo) * k + (P - pref[lo]);
-    key = ckr[src];
-    idx = cir[src];
-  };
-  const int h1 = wave_merge_rounds(0, p_hi - p_lo, k, get1, hk[wv], hi[wv], stk[wv], sti[wv]);
-  if (lane == 0) held_w[wv] = h1;
-  __syncthreads();
-
-  // stage 2: wave 0 merges the four lists (in wave order = index order)
-  if (wv == 0) {
-    const int c0 = held_w[0], c1 = held_w[1], c2 = held_w[2], c3 = held_w[3];
-    auto get2 = [&](int e, uint32_t& key, int32_t& idx) {
-      int w = 0, off = e;
-      if (off >= c0) { off -= c0; w = 1;
-        if (off >= c1) { off -= c1; w = 2;
-          if (off >= c2) { off -= c2; w = 3; } } }
-      key = hk[w][off];
-      idx = hi[w][off];
-    };
-    const int h2 = wave_merge_rounds(0, c0 + c1 + c2 + c3, k, get2, fk, fi, stk[0], sti[0]);
-    if (lane == 0) held_w[0] = h2;
-  }
-  __syncthreads();
-  const int cnt = held_w[0];
-
-  // bitonic sort of (~key, idx) ascending == key desc, idx asc
-  int P = 1;
-  while (P < k) P <<= 1;
-  for (int i = threadIdx.x; i < P; i += kThreads)
-    srt[i] = i < cnt ? (static_cast<uint64_t>(~fk[i]) << 32) | static_cast<uint32_t>(fi[i]) : ~0ull;
-  __syncthreads();
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < P / 2; i += kThreads) {
-        const int pos = 2 * i - (i & (stride - 1));
-        const int partner = pos + stride;
-        const bool up = (pos & size) == 0;
-        const uint64_t x = srt[pos], y = srt[partner];
-        if ((x > y) == up) {
-          srt[pos] = y;
-          srt[partner] = x;
+  if (fast) {
+    const bool all_eq = n_eq == need;
+    for (int i = tid; i < n; i += kSelThreads) {
+      const uint32_t key = ck[i], idx = ci[i];
+      if (key > T) {
+        const uint32_t p = atomicAdd(&s_cnt[0], 1u);
+        if (p < n_gt) sel[p] = sort_word(key, idx);
+      } else if (key == T) {
+        if (all_eq) {
+          const uint32_t p = atomicAdd(&s_cnt[1], 1u);
+          if (p < need) sel[n_gt + p] = sort_word(key, idx);
+        } else {  // ties at T: rank among the equal keys by index
+          uint32_t r = 0;
+          for (int j = 0; j < n; ++j) r += (ck[j] == T && ci[j] < idx) ? 1u : 0u;
+          if (r < need) sel[n_gt + r] = sort_word(key, idx);
         }
       }
+    }
+  } else {
+    uint32_t eq_run = 0;
+    for (int64_t base = 0; base < nv; base += kSelThreads) {
+      const int64_t j = base + tid;
+      const uint32_t key = j < nv ? krow[j] : 0u;
+      const bool gt = j < nv && key > T;
+      const bool eq = j < nv && key == T;
+      if (gt) {
+        const uint32_t p = atomicAdd(&s_cnt[0], 1u);
+        if (p < n_gt) sel[p] = sort_word(key, static_cast<uint32_t>(j));
+      }
+      const uint64_t m = __builtin_amdgcn_ballot_w64(eq);
+      if (lane == 0) s_wave_eq[wv] = static_cast<uint32_t>(__builtin_popcountll(m));
+      __syncthreads();
+      uint32_t before = 0, total = 0;
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) {
+        const uint32_t c = s_wave_eq[w2];
+        before += w2 < wv ? c : 0u;
+        total += c;
+      }
+      if (eq) {
+        const uint32_t r = eq_run + before + static_cast<uint32_t>(mbcnt64(m));
+        if (r < need) sel[n_gt + r] = sort_word(key, static_cast<uint32_t>(j));
+      }
+      eq_run += total;
       __syncthreads();
     }
   }
-  for (int i = threadIdx.x; i < k; i += kThreads) {
-    const bool ok = i < cnt;
-    const uint64_t v = srt[i];
-    out_idx[static_cast<int64_t>(b) * k + i] = ok ? static_cast<int64_t>(static_cast<uint32_t>(v & 0xffffffffu)) : -1;
-    if (out_score)
-      out_score[static_cast<int64_t>(b) * k + i] =
-          ok ? order_key_inv(~static_cast<uint32_t>(v >> 32)) : -__builtin_inff();
+  __syncthreads();
+  // the kk words are distinct: each one's output position is its rank
+  for (int i = tid; i < static_cast<int>(kk); i += kSelThreads) {
+    const uint64_t w = sel[i];
+    uint32_t r = 0;
+    for (int j = 0; j < static_cast<int>(kk); ++j) r += sel[j] < w ? 1u : 0u;
+    orow[r] = static_cast<int64_t>(static_cast<uint32_t>(w & 0xffffffffu));
+    if (srow) srow[r] = order_key_inv(~static_cast<uint32_t>(w >> 32));
   }
 }
 
-typedef void (*score_fn)(MfmaIdxArgs);
+typedef void (*kern_fn)(MfmaIdxArgs);
 
 template <int BITS, int IC>
-score_fn pick_nrb(int nrb) {
+kern_fn pick_score(int nrb) {
   switch (nrb) {
     case 1: return idx_mfma_score_kernel<BITS, IC, 1>;
     case 2: return idx_mfma_score_kernel<BITS, IC, 2>;
@@ -478,15 +653,14 @@ score_fn pick_nrb(int nrb) {
 }  // namespace
 
 size_t mfma_indexer_workspace(int64_t B, int64_t S, int32_t k) {
-  const int64_t n_wchunks = S > 0 ? ceil_div(S, kWaveKeys) : 1;
-  const size_t nc = static_cast<size_t>(B * n_wchunks * k);
-  return align_up(nc * 4, 256) * 2 + align_up(static_cast<size_t>(B * n_wchunks) * 4, 256);
+  (void)k;
+  return layout(B, S).total;
 }
 
 bool mfma_indexer_supported(int IH, int IC, int k, int64_t S) {
-  // S >= 1: the score loop reads the scale of key 0 for out-of-range lanes.
-  return IH >= 1 && IH <= 16 && (IC == 64 || IC == 128) && k <= kMaxMfmaK && S >= 1 &&
-         S <= static_cast<int64_t>(kMaxLists) * kWaveKeys;
+  // S >= 1: out-of-range lanes of the score loop read key 0's codes and scale.
+  return IH >= 1 && IH <= 4 * kMaxNrb && (IC == 64 || IC == 128) && k >= 1 && k <= kMaxMfmaK && S >= 1 &&
+         S <= kMaxKeys;
 }
 
 int launch_mfma_indexer(const float* q, const float* w, const void* codes, const float* kscale, const float* diag,
@@ -503,22 +677,48 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
   a.IH = IH;
   a.k = k;
   a.mode = mode;
-  a.n_wchunks = static_cast<int>(S > 0 ? ceil_div(S, kWaveKeys) : 1);
   a.wscale = wht_scale(IC);
-  const size_t nc = static_cast<size_t>(B * a.n_wchunks * k);
-  a.cand_key = static_cast<uint32_t*>(ws);
-  a.cand_idx = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + align_up(nc * 4, 256));
-  a.cand_cnt = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + 2 * align_up(nc * 4, 256));
+  const WsLayout l = layout(B, S);
+  char* base = static_cast<char*>(ws);
+  a.frag = reinterpret_cast<i32x4_t*>(base + l.frag);
+  a.fcomb = reinterpret_cast<float4*>(base + l.fcomb);
+  a.bounds = reinterpret_cast<float2*>(base + l.bounds);
+  a.keys = reinterpret_cast<uint32_t*>(base + l.keys);
+  a.hist = reinterpret_cast<uint32_t*>(base + l.hist);
+  a.cand_cnt = reinterpret_cast<uint32_t*>(base + l.cnt);
+  a.cand = reinterpret_cast<uint2*>(base + l.cand);
+
   const int nrb = (IH + 3) / 4;
-  score_fn fn = nullptr;
-  if (bits == 8) fn = IC == 64 ? pick_nrb<8, 64>(nrb) : pick_nrb<8, 128>(nrb);
-  else fn = IC == 64 ? pick_nrb<4, 64>(nrb) : pick_nrb<4, 128>(nrb);
-  if (!fn) return fail(AEKV_ERR_UNSUPPORTED, "%s: no matrix-core indexer for IH=%d IC=%d", who, IH, IC);
-  const int n_wg = static_cast<int>(S > 0 ? ceil_div(S, kChunkKeys) : 1);
-  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(n_wg), static_cast<uint32_t>(B)), dim3(kThreads), 0, st, a);
+  kern_fn prep = nullptr, score = nullptr;
+  if (bits == 8) {
+    prep = IC == 64 ? idx_mfma_prep_kernel<8, 64> : idx_mfma_prep_kernel<8, 128>;
+    score = IC == 64 ? pick_score<8, 64>(nrb) : pick_score<8, 128>(nrb);
+  } else {
+    prep = IC == 64 ? idx_mfma_prep_kernel<4, 64> : idx_mfma_prep_kernel<4, 128>;
+    score = IC == 64 ? pick_score<4, 64>(nrb) : pick_score<4, 128>(nrb);
+  }
+  if (!score) return fail(AEKV_ERR_UNSUPPORTED, "%s: no matrix-core indexer for IH=%d IC=%d", who, IH, IC);
+  // slot-group size of the score kernel (must match SPW there) and groups per wave: enough
+  // workgroups to fill the chip (~2048), at most 16 groups per wave
+  const int rb_bytes = bits == 8 ? IC : IC / 2;
+  const int64_t group_keys = 64 * (rb_bytes <= 32 ? 4 : (rb_bytes <= 64 ? 2 : 1));
+  const int64_t groups_per_row = ceil_div(S, group_keys);
+  int64_t gpw = (B * groups_per_row) / (4 * 2048);
+  gpw = std::min<int64_t>(16, std::max<int64_t>(1, gpw));
+  a.gpw = static_cast<int>(gpw);
+  const int64_t n_score = ceil_div(groups_per_row, 4 * gpw);
+  const int64_t n_cand = ceil_div(S, kCandChunk);
+  if (B > 65535 || n_score > 0x7fffffff || n_cand > 0x7fffffff)
+    return fail(AEKV_ERR_UNSUPPORTED, "%s: B=%lld S=%lld exceed the launch grid", who, static_cast<long long>(B),
+                static_cast<long long>(S));
+  const uint32_t by = static_cast<uint32_t>(B);
+  hipLaunchKernelGGL(prep, dim3(by), dim3(kThreads), 0, st, a);
   if (int rc = check_launch(who)) return rc;
-  hipLaunchKernelGGL(idx_mfma_merge_kernel, dim3(static_cast<uint32_t>(B)), dim3(kThreads), 0, st, a.cand_key,
-                     a.cand_idx, a.cand_cnt, a.n_wchunks, k, out_idx, out_score);
+  hipLaunchKernelGGL(score, dim3(static_cast<uint32_t>(n_score), by), dim3(kThreads), 0, st, a);
+  if (int rc = check_launch(who)) return rc;
+  hipLaunchKernelGGL(idx_mfma_cand_kernel, dim3(static_cast<uint32_t>(n_cand), by), dim3(kThreads), 0, st, a);
+  if (int rc = check_launch(who)) return rc;
+  hipLaunchKernelGGL(idx_mfma_final_kernel, dim3(by), dim3(kSelThreads), 0, st, a, out_idx, out_score);
   return check_launch(who);
 }
 

@@ -131,3 +131,35 @@ def indexer_path(request):
 ])
 def test_quant_indexer_shapes_both_paths(dev, indexer_path, B, S, IH, IC, bits, k, valid, mode):
     _quant_case(dev, B, S, IH, IC, bits, 50 + S % 97, mode=mode, k=k, valid=valid)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("n_special", [300, 100])
+def test_quant_indexer_exact_ties_take_lowest_indices(dev, indexer_path, bits, n_special):
+    # Every key is the same code row (equal scores); n_special keys get twice the scale (exactly
+    # twice the score).  300 specials put the k-th key inside a small tied group; 100 specials
+    # leave 156 picks among ~20000 equal keys (the threshold bin overflows any candidate list).
+    B, S, IH, IC, k = 2, 20000, 4, 64, 256
+    pq = PolarQuant(bits)
+    row = normal((1, 1, IC), 5, dtype=torch.bfloat16)
+    codes, scale = pq.encode(row.expand(B, S, IC).contiguous().to(dev))
+    q = normal((B, IH, IC), 6, dtype=torch.float32)
+    keyf = pq.decode(codes[:1, :1], scale[:1, :1], out_dtype=torch.float32).cpu()[0, 0]
+    q = torch.where((q @ keyf)[..., None] < 0, -q, q).to(dev)   # positive dots: nonzero scores
+    w = torch.ones(B, IH, device=dev)
+    g = torch.Generator().manual_seed(9)
+    special = [torch.randperm(S, generator=g)[:n_special].sort().values for _ in range(B)]
+    scale = scale.clone()
+    for b in range(B):
+        scale[b, special[b].to(dev)] *= 2
+    idx, sc = csa_indexer_topk_quant(q, w, codes, scale, k, quant=pq, return_scores=True)
+    idx = idx.cpu()
+    for b in range(B):
+        sp = special[b]
+        rest = torch.tensor(sorted(set(range(S)) - set(sp.tolist())), dtype=torch.int64)
+        want = sp[:k] if n_special >= k else torch.cat([sp, rest[:k - n_special]])
+        assert torch.equal(idx[b], want), (b, idx[b][:8], want[:8])
+    # scores: specials exactly twice the others
+    s = sc.cpu()
+    top = min(n_special, k)
+    assert torch.all(s[:, :top] == s[:, :1]) and torch.all(s[:, top:] * 2 == s[:, :1])
