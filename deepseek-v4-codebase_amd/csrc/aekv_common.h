@@ -34,6 +34,13 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
                         const int32_t* valid, int64_t B, int64_t S, int IH, int IC, int bits, int k, int mode, void* ws,
                         int64_t* out_idx, float* out_score, hipStream_t st, const char* who);
 bool use_specialised_codec();
+// Matrix-core decode attention for head_dim 128 (quant_attn_mfma.hip).
+bool quant_attn_mfma_supported(int64_t H, int64_t D);
+size_t quant_attn_mfma_workspace(int64_t B, int64_t H, int64_t n_src);
+int launch_quant_attn_mfma(const void* q, const void* codes, const float* scale, const int64_t* sel,
+                           const void* window, const float* sink, const float* diag, int64_t B, int64_t H, int64_t S,
+                           int64_t K, bool all_blocks, int64_t W, int bits, float softmax_scale, void* ws,
+                           void* out, hipStream_t st, const char* who);
 
 // ---- device helpers ------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __builtin_bit_cast(float, bits16 << 16); }

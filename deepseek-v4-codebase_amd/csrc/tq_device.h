@@ -105,15 +105,22 @@ __device__ __forceinline__ float group_absmax(const float (&a)[EPL]) {
 }
 
 
-// Dequantise the EPL elements of one vector held by this lane: codes * scale -> WHT -> * c -> * diag
-// (turbo_quant.py:187-211).  `row` points at the vector's code bytes.
+// Code bytes a lane holds for its EPL elements of one vector.
 template <int BITS, int D>
-__device__ __forceinline__ void decode_lane(const uint8_t* __restrict__ row, float s, int sub,
-                                            const float (&dg)[(D < 8 ? D : 8)], float c,
-                                            float (&a)[(D < 8 ? D : 8)]) {
+struct LaneCodes {
+  static constexpr int EPL = D < 8 ? D : 8;
+  static constexpr int NB = BITS == 8 ? EPL : EPL / 2;  // code bytes per lane
+  using type = Bytes<NB>;
+};
+
+// Dequantise the EPL elements of one vector held by this lane: codes * scale -> WHT -> * c -> * diag
+// (turbo_quant.py:187-211), from the lane's code bytes (bytes sub*NB .. of the vector's row).
+template <int BITS, int D>
+__device__ __forceinline__ void decode_lane_bytes(const typename LaneCodes<BITS, D>::type& w, float s, int sub,
+                                                  const float (&dg)[(D < 8 ? D : 8)], float c,
+                                                  float (&a)[(D < 8 ? D : 8)]) {
   constexpr int EPL = D < 8 ? D : 8;
-  constexpr int NB = BITS == 8 ? EPL : EPL / 2;
-  Bytes<NB> w = *reinterpret_cast<const Bytes<NB>*>(row + sub * NB);
+  constexpr int NB = LaneCodes<BITS, D>::NB;
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     if constexpr (BITS == 8) {
@@ -128,6 +135,16 @@ __device__ __forceinline__ void decode_lane(const uint8_t* __restrict__ row, flo
   wht_butterflies<D, EPL>(a, sub);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) a[e] = (a[e] * c) * dg[e];
+}
+
+// The same, loading the lane's bytes from `row`, the vector's code row.
+template <int BITS, int D>
+__device__ __forceinline__ void decode_lane(const uint8_t* __restrict__ row, float s, int sub,
+                                            const float (&dg)[(D < 8 ? D : 8)], float c,
+                                            float (&a)[(D < 8 ? D : 8)]) {
+  using W = typename LaneCodes<BITS, D>::type;
+  const W w = *reinterpret_cast<const W*>(row + sub * LaneCodes<BITS, D>::NB);
+  decode_lane_bytes<BITS, D>(w, s, sub, dg, c, a);
 }
 
 // Specialised production-shape kernels (tq_encode_d128.hip).  Each returns false (and launches

@@ -176,3 +176,35 @@ def test_config3_csa_decode_end_to_end(dev):
     assert_topk_matches(idx.cpu().numpy(), scores, 256, tol)
     # ... and attention over the selected blocks vs the oracle on the same selection
     _close(out.view(B, H, D), _oracle_quant(pq, kv_codes, kv_scale, idx, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
+
+
+@pytest.fixture(params=["matrix", "generic"])
+def attn_path(request):
+    """Run a case on the matrix-core attention (default for head_dim 128) and on the generic one."""
+    from aetherkv import _lib as L
+    prev = L.lib().aekv_set_generic_kernels(1 if request.param == "generic" else 0)
+    yield request.param
+    L.lib().aekv_set_generic_kernels(prev)
+
+
+@pytest.mark.parametrize("B,H,S,K,W,bits", [
+    (3, 12, 100, 37, 0, 4),      # one partial tile, no window
+    (2, 16, 300, None, 5, 8),    # every block (HCA), 3 tiles, 16 heads
+    (2, 1, 50, 7, 130, 4),       # one head, window spills into a second tile
+    (2, 12, 1200, None, 128, 4), # 11 tiles -> split over workgroups + combine
+])
+def test_quant_attention_head_dim_128_shapes(dev, attn_path, B, H, S, K, W, bits):
+    D = 128
+    pq, codes, scale, q, win, sink = _quant_inputs(dev, B, H, D, S, max(W, 1), bits, 60 + S % 89)
+    win = win[:, :W].contiguous() if W else None
+    sel = None
+    if K is not None:
+        g = torch.Generator().manual_seed(4)
+        sel = torch.randint(-2, S + 2, (B, K), generator=g).to(dev)   # a few out-of-range entries
+    sm = 0.11
+    got = quant_sink_attention(q, codes, scale, sel, win, sink, sm, quant=pq)
+    want = O.quant_attention(to_np_f32(q).reshape(B, H, D), codes.cpu().numpy(), scale.cpu().numpy(),
+                             None if sel is None else sel.cpu().numpy(),
+                             np.zeros((B, 0, D), np.float32) if win is None else to_np_f32(win), to_np_f32(sink),
+                             O.diag(42, D), bits, sm)
+    _close(got.view(B, H, D), want, QUANT_RTOL, QUANT_ATOL)
