@@ -59,20 +59,37 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-// Lane exchange with partner lane ^ HL inside a wave64.  HL 1/2 use DPP quad_perm, 4/8/16 the
-// ds_swizzle xor mode (within 32 lanes), 32 a ds_bpermute.
-template <int HL>
+// Lane exchange with partner lane ^ HL inside a wave64, on the VALU (no LDS pipe):
+//   1, 2  DPP quad_perm [1,0,3,2] / [2,3,0,1];
+//   4     DPP row_half_mirror (i ^ 7) then quad_perm [3,2,1,0] (i ^ 3);
+//   8     DPP row_ror:8 within the 16-lane row;
+//   16/32 v_permlane16_swap / v_permlane32_swap of the value with itself: the partner lands in the
+//         first result on lanes with that lane bit set and in the second on the others.
+// LDS_PIPE = true moves 4/8/16 to ds_swizzle (xor mode) and 32 to ds_bpermute instead: longer
+// latency, but off the VALU, which pays in VALU-bound streaming kernels.
+template <int HL, bool LDS_PIPE = false>
 __device__ __forceinline__ float xor_lane(float v) {
   int i = __builtin_bit_cast(int, v);
-  if constexpr (HL == 1) {
-    i = __builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  if constexpr (LDS_PIPE && (HL == 4 || HL == 8 || HL == 16)) {
+    i = __builtin_amdgcn_ds_swizzle(i, (HL << 10) | 0x1F);
+  } else if constexpr (LDS_PIPE && HL == 32) {
+    i = __builtin_amdgcn_ds_bpermute(static_cast<int>(((threadIdx.x & 63) ^ 32) << 2), i);
+  } else if constexpr (HL == 1) {
+    i = __builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false);
   } else if constexpr (HL == 2) {
-    i = __builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-  } else if constexpr (HL == 4 || HL == 8 || HL == 16) {
-    i = __builtin_amdgcn_ds_swizzle(i, (HL << 10) | 0x1F);         // bitmask mode, xor HL
+    i = __builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (HL == 4) {
+    i = __builtin_amdgcn_update_dpp(0, i, 0x141, 0xF, 0xF, false);
+    i = __builtin_amdgcn_update_dpp(0, i, 0x1B, 0xF, 0xF, false);
+  } else if constexpr (HL == 8) {
+    i = __builtin_amdgcn_update_dpp(0, i, 0x128, 0xF, 0xF, false);
+  } else if constexpr (HL == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(i), static_cast<uint32_t>(i), false, false);
+    i = static_cast<int>((threadIdx.x & 16) ? r[0] : r[1]);
   } else {
     static_assert(HL == 32, "xor_lane: HL must be a power of two below 64");
-    i = __builtin_amdgcn_ds_bpermute(static_cast<int>(((threadIdx.x & 63) ^ 32) << 2), i);
+    const auto r = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(i), static_cast<uint32_t>(i), false, false);
+    i = static_cast<int>((threadIdx.x & 32) ? r[0] : r[1]);
   }
   return __builtin_bit_cast(float, i);
 }

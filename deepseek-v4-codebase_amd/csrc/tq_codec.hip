@@ -48,7 +48,7 @@ __global__ __launch_bounds__(kThreads) void tq_forward_kernel(const void* __rest
 #pragma unroll
       for (int e = 0; e < EPL; ++e) a[e] = a[e] * dg[e];  // x.float() * diag (exact sign flip)
     }
-    wht_butterflies<D, EPL>(a, sub);
+    wht_butterflies<D, EPL, true>(a, sub);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) a[e] = a[e] * c;  // * fp32(d ** -0.5)
 
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(kThreads) void tq_forward_kernel(const void* __rest
       }
     } else {
       constexpr float Q = MODE == kModeEnc8 ? 127.0f : 7.0f;
-      float m = group_absmax<D, EPL>(a);
+      float m = group_absmax<D, EPL, true>(a);
       m = fmaxf(m, 1e-8f);  // clamp_(min=1e-8)
       int q[EPL];
 #pragma unroll
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kThreads) void tq_decode_kernel(const void* __restr
     float a[EPL];
     // inactive lanes decode row 0 so every lane joins the cross-lane butterflies
     const int64_t vr = ok ? v : 0;
-    decode_lane<BITS, D>(static_cast<const uint8_t*>(codes) + vr * (BITS == 8 ? D : D / 2), scale[vr], sub, dg, c, a);
+    decode_lane<BITS, D, true>(static_cast<const uint8_t*>(codes) + vr * (BITS == 8 ? D : D / 2), scale[vr], sub, dg, c, a);
     if (ok) {
       uint8_t* o = static_cast<uint8_t*>(out) + (v * D + sub * EPL) * (ODT == AEKV_F32 ? 4 : 2);
       if constexpr (ODT == AEKV_F32) {

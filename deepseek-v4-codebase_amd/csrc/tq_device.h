@@ -55,18 +55,19 @@ __device__ __forceinline__ void load_elems(const void* base, int64_t off, bool o
   }
 }
 
-template <int HL, int EPL>
+template <int HL, int EPL, bool LDS_PIPE = false>
 __device__ __forceinline__ void cross_stage(float (&a)[EPL], int sub) {
   const float s = (sub & HL) ? -1.0f : 1.0f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
-    const float p = xor_lane<HL>(a[e]);
+    const float p = xor_lane<HL, LDS_PIPE>(a[e]);
     a[e] = fmaf(a[e], s, p);  // lower lane: a + p ; upper lane: p - a   (product exact)
   }
 }
 
-// Butterfly stages of a D-point transform spread over LPV lanes x EPL elements.
-template <int D, int EPL>
+// Butterfly stages of a D-point transform spread over LPV lanes x EPL elements.  LDS_PIPE selects
+// the lane-exchange path (see xor_lane).
+template <int D, int EPL, bool LDS_PIPE = false>
 __device__ __forceinline__ void wht_butterflies(float (&a)[EPL], int sub) {
   constexpr int LPV = D / EPL;
 #pragma unroll
@@ -81,26 +82,26 @@ __device__ __forceinline__ void wht_butterflies(float (&a)[EPL], int sub) {
       }
     }
   }
-  if constexpr (LPV > 1) cross_stage<1>(a, sub);
-  if constexpr (LPV > 2) cross_stage<2>(a, sub);
-  if constexpr (LPV > 4) cross_stage<4>(a, sub);
-  if constexpr (LPV > 8) cross_stage<8>(a, sub);
-  if constexpr (LPV > 16) cross_stage<16>(a, sub);
-  if constexpr (LPV > 32) cross_stage<32>(a, sub);
+  if constexpr (LPV > 1) cross_stage<1, EPL, LDS_PIPE>(a, sub);
+  if constexpr (LPV > 2) cross_stage<2, EPL, LDS_PIPE>(a, sub);
+  if constexpr (LPV > 4) cross_stage<4, EPL, LDS_PIPE>(a, sub);
+  if constexpr (LPV > 8) cross_stage<8, EPL, LDS_PIPE>(a, sub);
+  if constexpr (LPV > 16) cross_stage<16, EPL, LDS_PIPE>(a, sub);
+  if constexpr (LPV > 32) cross_stage<32, EPL, LDS_PIPE>(a, sub);
 }
 
-template <int D, int EPL>
+template <int D, int EPL, bool LDS_PIPE = false>
 __device__ __forceinline__ float group_absmax(const float (&a)[EPL]) {
   constexpr int LPV = D / EPL;
   float m = 0.0f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) m = fmaxf(m, fabsf(a[e]));
-  if constexpr (LPV > 1) m = fmaxf(m, xor_lane<1>(m));
-  if constexpr (LPV > 2) m = fmaxf(m, xor_lane<2>(m));
-  if constexpr (LPV > 4) m = fmaxf(m, xor_lane<4>(m));
-  if constexpr (LPV > 8) m = fmaxf(m, xor_lane<8>(m));
-  if constexpr (LPV > 16) m = fmaxf(m, xor_lane<16>(m));
-  if constexpr (LPV > 32) m = fmaxf(m, xor_lane<32>(m));
+  if constexpr (LPV > 1) m = fmaxf(m, xor_lane<1, LDS_PIPE>(m));
+  if constexpr (LPV > 2) m = fmaxf(m, xor_lane<2, LDS_PIPE>(m));
+  if constexpr (LPV > 4) m = fmaxf(m, xor_lane<4, LDS_PIPE>(m));
+  if constexpr (LPV > 8) m = fmaxf(m, xor_lane<8, LDS_PIPE>(m));
+  if constexpr (LPV > 16) m = fmaxf(m, xor_lane<16, LDS_PIPE>(m));
+  if constexpr (LPV > 32) m = fmaxf(m, xor_lane<32, LDS_PIPE>(m));
   return m;
 }
 
@@ -115,7 +116,7 @@ struct LaneCodes {
 
 // Dequantise the EPL elements of one vector held by this lane: codes * scale -> WHT -> * c -> * diag
 // (turbo_quant.py:187-211), from the lane's code bytes (bytes sub*NB .. of the vector's row).
-template <int BITS, int D>
+template <int BITS, int D, bool LDS_PIPE = false>
 __device__ __forceinline__ void decode_lane_bytes(const typename LaneCodes<BITS, D>::type& w, float s, int sub,
                                                   const float (&dg)[(D < 8 ? D : 8)], float c,
                                                   float (&a)[(D < 8 ? D : 8)]) {
@@ -132,19 +133,19 @@ __device__ __forceinline__ void decode_lane_bytes(const typename LaneCodes<BITS,
       a[2 * i + 1] = static_cast<float>(hi) * s;
     }
   }
-  wht_butterflies<D, EPL>(a, sub);
+  wht_butterflies<D, EPL, LDS_PIPE>(a, sub);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) a[e] = (a[e] * c) * dg[e];
 }
 
 // The same, loading the lane's bytes from `row`, the vector's code row.
-template <int BITS, int D>
+template <int BITS, int D, bool LDS_PIPE = false>
 __device__ __forceinline__ void decode_lane(const uint8_t* __restrict__ row, float s, int sub,
                                             const float (&dg)[(D < 8 ? D : 8)], float c,
                                             float (&a)[(D < 8 ? D : 8)]) {
   using W = typename LaneCodes<BITS, D>::type;
   const W w = *reinterpret_cast<const W*>(row + sub * LaneCodes<BITS, D>::NB);
-  decode_lane_bytes<BITS, D>(w, s, sub, dg, c, a);
+  decode_lane_bytes<BITS, D, LDS_PIPE>(w, s, sub, dg, c, a);
 }
 
 // Specialised production-shape kernels (tq_encode_d128.hip).  Each returns false (and launches

@@ -10,9 +10,11 @@
 //   v_permlane32_swap exchanges two registers so that every lane ends up holding (lower, upper)
 //   of one pair and applies the same add/sub.  After both swaps lane (g1, g0) holds elements
 //   e = 64*R4 + 32*g1 + 16*g0 + (R & 15) in register R, so its codes are two runs of 8 bytes.
-// * x * diag and the first butterfly stage are one v_dot2_f32_bf16 per output: the packed bf16
-//   word times the bf16 pair (diag[2k], +-diag[2k+1]) (neg_hi for the difference) — exact
-//   products, one rounding, i.e. the reference's fp32 add/sub.
+// * x * diag and the first butterfly stage: per packed bf16 word, lo = w << 16, hi*diag = the
+//   high half with its sign flipped by diag (one bitwise op), and a + b / a - b =
+//   fma(lo, diag_lo, +-hi*diag) — an exact product and one rounding, i.e. the reference's fp32
+//   add/sub.  (v_dot2_f32_bf16 computes the same sum but does not round it like an fp32 add when
+//   the two halves are more than 2^16 apart, so it is not used.)
 // * Scale folding.  max|rot| = RN(c * max|raw|) because rounding is monotonic (raw = butterfly
 //   output before the * c, c = fp32(128^-0.5)), so the per-element work uses the exact product
 //   P = raw * K with K = RN(RN(7c) * rcp(m)) (v_rcp_f32, relative error <= 2^-23) instead of
@@ -36,21 +38,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr float kMagic8 = 12582920.0f;  // 1.5 * 2^23 + 8: RN(t + kMagic8) = kMagic8 + rne(t), ulp 1
 constexpr float kDelta = 5e-6f;
-
-// v_dot2_f32_bf16 with a zero accumulator: w.lo * d.lo + w.hi * d.hi, and the same with d.hi
-// negated (neg_hi).  With d = (diag[2k], diag[2k+1]) as bf16 +-1 the products are exact and the sum
-// is rounded once: this is the reference's x * diag followed by the fp32 a + b / a - b of the
-// first butterfly stage, applied directly to the two bf16 halves of a packed word.
-__device__ __forceinline__ float dot2_sum(uint32_t w, uint32_t d) {
-  float r;
-  asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(w), "v"(d));
-  return r;
-}
-__device__ __forceinline__ float dot2_diff(uint32_t w, uint32_t d) {
-  float r;
-  asm("v_dot2_f32_bf16 %0, %1, %2, 0 neg_hi:[0,1,0]" : "=v"(r) : "v"(w), "v"(d));
-  return r;
-}
 
 __device__ __forceinline__ void swap16(float& a, float& b) {
   auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), false,
@@ -93,11 +80,14 @@ __global__ __launch_bounds__(kThreads) void tq_encode4_d128_bf16_kernel(const ui
   const int lane = threadIdx.x & 63;
   const int v = lane & 15, g = lane >> 4, g0 = g & 1, g1 = g >> 1;
 
-  // bf16 pairs (diag[32g + 2k], diag[32g + 2k + 1]) for the packed words this lane loads
-  uint32_t dg[16];
+  // diag of the packed words this lane loads: diag[32g + 2k] as +-1, diag[32g + 2k + 1] as a sign mask
+  float dlo[16];
+  uint32_t shi[16];
 #pragma unroll
-  for (int k = 0; k < 16; ++k)
-    dg[k] = (diag[32 * g + 2 * k] < 0.0f ? 0xBF80u : 0x3F80u) | (diag[32 * g + 2 * k + 1] < 0.0f ? 0xBF800000u : 0x3F800000u);
+  for (int k = 0; k < 16; ++k) {
+    dlo[k] = diag[32 * g + 2 * k];
+    shi[k] = diag[32 * g + 2 * k + 1] < 0.0f ? 0x80000000u : 0u;
+  }
 
   const int64_t n_groups = (n_vec + 15) >> 4;
   const int64_t wave = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> 6;
@@ -119,8 +109,11 @@ __global__ __launch_bounds__(kThreads) void tq_encode4_d128_bf16_kernel(const ui
     float a[32];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      a[2 * k] = dot2_sum(w[k], dg[k]);       // stage h = 1 on x * diag: lo + hi
-      a[2 * k + 1] = dot2_diff(w[k], dg[k]);  //                           lo - hi
+      // stage h = 1 on x * diag: lo + hi, lo - hi
+      const float lo = __builtin_bit_cast(float, w[k] << 16);
+      const float hs = __builtin_bit_cast(float, (w[k] & 0xFFFF0000u) ^ shi[k]);
+      a[2 * k] = fmaf(lo, dlo[k], hs);
+      a[2 * k + 1] = fmaf(lo, dlo[k], -hs);
     }
     // stages h = 2, 4, 8, 16 in registers
 #pragma unroll
