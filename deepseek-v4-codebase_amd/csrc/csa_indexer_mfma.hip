@@ -19,13 +19,12 @@
 //          fragments and combine constants to the workspace, clears the row's histogram.
 //   score  (wide grid)  scores every visible key, stores its order-preserving uint32 key, and
 //          counts keys per bin of the key's top 12 bits (LDS histogram, flushed with atomics).
-//   cand   (wide grid)  finds the bin t1 holding the k-th largest key from the row histogram and
-//          appends every key in bins >= t1 (key, index) to the row's candidate list.
-//   final  (one workgroup per row)  two more radix levels (bits 19..8, 7..0, LDS histograms)
-//          over the candidates give the k-th largest key T; keys > T and the lowest-index keys
-//          == T are taken and placed by rank under (key desc, index asc).  If the bins >= t1
-//          hold more keys than the candidate list can take (many equal keys), the same levels
-//          run over all of the row's stored keys, read in index order.
+//   final  (one workgroup per row)  finds the bin t1 holding the k-th largest key from the row
+//          histogram, streams the row's keys and collects those in bins >= t1 in LDS, then two
+//          more radix levels (bits 19..8, 7..0, LDS histograms) give the k-th largest key T;
+//          keys > T and the lowest-index keys == T are taken and placed by rank under
+//          (key desc, index asc).  If the bins >= t1 hold more keys than LDS takes (many equal
+//          keys), the same levels run over all of the row's stored keys, read in index order.
 // Both routes return the top-k under the total order (score desc, index asc).
 #include <algorithm>
 
@@ -37,11 +36,10 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kSelThreads = 1024;
 constexpr int kHistBins = 4096;      // top 12 bits of the order key
-constexpr int kCandCap = 4096;       // candidate list per row (fast route)
+constexpr int kCandCap = 4096;       // candidates a row's workgroup collects in LDS (fast route)
 constexpr int kMaxMfmaK = 1024;
 constexpr int kMaxNrb = 4;           // row blocks of 4 heads (IH <= 16)
 constexpr int kMaxKs = 2;            // k-steps of 64 (IC <= 128)
-constexpr int kCandChunk = 8192;     // keys per workgroup of the candidate kernel
 constexpr int64_t kMaxKeys = int64_t(1) << 30;
 
 typedef __attribute__((ext_vector_type(4))) int i32x4_t;
@@ -66,14 +64,13 @@ struct MfmaIdxArgs {
   i32x4_t* frag;         // [B][kMaxNrb][kMaxKs][64]  A fragments per lane
   float4* fcomb;         // [B][kMaxNrb][64]          digit factors x weight
   float2* bounds;        // [B][kMaxNrb][64]          relu clamp bounds
-  uint32_t* keys;        // [B][S]                    order keys of visible keys
+  uint32_t* keys;        // [B][ks]                   order keys of visible keys
+  int64_t ks;            // key row stride: S rounded up to a multiple of 4 (16-byte rows)
   uint32_t* hist;        // [B][kHistBins]
-  uint32_t* cand_cnt;    // [B]
-  uint2* cand;           // [B][kCandCap]             (key, index)
 };
 
 struct WsLayout {
-  size_t frag, fcomb, bounds, keys, hist, cnt, cand, total;
+  size_t frag, fcomb, bounds, keys, hist, total;
 };
 
 WsLayout layout(int64_t B, int64_t S) {
@@ -87,10 +84,8 @@ WsLayout layout(int64_t B, int64_t S) {
   l.frag = take(static_cast<size_t>(B) * kMaxNrb * kMaxKs * 64 * sizeof(i32x4_t));
   l.fcomb = take(static_cast<size_t>(B) * kMaxNrb * 64 * sizeof(float4));
   l.bounds = take(static_cast<size_t>(B) * kMaxNrb * 64 * sizeof(float2));
-  l.keys = take(static_cast<size_t>(B) * static_cast<size_t>(S) * 4);
+  l.keys = take(static_cast<size_t>(B) * static_cast<size_t>(align_up(static_cast<size_t>(S), 4)) * 4);
   l.hist = take(static_cast<size_t>(B) * kHistBins * 4);
-  l.cnt = take(static_cast<size_t>(B) * 4);
-  l.cand = take(static_cast<size_t>(B) * kCandCap * sizeof(uint2));
   l.total = o;
   return l;
 }
@@ -151,17 +146,18 @@ __device__ __forceinline__ void walk_bins(const uint32_t (&v)[PER], int tid, uin
     if (!done && c + v[i] >= need) {
       s_res[0] = static_cast<uint32_t>(PER * tid + i);
       s_res[1] = c;
+      s_res[2] = v[i];
       done = true;
     }
     c += v[i];
   }
 }
 
-// Block-wide (NT threads, NT * PER bins).  Every thread returns the result.  s_tot holds NT/64
-// words, s_res 2; both may be reused after the call.
+// Block-wide (NT threads, NT * PER bins).  Every thread returns the result (and the count of
+// bin t).  s_tot holds NT/64 words, s_res 3; both may be reused after the call.
 template <int NT, int PER>
 __device__ void block_threshold(const uint32_t* h, uint32_t need, uint32_t* s_tot, uint32_t* s_res, uint32_t& t_out,
-                                uint32_t& above_out) {
+                                uint32_t& above_out, uint32_t& count_out) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   uint32_t v[PER];
@@ -180,10 +176,11 @@ __device__ void block_threshold(const uint32_t* h, uint32_t need, uint32_t* s_to
   __syncthreads();
   t_out = s_res[0];
   above_out = s_res[1];
+  count_out = s_res[2];
   __syncthreads();
 }
 
-// Wave-only variant over 64 * PER bins (called by one whole wave); the result lands in s_res.
+// Wave-only variant over 64 * PER bins (called by one whole wave); the result lands in s_res[0..2].
 template <int PER>
 __device__ void wave_threshold(const uint32_t* h, uint32_t need, uint32_t* s_res) {
   const int lane = threadIdx.x & 63;
@@ -196,7 +193,7 @@ __device__ void wave_threshold(const uint32_t* h, uint32_t need, uint32_t* s_res
   if (excl < need && incl >= need) walk_bins<PER>(v, lane, excl, need, s_res);
 }
 
-// ---- prep: query rotation, digits, A fragments; clears the row's histogram and count ----------
+// ---- prep: query rotation, digits, A fragments; clears the row's histogram --------------------
 template <int BITS, int IC>
 __global__ __launch_bounds__(kThreads) void idx_mfma_prep_kernel(MfmaIdxArgs a) {
   constexpr int KS = IC / 64;
@@ -211,7 +208,6 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_prep_kernel(MfmaIdxArgs a) 
     uint4* hz = reinterpret_cast<uint4*>(a.hist + static_cast<int64_t>(b) * kHistBins);
     for (int i = threadIdx.x; i < kHistBins / 4; i += kThreads) hz[i] = make_uint4(0u, 0u, 0u, 0u);
   }
-  if (threadIdx.x == 0) a.cand_cnt[b] = 0u;
 
   // wave wv handles heads wv, wv+4, wv+8, wv+12; lane l holds elements l + 64e of the head.
   // q~ = _wht(diag * q): stages h = 1..32 pair lanes (xor_lane), stage 64 pairs e = 0 and 1.
@@ -347,7 +343,7 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a)
 
   const uint8_t* crow = a.codes + static_cast<int64_t>(b) * S * RB;
   const float* srow = a.kscale + static_cast<int64_t>(b) * S;
-  uint32_t* krow = a.keys + static_cast<int64_t>(b) * S;
+  uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.ks;
   constexpr int64_t kGroupKeys = SPW * 64;
   const int64_t wave_base = (static_cast<int64_t>(blockIdx.x) * 4 + wv) * a.gpw * kGroupKeys;
 #pragma unroll 1
@@ -433,81 +429,28 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a)
   }
 }
 
-// ---- cand: keys in bins >= t1 -> the row's candidate list ----------------------------------------
-// Each wave reads its 2048 keys (8 steps of 4 coalesced 64-key loads) before reserving its slots
-// with one atomic.
-__global__ __launch_bounds__(kThreads) void idx_mfma_cand_kernel(MfmaIdxArgs a) {
-  constexpr int kWaveSpan = kCandChunk / 4;
-  constexpr int kSteps = kWaveSpan / 256;
-  __shared__ uint32_t s_tot[kThreads / 64];
-  __shared__ uint32_t s_res[2];
-  const int b = blockIdx.y;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int64_t nv = visible(a, b);
-  const uint32_t kk = static_cast<uint32_t>(min<int64_t>(a.k, nv));
-  const int64_t j0 = static_cast<int64_t>(blockIdx.x) * kCandChunk;
-  if (kk == 0 || j0 >= nv) return;  // workgroup-uniform
-  const uint32_t* gh = a.hist + static_cast<int64_t>(b) * kHistBins;
-  uint32_t t1, above;
-  block_threshold<kThreads, kHistBins / kThreads>(gh, kk, s_tot, s_res, t1, above);
-  if (above + gh[t1] > static_cast<uint32_t>(kCandCap)) return;  // the final kernel selects from all keys
-  const uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.S;
-  uint2* crow = a.cand + static_cast<int64_t>(b) * kCandCap;
-  const int64_t j1 = min<int64_t>(nv, j0 + kCandChunk);
-  const int64_t wb = j0 + static_cast<int64_t>(wv) * kWaveSpan;
-  uint32_t key[kSteps][4];
-#pragma unroll
-  for (int st = 0; st < kSteps; ++st)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t j = wb + 256 * st + 64 * u + lane;
-      key[st][u] = j < j1 ? krow[j] : 0u;
-    }
-  int n = 0;
-#pragma unroll
-  for (int st = 0; st < kSteps; ++st)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t j = wb + 256 * st + 64 * u + lane;
-      n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(j < j1 && (key[st][u] >> 20) >= t1));
-    }
-  if (n == 0) return;  // wave-uniform, no barrier follows
-  uint32_t run = 0;
-  if (lane == 0) run = atomicAdd(&a.cand_cnt[b], static_cast<uint32_t>(n));
-  run = __builtin_amdgcn_readfirstlane(run);
-#pragma unroll
-  for (int st = 0; st < kSteps; ++st)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t j = wb + 256 * st + 64 * u + lane;
-      const bool take = j < j1 && (key[st][u] >> 20) >= t1;
-      const uint64_t m = __builtin_amdgcn_ballot_w64(take);
-      if (take) {
-        const uint32_t p = run + static_cast<uint32_t>(mbcnt64(m));
-        if (p < static_cast<uint32_t>(kCandCap)) crow[p] = make_uint2(key[st][u], static_cast<uint32_t>(j));
-      }
-      run += static_cast<uint32_t>(__builtin_popcountll(m));
-    }
-}
-
 // ---- final: exact top-k of a row, sorted ------------------------------------------------------
 __device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
   // ascending order of (~key, idx) == key descending, index ascending
   return (static_cast<uint64_t>(~key) << 32) | idx;
 }
 
-// Radix levels 2 and 3 (bits 19..8, then 7..0) below the level-1 bin t1 narrow the threshold to
-// the k-th largest key T; the row's keys > T are taken with the lowest-index keys == T, and the
-// kk selected words are placed by rank.  Fast route: the keys are the candidates (every key in
-// bins >= t1, in LDS); exact route: all visible keys of the row, read in index order.
+// One workgroup per row.  Level 1: the row histogram gives the bin t1 holding the k-th largest key;
+// the row's keys are streamed (every load of a 64K-key chunk issued before any is used) and those
+// in bins >= t1 collected in LDS.  Levels 2 and 3 (bits 19..8, then 7..0, LDS histograms) narrow
+// the threshold to the k-th largest key T; keys > T are taken with the lowest-index keys == T and
+// the kk selected words are placed by rank.  If bins >= t1 hold more keys than LDS takes (many
+// equal keys), the levels run over the row's stored keys instead, read in index order.
 __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs a, int64_t* __restrict__ out_idx,
                                                                      float* __restrict__ out_score) {
   constexpr int NW = kSelThreads / 64;
+  constexpr int kVecPerThread = 16;                        // uint4 loads per thread per chunk
+  constexpr int kChunkKeys = kSelThreads * 4 * kVecPerThread;
   __shared__ uint32_t ck[kCandCap];
   __shared__ uint32_t ci[kCandCap];
   __shared__ __align__(16) uint32_t h[kHistBins];
   __shared__ uint64_t sel[kMaxMfmaK];
-  __shared__ uint32_t s_tot[NW], s_res[2], s_cnt[2], s_wave_eq[NW];
+  __shared__ uint32_t s_tot[NW], s_res[3], s_cnt[2], s_wave_eq[NW];
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t nv = visible(a, b);
@@ -520,21 +463,53 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
     if (srow) srow[i] = -__builtin_inff();
   }
   if (kk == 0) return;
-  const uint32_t* gh = a.hist + static_cast<int64_t>(b) * kHistBins;
-  uint32_t t1, above1;
-  block_threshold<kSelThreads, kHistBins / kSelThreads>(gh, kk, s_tot, s_res, t1, above1);
-  const bool fast = above1 + gh[t1] <= static_cast<uint32_t>(kCandCap);
-  const uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.S;
-  int n = 0;
+  const uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.ks;
+  const uint4* krow4 = reinterpret_cast<const uint4*>(krow);
+
+  // level 1, overlapped with the first chunk's loads
+  uint4 kv[kVecPerThread];
+  auto load_chunk = [&](int64_t c0) {
+#pragma unroll
+    for (int r = 0; r < kVecPerThread; ++r) {
+      const int64_t j = c0 + 4 * (static_cast<int64_t>(r) * kSelThreads + tid);
+      kv[r] = j < nv ? krow4[j >> 2] : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  load_chunk(0);
+  if (tid == 0) s_cnt[0] = 0u;
+  uint32_t t1, above1, in_t1;
+  block_threshold<kSelThreads, kHistBins / kSelThreads>(a.hist + static_cast<int64_t>(b) * kHistBins, kk, s_tot, s_res,
+                                                        t1, above1, in_t1);
+  const bool fast = above1 + in_t1 <= static_cast<uint32_t>(kCandCap);
   if (fast) {
-    n = static_cast<int>(min<uint32_t>(a.cand_cnt[b], kCandCap));
-    const uint2* crow = a.cand + static_cast<int64_t>(b) * kCandCap;
-    for (int i = tid; i < n; i += kSelThreads) {
-      const uint2 c = crow[i];
-      ck[i] = c.x;
-      ci[i] = c.y;
+    for (int64_t c0 = 0; c0 < nv; c0 += kChunkKeys) {
+      if (c0 > 0) load_chunk(c0);
+#pragma unroll
+      for (int r = 0; r < kVecPerThread; ++r) {
+        const int64_t j = c0 + 4 * (static_cast<int64_t>(r) * kSelThreads + tid);
+        const uint32_t kw[4] = {kv[r].x, kv[r].y, kv[r].z, kv[r].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool take = j + e < nv && (kw[e] >> 20) >= t1;
+          const uint64_t m = __builtin_amdgcn_ballot_w64(take);
+          if (m == 0) continue;  // wave-uniform
+          uint32_t base = 0;
+          if (lane == 0) base = atomicAdd(&s_cnt[0], static_cast<uint32_t>(__builtin_popcountll(m)));
+          base = __builtin_amdgcn_readfirstlane(base);
+          if (take) {
+            const uint32_t p = base + static_cast<uint32_t>(mbcnt64(m));
+            if (p < static_cast<uint32_t>(kCandCap)) {
+              ck[p] = kw[e];
+              ci[p] = static_cast<uint32_t>(j + e);
+            }
+          }
+        }
+      }
     }
   }
+  __syncthreads();
+  const int n = fast ? static_cast<int>(min<uint32_t>(s_cnt[0], kCandCap)) : 0;
+
   uint32_t need = kk - above1;  // >= 1 keys still to take at or below bin t1
   uint32_t prefix = t1;
   int shift = 20;
@@ -558,15 +533,17 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
       }
     }
     __syncthreads();
-    uint32_t t, ab;
+    uint32_t t, ab, cnt_t;
     if (lvl == 0) {
-      block_threshold<kSelThreads, kHistBins / kSelThreads>(h, need, s_tot, s_res, t, ab);
+      block_threshold<kSelThreads, kHistBins / kSelThreads>(h, need, s_tot, s_res, t, ab, cnt_t);
     } else {
       if (wv == 0) wave_threshold<4>(h, need, s_res);  // 256 bins
       __syncthreads();
       t = s_res[0];
       ab = s_res[1];
+      cnt_t = s_res[2];
     }
+    (void)cnt_t;
     need -= ab;
     prefix = (prefix << wbits) | t;
     shift = nshift;
@@ -574,6 +551,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
   const uint32_t T = prefix;          // the k-th largest key
   const uint32_t n_eq = h[T & 0xFFu]; // keys == T
   const uint32_t n_gt = kk - need;    // keys > T; `need` keys == T are taken, lowest index first
+  __syncthreads();
   if (tid == 0) {
     s_cnt[0] = 0u;
     s_cnt[1] = 0u;
@@ -685,8 +663,7 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
   a.bounds = reinterpret_cast<float2*>(base + l.bounds);
   a.keys = reinterpret_cast<uint32_t*>(base + l.keys);
   a.hist = reinterpret_cast<uint32_t*>(base + l.hist);
-  a.cand_cnt = reinterpret_cast<uint32_t*>(base + l.cnt);
-  a.cand = reinterpret_cast<uint2*>(base + l.cand);
+  a.ks = static_cast<int64_t>(align_up(static_cast<size_t>(S), 4));
 
   const int nrb = (IH + 3) / 4;
   kern_fn prep = nullptr, score = nullptr;
@@ -707,16 +684,13 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
   gpw = std::min<int64_t>(16, std::max<int64_t>(1, gpw));
   a.gpw = static_cast<int>(gpw);
   const int64_t n_score = ceil_div(groups_per_row, 4 * gpw);
-  const int64_t n_cand = ceil_div(S, kCandChunk);
-  if (B > 65535 || n_score > 0x7fffffff || n_cand > 0x7fffffff)
+  if (B > 65535 || n_score > 0x7fffffff)
     return fail(AEKV_ERR_UNSUPPORTED, "%s: B=%lld S=%lld exceed the launch grid", who, static_cast<long long>(B),
                 static_cast<long long>(S));
   const uint32_t by = static_cast<uint32_t>(B);
   hipLaunchKernelGGL(prep, dim3(by), dim3(kThreads), 0, st, a);
   if (int rc = check_launch(who)) return rc;
   hipLaunchKernelGGL(score, dim3(static_cast<uint32_t>(n_score), by), dim3(kThreads), 0, st, a);
-  if (int rc = check_launch(who)) return rc;
-  hipLaunchKernelGGL(idx_mfma_cand_kernel, dim3(static_cast<uint32_t>(n_cand), by), dim3(kThreads), 0, st, a);
   if (int rc = check_launch(who)) return rc;
   hipLaunchKernelGGL(idx_mfma_final_kernel, dim3(by), dim3(kSelThreads), 0, st, a, out_idx, out_score);
   return check_launch(who);

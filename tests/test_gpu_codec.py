@@ -151,6 +151,34 @@ def test_encode_near_tie_rows_bit_exact(dev, bits):
     np.testing.assert_array_equal(scale.cpu().numpy(), want_s)
 
 
+def wide_pair_rows(n: int, seed: int) -> torch.Tensor:
+    """bf16 rows whose only nonzero elements are one pair (2k, 2k+1) with magnitudes 2^9 .. 2^30
+    apart: the first butterfly stage a +- b is then inexact in fp32 (ties included) and its rounding
+    reaches the row maximum, i.e. the scale."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.zeros(n, 128)
+    k = torch.randint(0, 64, (n,), generator=g)
+    ma = 1 + torch.randint(0, 128, (n,), generator=g) / 128.0
+    mb = 1 + torch.randint(0, 128, (n,), generator=g) / 128.0
+    gap = torch.randint(9, 31, (n,), generator=g).float()
+    sa = torch.where(torch.rand(n, generator=g) < 0.5, -1.0, 1.0)
+    sb = torch.where(torch.rand(n, generator=g) < 0.5, -1.0, 1.0)
+    rows = torch.arange(n)
+    big_first = torch.rand(n, generator=g) < 0.5
+    x[rows, 2 * k + (~big_first).long()] = sa * ma * 4.0
+    x[rows, 2 * k + big_first.long()] = sb * mb * 4.0 * torch.exp2(-gap)
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_encode_inexact_first_stage_bit_exact(dev, bits):
+    x = wide_pair_rows(4096, 23)
+    want_c, want_s = O.encode(bf16_bits(x), "bf16", bits, O.diag(42, 128))
+    codes, scale = PolarQuant(bits).encode(x.to(dev))
+    np.testing.assert_array_equal(scale.cpu().numpy(), want_s)
+    np.testing.assert_array_equal(codes.cpu().numpy(), want_c)
+
+
 def test_specialised_and_generic_encode_agree(dev):
     import aetherkv._lib as L
 
