@@ -16,15 +16,15 @@
 //
 // Kernels (one stream, in order):
 //   prep   (one workgroup per row)  rotates the query, splits the digits, writes the lanes' A
-//          fragments and combine constants to the workspace, clears the row's histogram.
-//   score  (wide grid)  scores every visible key, stores its order-preserving uint32 key, and
-//          counts keys per bin of the key's top 12 bits (LDS histogram, flushed with atomics).
-//   final  (one workgroup per row)  finds the bin t1 holding the k-th largest key from the row
-//          histogram, streams the row's keys and collects those in bins >= t1 in LDS, then two
-//          more radix levels (bits 19..8, 7..0, LDS histograms) give the k-th largest key T;
-//          keys > T and the lowest-index keys == T are taken and placed by rank under
-//          (key desc, index asc).  If the bins >= t1 hold more keys than LDS takes (many equal
-//          keys), the same levels run over all of the row's stored keys, read in index order.
+//          fragments and combine constants to the workspace.
+//   score  (wide grid)  scores every visible key, stores its order-preserving uint32 key and the
+//          max of every 16-key slot.
+//   final  (one workgroup per row)  bounds the k-th largest key from below by the k-th largest
+//          slot max (12-bit resolution), reads only the slots that can hold a top-k key, and
+//          selects exactly among their keys with three LDS radix levels; keys > T and the
+//          lowest-index keys == T are taken and placed by rank under (key desc, index asc).  If
+//          the candidates overflow LDS (many equal keys), the levels run over all of the row's
+//          stored keys, read in index order.
 // Both routes return the top-k under the total order (score desc, index asc).
 #include <algorithm>
 
@@ -37,6 +37,7 @@ constexpr int kThreads = 256;
 constexpr int kSelThreads = 1024;
 constexpr int kHistBins = 4096;      // top 12 bits of the order key
 constexpr int kCandCap = 4096;       // candidates a row's workgroup collects in LDS (fast route)
+constexpr int kSortCap = 2048;       // at most this many candidates are sorted outright
 constexpr int kMaxMfmaK = 1024;
 constexpr int kMaxNrb = 4;           // row blocks of 4 heads (IH <= 16)
 constexpr int kMaxKs = 2;            // k-steps of 64 (IC <= 128)
@@ -65,12 +66,13 @@ struct MfmaIdxArgs {
   float4* fcomb;         // [B][kMaxNrb][64]          digit factors x weight
   float2* bounds;        // [B][kMaxNrb][64]          relu clamp bounds
   uint32_t* keys;        // [B][ks]                   order keys of visible keys
-  int64_t ks;            // key row stride: S rounded up to a multiple of 4 (16-byte rows)
-  uint32_t* hist;        // [B][kHistBins]
+  int64_t ks;            // key row stride: S rounded up to a multiple of 16 (whole slots)
+  uint32_t* smax;        // [B][ms]                   max order key of each 16-key slot
+  int64_t ms;            // slot-max row stride: ceil(S / 16) rounded up to a multiple of 4
 };
 
 struct WsLayout {
-  size_t frag, fcomb, bounds, keys, hist, total;
+  size_t frag, fcomb, bounds, keys, smax, total;
 };
 
 WsLayout layout(int64_t B, int64_t S) {
@@ -84,8 +86,8 @@ WsLayout layout(int64_t B, int64_t S) {
   l.frag = take(static_cast<size_t>(B) * kMaxNrb * kMaxKs * 64 * sizeof(i32x4_t));
   l.fcomb = take(static_cast<size_t>(B) * kMaxNrb * 64 * sizeof(float4));
   l.bounds = take(static_cast<size_t>(B) * kMaxNrb * 64 * sizeof(float2));
-  l.keys = take(static_cast<size_t>(B) * static_cast<size_t>(align_up(static_cast<size_t>(S), 4)) * 4);
-  l.hist = take(static_cast<size_t>(B) * kHistBins * 4);
+  l.keys = take(static_cast<size_t>(B) * static_cast<size_t>(align_up(static_cast<size_t>(S), 16)) * 4);
+  l.smax = take(static_cast<size_t>(B) * align_up((static_cast<size_t>(S) + 15) / 16, 4) * 4);
   l.total = o;
   return l;
 }
@@ -193,7 +195,7 @@ __device__ void wave_threshold(const uint32_t* h, uint32_t need, uint32_t* s_res
   if (excl < need && incl >= need) walk_bins<PER>(v, lane, excl, need, s_res);
 }
 
-// ---- prep: query rotation, digits, A fragments; clears the row's histogram --------------------
+// ---- prep: query rotation, digits, A fragments ------------------------------------------------
 template <int BITS, int IC>
 __global__ __launch_bounds__(kThreads) void idx_mfma_prep_kernel(MfmaIdxArgs a) {
   constexpr int KS = IC / 64;
@@ -204,10 +206,6 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_prep_kernel(MfmaIdxArgs a) 
   const int IH = a.IH;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
 
-  {
-    uint4* hz = reinterpret_cast<uint4*>(a.hist + static_cast<int64_t>(b) * kHistBins);
-    for (int i = threadIdx.x; i < kHistBins / 4; i += kThreads) hz[i] = make_uint4(0u, 0u, 0u, 0u);
-  }
 
   // wave wv handles heads wv, wv+4, wv+8, wv+12; lane l holds elements l + 64e of the head.
   // q~ = _wht(diag * q): stages h = 1..32 pair lanes (xor_lane), stage 64 pairs e = 0 and 1.
@@ -307,7 +305,7 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_prep_kernel(MfmaIdxArgs a) 
   a.bounds[fb * 64 + lane] = make_float2(hb[ho][0], hb[ho][1]);
 }
 
-// ---- score: keys -> order keys + histogram of their top 12 bits --------------------------------
+// ---- score: keys -> order keys + the max of every 16-key slot ----------------------------------
 // A wave scores groups of SPW slots of 64 keys; lane l keeps key base + 64s + l of slot s.  All
 // loads of a group are issued before its matrix work.
 template <int BITS, int IC, int NRB>
@@ -316,13 +314,11 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a)
   constexpr int RB = BITS == 8 ? IC : IC / 2;        // code bytes per key
   constexpr int SPW = RB <= 32 ? 4 : (RB <= 64 ? 2 : 1);
   constexpr int LW = BITS == 8 ? 4 : 2;               // dwords per lane per k-step
-  __shared__ uint32_t hist[kHistBins];
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
   const int64_t S = a.S;
   const int64_t nv = visible(a, b);
 
-  for (int i = threadIdx.x; i < kHistBins; i += kThreads) hist[i] = 0u;
   i32x4_t A[NRB][KS];
   float f[NRB][4], lo[NRB], hi[NRB];
 #pragma unroll
@@ -344,6 +340,7 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a)
   const uint8_t* crow = a.codes + static_cast<int64_t>(b) * S * RB;
   const float* srow = a.kscale + static_cast<int64_t>(b) * S;
   uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.ks;
+  uint32_t* mrow = a.smax + static_cast<int64_t>(b) * a.ms;
   constexpr int64_t kGroupKeys = SPW * 64;
   const int64_t wave_base = (static_cast<int64_t>(blockIdx.x) * 4 + wv) * a.gpw * kGroupKeys;
 #pragma unroll 1
@@ -414,18 +411,16 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a)
       // lane l keeps key kb + 64s + l, i.e. tq = l / 16
       const float mine = g == 0 ? tq_t[0] : (g == 1 ? tq_t[1] : (g == 2 ? tq_t[2] : tq_t[3]));
       const int64_t jo = kb + 64 * s + lane;
-      if (jo < nv) {
-        const uint32_t key = order_key(mine * scl[s]);
-        krow[jo] = key;
-        atomicAdd(&hist[key >> 20], 1u);
-      }
+      const uint32_t key = jo < nv ? order_key(mine * scl[s]) : 0u;
+      if (jo < nv) krow[jo] = key;
+      // max of the 16-key slot of lanes 16u .. 16u+15, stored by its first lane
+      uint32_t mx = key;
+      mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<1>(__builtin_bit_cast(float, mx))));
+      mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<2>(__builtin_bit_cast(float, mx))));
+      mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<4>(__builtin_bit_cast(float, mx))));
+      mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<8>(__builtin_bit_cast(float, mx))));
+      if ((lane & 15) == 0 && jo < nv) mrow[jo >> 4] = mx;
     }
-  }
-  __syncthreads();
-  uint32_t* gh = a.hist + static_cast<int64_t>(b) * kHistBins;
-  for (int i = threadIdx.x; i < kHistBins; i += kThreads) {
-    const uint32_t c = hist[i];
-    if (c) atomicAdd(&gh[i], c);
   }
 }
 
@@ -435,22 +430,24 @@ __device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
   return (static_cast<uint64_t>(~key) << 32) | idx;
 }
 
-// One workgroup per row.  Level 1: the row histogram gives the bin t1 holding the k-th largest key;
-// the row's keys are streamed (every load of a 64K-key chunk issued before any is used) and those
-// in bins >= t1 collected in LDS.  Levels 2 and 3 (bits 19..8, then 7..0, LDS histograms) narrow
-// the threshold to the k-th largest key T; keys > T are taken with the lowest-index keys == T and
-// the kk selected words are placed by rank.  If bins >= t1 hold more keys than LDS takes (many
-// equal keys), the levels run over the row's stored keys instead, read in index order.
+// One workgroup per row.
+//  1. Slot bound: every 16-key slot's max is one of its keys, so if kk slot maxima are >= tau
+//     then the kk-th largest key is >= tau, and every top-kk key lies in a slot whose max is >=
+//     tau.  tau is the floor of the 12-bit bin holding the kk-th largest slot max (LDS histogram
+//     of the maxima); only the slots with max >= tau are read, and their keys >= tau collected.
+//  2. Three radix levels over the candidates (bits 31..20, 19..8, 7..0; LDS histograms) give
+//     the kk-th largest key T; keys > T are taken with the lowest-index keys == T and the kk words
+//     placed by rank.  If the candidates overflow LDS (many equal keys), the levels run over all
+//     of the row's keys, read in index order.
 __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs a, int64_t* __restrict__ out_idx,
                                                                      float* __restrict__ out_score) {
   constexpr int NW = kSelThreads / 64;
-  constexpr int kVecPerThread = 16;                        // uint4 loads per thread per chunk
-  constexpr int kChunkKeys = kSelThreads * 4 * kVecPerThread;
-  __shared__ uint32_t ck[kCandCap];
-  __shared__ uint32_t ci[kCandCap];
+  __shared__ uint64_t cbuf[kCandCap];  // candidates: keys ck[] then indices ci[], or sort words
   __shared__ __align__(16) uint32_t h[kHistBins];
   __shared__ uint64_t sel[kMaxMfmaK];
   __shared__ uint32_t s_tot[NW], s_res[3], s_cnt[2], s_wave_eq[NW];
+  uint32_t* ck = reinterpret_cast<uint32_t*>(cbuf);
+  uint32_t* ci = ck + kCandCap;
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t nv = visible(a, b);
@@ -465,90 +462,174 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
   if (kk == 0) return;
   const uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.ks;
   const uint4* krow4 = reinterpret_cast<const uint4*>(krow);
+  const uint32_t* mrow = a.smax + static_cast<int64_t>(b) * a.ms;
+  const int64_t n_slots = (nv + 15) >> 4;
 
-  // level 1, overlapped with the first chunk's loads
-  uint4 kv[kVecPerThread];
-  auto load_chunk = [&](int64_t c0) {
+  // ---- 1. slot bound and candidates ----
+  // thread tid owns slots c0 + tid + r * kSelThreads (r < 4) of each pass of 4096 slots; with
+  // n_slots <= 4096 (S <= 65536) the maxima loaded for the histogram are reused for the scan
+  constexpr int kSlotPer = 4;
+  constexpr int64_t kSlotPass = static_cast<int64_t>(kSlotPer) * kSelThreads;
+  for (int i = tid; i < kHistBins; i += kSelThreads) h[i] = 0u;
+  if (tid == 0) s_cnt[0] = 0u;
+  uint32_t mx[kSlotPer];
+  auto load_max = [&](int64_t c0) {
 #pragma unroll
-    for (int r = 0; r < kVecPerThread; ++r) {
-      const int64_t j = c0 + 4 * (static_cast<int64_t>(r) * kSelThreads + tid);
-      kv[r] = j < nv ? krow4[j >> 2] : make_uint4(0u, 0u, 0u, 0u);
+    for (int r = 0; r < kSlotPer; ++r) {
+      const int64_t sl = c0 + tid + static_cast<int64_t>(r) * kSelThreads;
+      mx[r] = sl < n_slots ? mrow[sl] : 0u;
     }
   };
-  load_chunk(0);
-  if (tid == 0) s_cnt[0] = 0u;
-  uint32_t t1, above1, in_t1;
-  block_threshold<kSelThreads, kHistBins / kSelThreads>(a.hist + static_cast<int64_t>(b) * kHistBins, kk, s_tot, s_res,
-                                                        t1, above1, in_t1);
-  const bool fast = above1 + in_t1 <= static_cast<uint32_t>(kCandCap);
-  if (fast) {
-    for (int64_t c0 = 0; c0 < nv; c0 += kChunkKeys) {
-      if (c0 > 0) load_chunk(c0);
+  load_max(0);
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
+    if (c0 > 0) load_max(c0);
 #pragma unroll
-      for (int r = 0; r < kVecPerThread; ++r) {
-        const int64_t j = c0 + 4 * (static_cast<int64_t>(r) * kSelThreads + tid);
-        const uint32_t kw[4] = {kv[r].x, kv[r].y, kv[r].z, kv[r].w};
+    for (int r = 0; r < kSlotPer; ++r)
+      if (c0 + tid + static_cast<int64_t>(r) * kSelThreads < n_slots) atomicAdd(&h[mx[r] >> 20], 1u);
+  }
+  __syncthreads();
+  uint32_t tau = 0u;
+  if (static_cast<int64_t>(kk) <= n_slots) {
+    uint32_t t, ab, ct;
+    block_threshold<kSelThreads, kHistBins / kSelThreads>(h, kk, s_tot, s_res, t, ab, ct);
+    (void)ab;
+    (void)ct;
+    tau = t << 20;
+  }
+  // qualifying slots (max >= tau) are compacted into a list (in h, free until the radix levels),
+  // then one thread per listed slot reads its 16 keys and appends those >= tau
+  for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
+    if (n_slots > kSlotPass) load_max(c0);
+    __syncthreads();  // h and s_cnt[1] are free
+    if (tid == 0) s_cnt[1] = 0u;
+    __syncthreads();
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool take = j + e < nv && (kw[e] >> 20) >= t1;
-          const uint64_t m = __builtin_amdgcn_ballot_w64(take);
-          if (m == 0) continue;  // wave-uniform
-          uint32_t base = 0;
-          if (lane == 0) base = atomicAdd(&s_cnt[0], static_cast<uint32_t>(__builtin_popcountll(m)));
-          base = __builtin_amdgcn_readfirstlane(base);
-          if (take) {
-            const uint32_t p = base + static_cast<uint32_t>(mbcnt64(m));
-            if (p < static_cast<uint32_t>(kCandCap)) {
-              ck[p] = kw[e];
-              ci[p] = static_cast<uint32_t>(j + e);
-            }
+    for (int r = 0; r < kSlotPer; ++r) {
+      const int64_t sl = c0 + tid + static_cast<int64_t>(r) * kSelThreads;
+      const bool q = sl < n_slots && mx[r] >= tau;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(q);
+      if (m == 0) continue;  // wave-uniform
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&s_cnt[1], static_cast<uint32_t>(__builtin_popcountll(m)));
+      base = __builtin_amdgcn_readfirstlane(base);
+      if (q) h[base + static_cast<uint32_t>(mbcnt64(m))] = static_cast<uint32_t>(sl - c0);
+    }
+    __syncthreads();
+    const int n_list = static_cast<int>(s_cnt[1]);
+    for (int li = tid; li < n_list; li += kSelThreads) {
+      const int64_t sl = c0 + h[li];
+      uint32_t kw[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 v = krow4[sl * 4 + q];
+        kw[4 * q] = v.x;
+        kw[4 * q + 1] = v.y;
+        kw[4 * q + 2] = v.z;
+        kw[4 * q + 3] = v.w;
+      }
+      uint32_t c = 0;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) c += (16 * sl + e < nv && kw[e] >= tau) ? 1u : 0u;
+      uint32_t p = atomicAdd(&s_cnt[0], c);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        if (16 * sl + e < nv && kw[e] >= tau) {
+          if (p < static_cast<uint32_t>(kCandCap)) {
+            ck[p] = kw[e];
+            ci[p] = static_cast<uint32_t>(16 * sl + e);
           }
+          ++p;
         }
       }
     }
   }
   __syncthreads();
-  const int n = fast ? static_cast<int>(min<uint32_t>(s_cnt[0], kCandCap)) : 0;
+  const uint32_t n_cand = s_cnt[0];
+  const bool fast = n_cand <= static_cast<uint32_t>(kCandCap);
+  const int n = fast ? static_cast<int>(n_cand) : 0;
 
-  uint32_t need = kk - above1;  // >= 1 keys still to take at or below bin t1
-  uint32_t prefix = t1;
-  int shift = 20;
+  // ---- 2a. up to kSortCap candidates (the usual case): sort them all, emit the first kk ----
+  if (fast && n <= kSortCap) {
+    int P = 64;
+    while (P < n) P <<= 1;
+    uint64_t w[kSortCap / kSelThreads];
+#pragma unroll
+    for (int r = 0; r < kSortCap / kSelThreads; ++r) {
+      const int i = tid + r * kSelThreads;
+      w[r] = i < n ? sort_word(ck[i], ci[i]) : ~0ull;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kSortCap / kSelThreads; ++r) {
+      const int i = tid + r * kSelThreads;
+      if (i < P) cbuf[i] = w[r];
+    }
+    __syncthreads();
+    for (int size = 2; size <= P; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < P / 2; i += kSelThreads) {
+          const int pos = 2 * i - (i & (stride - 1));
+          const int partner = pos + stride;
+          const bool up = (pos & size) == 0;
+          const uint64_t x = cbuf[pos], y = cbuf[partner];
+          if ((x > y) == up) {
+            cbuf[pos] = y;
+            cbuf[partner] = x;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int i = tid; i < static_cast<int>(kk); i += kSelThreads) {
+      const uint64_t v = cbuf[i];
+      orow[i] = static_cast<int64_t>(static_cast<uint32_t>(v & 0xffffffffu));
+      if (srow) srow[i] = order_key_inv(~static_cast<uint32_t>(v >> 32));
+    }
+    return;
+  }
+
+  // ---- 2. three radix levels down to the kk-th largest key T ----
+  uint32_t need = kk;  // keys still to take at or below the current prefix
+  uint32_t prefix = 0u;
+  int shift = 32;
 #pragma unroll 1
-  for (int lvl = 0; lvl < 2; ++lvl) {
-    const int wbits = lvl == 0 ? 12 : 8;
+  for (int lvl = 0; lvl < 3; ++lvl) {
+    const int wbits = lvl < 2 ? 12 : 8;
     const int nb = 1 << wbits;
     const int nshift = shift - wbits;
     const uint32_t mask = static_cast<uint32_t>(nb - 1);
+    __syncthreads();  // the previous level's readers of h are done
     for (int i = tid; i < nb; i += kSelThreads) h[i] = 0u;
     __syncthreads();
+    // (key >> 32) is undefined: level 0 has no prefix to match
     if (fast) {
       for (int i = tid; i < n; i += kSelThreads) {
         const uint32_t key = ck[i];
-        if ((key >> shift) == prefix) atomicAdd(&h[(key >> nshift) & mask], 1u);
+        if (lvl == 0 || (key >> shift) == prefix) atomicAdd(&h[(key >> nshift) & mask], 1u);
       }
     } else {
       for (int64_t j = tid; j < nv; j += kSelThreads) {
         const uint32_t key = krow[j];
-        if ((key >> shift) == prefix) atomicAdd(&h[(key >> nshift) & mask], 1u);
+        if (lvl == 0 || (key >> shift) == prefix) atomicAdd(&h[(key >> nshift) & mask], 1u);
       }
     }
     __syncthreads();
-    uint32_t t, ab, cnt_t;
-    if (lvl == 0) {
-      block_threshold<kSelThreads, kHistBins / kSelThreads>(h, need, s_tot, s_res, t, ab, cnt_t);
+    uint32_t t, ab, ct;
+    if (lvl < 2) {
+      block_threshold<kSelThreads, kHistBins / kSelThreads>(h, need, s_tot, s_res, t, ab, ct);
     } else {
       if (wv == 0) wave_threshold<4>(h, need, s_res);  // 256 bins
       __syncthreads();
       t = s_res[0];
       ab = s_res[1];
-      cnt_t = s_res[2];
     }
-    (void)cnt_t;
+    (void)ct;
     need -= ab;
     prefix = (prefix << wbits) | t;
     shift = nshift;
   }
-  const uint32_t T = prefix;          // the k-th largest key
+  const uint32_t T = prefix;          // the kk-th largest key
   const uint32_t n_eq = h[T & 0xFFu]; // keys == T
   const uint32_t n_gt = kk - need;    // keys > T; `need` keys == T are taken, lowest index first
   __syncthreads();
@@ -605,13 +686,22 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
     }
   }
   __syncthreads();
-  // the kk words are distinct: each one's output position is its rank
-  for (int i = tid; i < static_cast<int>(kk); i += kSelThreads) {
-    const uint64_t w = sel[i];
+  // the kk words are distinct: each one's output position is its rank.  Four adjacent lanes
+  // share an element, each counting over a quarter of the words.
+  const int q4 = (static_cast<int>(kk) + 3) / 4;
+  for (int base = 0; base < static_cast<int>(kk); base += kSelThreads / 4) {
+    const int i = base + (tid >> 2), part = tid & 3;
+    const uint64_t w = i < static_cast<int>(kk) ? sel[i] : 0ull;
+    const int j0 = part * q4, j1 = min(static_cast<int>(kk), j0 + q4);
     uint32_t r = 0;
-    for (int j = 0; j < static_cast<int>(kk); ++j) r += sel[j] < w ? 1u : 0u;
-    orow[r] = static_cast<int64_t>(static_cast<uint32_t>(w & 0xffffffffu));
-    if (srow) srow[r] = order_key_inv(~static_cast<uint32_t>(w >> 32));
+#pragma unroll 8
+    for (int j = j0; j < j1; ++j) r += sel[j] < w ? 1u : 0u;
+    r += __builtin_bit_cast(uint32_t, xor_lane<1>(__builtin_bit_cast(float, r)));
+    r += __builtin_bit_cast(uint32_t, xor_lane<2>(__builtin_bit_cast(float, r)));
+    if (part == 0 && i < static_cast<int>(kk)) {
+      orow[r] = static_cast<int64_t>(static_cast<uint32_t>(w & 0xffffffffu));
+      if (srow) srow[r] = order_key_inv(~static_cast<uint32_t>(w >> 32));
+    }
   }
 }
 
@@ -662,8 +752,9 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
   a.fcomb = reinterpret_cast<float4*>(base + l.fcomb);
   a.bounds = reinterpret_cast<float2*>(base + l.bounds);
   a.keys = reinterpret_cast<uint32_t*>(base + l.keys);
-  a.hist = reinterpret_cast<uint32_t*>(base + l.hist);
-  a.ks = static_cast<int64_t>(align_up(static_cast<size_t>(S), 4));
+  a.smax = reinterpret_cast<uint32_t*>(base + l.smax);
+  a.ms = static_cast<int64_t>(align_up((static_cast<size_t>(S) + 15) / 16, 4));
+  a.ks = static_cast<int64_t>(align_up(static_cast<size_t>(S), 16));
 
   const int nrb = (IH + 3) / 4;
   kern_fn prep = nullptr, score = nullptr;
