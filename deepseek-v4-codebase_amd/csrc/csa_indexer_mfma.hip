@@ -15,10 +15,9 @@
 // ~2^-27 of max|q~_h|) and three fp32 roundings, i.e. fp32-level scores.
 //
 // Kernels (one stream, in order):
-//   prep   (one workgroup per row)  rotates the query, splits the digits, writes the lanes' A
-//          fragments and combine constants to the workspace.
-//   score  (wide grid)  scores every visible key, stores its order-preserving uint32 key and the
-//          max of every 16-key slot.
+//   score  (wide grid)  rotates the row's query and splits the digits in LDS (per workgroup),
+//          scores every visible key, stores its order-preserving uint32 key and the max of every
+//          16-key slot.
 //   final  (one workgroup per row)  bounds the k-th largest key from below by the k-th largest
 //          slot max (12-bit resolution), reads only the slots that can hold a top-k key, and
 //          selects exactly among their keys with three LDS radix levels; keys > T and the
@@ -40,7 +39,6 @@ constexpr int kCandCap = 4096;       // candidates a row's workgroup collects in
 constexpr int kSortCap = 2048;       // at most this many candidates are sorted outright
 constexpr int kMaxMfmaK = 1024;
 constexpr int kMaxNrb = 4;           // row blocks of 4 heads (IH <= 16)
-constexpr int kMaxKs = 2;            // k-steps of 64 (IC <= 128)
 constexpr int64_t kMaxKeys = int64_t(1) << 30;
 
 typedef __attribute__((ext_vector_type(4))) int i32x4_t;
@@ -62,9 +60,6 @@ struct MfmaIdxArgs {
   int IH, k, mode;
   int gpw;               // slot groups per wave in the score kernel
   float wscale;
-  i32x4_t* frag;         // [B][kMaxNrb][kMaxKs][64]  A fragments per lane
-  float4* fcomb;         // [B][kMaxNrb][64]          digit factors x weight
-  float2* bounds;        // [B][kMaxNrb][64]          relu clamp bounds
   uint32_t* keys;        // [B][ks]                   order keys of visible keys
   int64_t ks;            // key row stride: S rounded up to a multiple of 16 (whole slots)
   uint32_t* smax;        // [B][ms]                   max order key of each 16-key slot
@@ -72,7 +67,7 @@ struct MfmaIdxArgs {
 };
 
 struct WsLayout {
-  size_t frag, fcomb, bounds, keys, smax, total;
+  size_t keys, smax, total;
 };
 
 WsLayout layout(int64_t B, int64_t S) {
@@ -83,9 +78,6 @@ WsLayout layout(int64_t B, int64_t S) {
     o += align_up(bytes, 256);
     return at;
   };
-  l.frag = take(static_cast<size_t>(B) * kMaxNrb * kMaxKs * 64 * sizeof(i32x4_t));
-  l.fcomb = take(static_cast<size_t>(B) * kMaxNrb * 64 * sizeof(float4));
-  l.bounds = take(static_cast<size_t>(B) * kMaxNrb * 64 * sizeof(float2));
   l.keys = take(static_cast<size_t>(B) * static_cast<size_t>(align_up(static_cast<size_t>(S), 16)) * 4);
   l.smax = take(static_cast<size_t>(B) * align_up((static_cast<size_t>(S) + 15) / 16, 4) * 4);
   l.total = o;
@@ -195,22 +187,19 @@ __device__ void wave_threshold(const uint32_t* h, uint32_t need, uint32_t* s_res
   if (excl < need && incl >= need) walk_bins<PER>(v, lane, excl, need, s_res);
 }
 
-// ---- prep: query rotation, digits, A fragments ------------------------------------------------
-template <int BITS, int IC>
-__global__ __launch_bounds__(kThreads) void idx_mfma_prep_kernel(MfmaIdxArgs a) {
+// ---- query side: rotation, digits, A fragments (once per workgroup, in LDS) --------------------
+// Wave wv rotates heads wv, wv+4, .. (< 4*NRB); lane l holds elements l + 64e of the head.
+// q~ = _wht(diag * q): stages h = 1..32 pair lanes (xor_lane), stage 64 pairs e = 0 and 1.  Then
+// every lane assembles its A fragments (4 heads x 4 digits per row block) and combine constants.
+template <int BITS, int IC, int NRB>
+__device__ __forceinline__ void query_fragments(const MfmaIdxArgs& a, int b, int8_t (*dig)[16][IC], float (*hf)[4],
+                                                float (*hb)[2], i32x4_t (&A)[NRB][IC / 64], float (&f)[NRB][4],
+                                                float (&lo)[NRB], float (&hi)[NRB]) {
   constexpr int KS = IC / 64;
-  __shared__ int8_t dig[4][16][IC];
-  __shared__ float hf[16][4];  // per head: digit factors S * 2^-7d (/16 for 4-bit) * weight
-  __shared__ float hb[16][2];  // per head: clamp bounds
-  const int b = blockIdx.x;
+  constexpr int EPL = IC / 64;
   const int IH = a.IH;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
-
-
-  // wave wv handles heads wv, wv+4, wv+8, wv+12; lane l holds elements l + 64e of the head.
-  // q~ = _wht(diag * q): stages h = 1..32 pair lanes (xor_lane), stage 64 pairs e = 0 and 1.
-  constexpr int EPL = IC / 64;
-  for (int h = wv; h < 16; h += 4) {
+  for (int h = wv; h < 4 * NRB; h += 4) {
     float v[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
@@ -258,15 +247,15 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_prep_kernel(MfmaIdxArgs a) 
       }
     }
     if (lane == 0) {
-      float wa = 0.0f, lo = -__builtin_inff(), hi = __builtin_inff();
+      float wa = 0.0f, lw = -__builtin_inff(), hw = __builtin_inff();
       if (h < IH) {
         const float wr = a.w[static_cast<int64_t>(b) * IH + h];
         if (a.mode == AEKV_IDX_SOFTPLUS) {
           wa = softplus_f32(wr);
-          lo = 0.0f;
+          lw = 0.0f;
         } else if (a.mode == AEKV_IDX_RAW) {
           wa = wr;
-          if (wr >= 0.0f) lo = 0.0f; else hi = 0.0f;  // relu(dot)*w = clamp(dot*w) toward 0
+          if (wr >= 0.0f) lw = 0.0f; else hw = 0.0f;  // relu(dot)*w = clamp(dot*w) toward 0
         } else {
           wa = fmaxf(wr, 0.0f);                       // relu on the weight only
         }
@@ -274,35 +263,34 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_prep_kernel(MfmaIdxArgs a) 
       const float unit = BITS == 4 ? 1.0f / 16.0f : 1.0f;
 #pragma unroll
       for (int d = 0; d < 4; ++d) hf[h][d] = ldexpf(step, -7 * d) * unit * wa;
-      hb[h][0] = lo;
-      hb[h][1] = hi;
+      hb[h][0] = lw;
+      hb[h][1] = hw;
     }
   }
   __syncthreads();
-
-  // wave wv writes row block rb = wv (heads 4rb..4rb+3): A rows = 4 heads x 4 digits
-  const int rb = wv;
   const int row = lane & 15;
-  const int h = 4 * rb + (row >> 2), d = row & 3;
-  const int64_t fb = static_cast<int64_t>(b) * kMaxNrb + rb;
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    i32x4_t A;
+  for (int rb = 0; rb < NRB; ++rb) {
+    const int h = 4 * rb + (row >> 2), d = row & 3;  // A rows = 4 heads x 4 digits
 #pragma unroll
-    for (int dw = 0; dw < 4; ++dw) {
-      uint32_t word = 0;
+    for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-      for (int by = 0; by < 4; ++by) {
-        const int c = cmap<BITS>(ks, g, 4 * dw + by);
-        word |= (static_cast<uint32_t>(static_cast<uint8_t>(dig[d][h][c])) << (8 * by));
+      for (int dw = 0; dw < 4; ++dw) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int by = 0; by < 4; ++by) {
+          const int c = cmap<BITS>(ks, g, 4 * dw + by);
+          word |= (static_cast<uint32_t>(static_cast<uint8_t>(dig[d][h][c])) << (8 * by));
+        }
+        A[rb][ks][dw] = static_cast<int>(word);
       }
-      A[dw] = static_cast<int>(word);
     }
-    a.frag[(fb * kMaxKs + ks) * 64 + lane] = A;
+    const int ho = 4 * rb + g;  // output rows 4g..4g+3 = head 4rb+g, digits 0..3
+#pragma unroll
+    for (int d2 = 0; d2 < 4; ++d2) f[rb][d2] = hf[ho][d2];
+    lo[rb] = hb[ho][0];
+    hi[rb] = hb[ho][1];
   }
-  const int ho = 4 * rb + g;  // output rows 4g..4g+3 = head 4rb+g, digits 0..3
-  a.fcomb[fb * 64 + lane] = make_float4(hf[ho][0], hf[ho][1], hf[ho][2], hf[ho][3]);
-  a.bounds[fb * 64 + lane] = make_float2(hb[ho][0], hb[ho][1]);
 }
 
 // ---- score: keys -> order keys + the max of every 16-key slot ----------------------------------
@@ -319,23 +307,12 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a)
   const int64_t S = a.S;
   const int64_t nv = visible(a, b);
 
+  __shared__ int8_t dig[4][16][IC];
+  __shared__ float hf[16][4];  // per head: digit factors S * 2^-7d (/16 for 4-bit) * weight
+  __shared__ float hb[16][2];  // per head: clamp bounds
   i32x4_t A[NRB][KS];
   float f[NRB][4], lo[NRB], hi[NRB];
-#pragma unroll
-  for (int rb = 0; rb < NRB; ++rb) {
-    const int64_t fb = static_cast<int64_t>(b) * kMaxNrb + rb;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) A[rb][ks] = a.frag[(fb * kMaxKs + ks) * 64 + lane];
-    const float4 fc = a.fcomb[fb * 64 + lane];
-    f[rb][0] = fc.x;
-    f[rb][1] = fc.y;
-    f[rb][2] = fc.z;
-    f[rb][3] = fc.w;
-    const float2 bd = a.bounds[fb * 64 + lane];
-    lo[rb] = bd.x;
-    hi[rb] = bd.y;
-  }
-  __syncthreads();
+  query_fragments<BITS, IC, NRB>(a, b, dig, hf, hb, A, f, lo, hi);
 
   const uint8_t* crow = a.codes + static_cast<int64_t>(b) * S * RB;
   const float* srow = a.kscale + static_cast<int64_t>(b) * S;
@@ -748,23 +725,15 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
   a.wscale = wht_scale(IC);
   const WsLayout l = layout(B, S);
   char* base = static_cast<char*>(ws);
-  a.frag = reinterpret_cast<i32x4_t*>(base + l.frag);
-  a.fcomb = reinterpret_cast<float4*>(base + l.fcomb);
-  a.bounds = reinterpret_cast<float2*>(base + l.bounds);
   a.keys = reinterpret_cast<uint32_t*>(base + l.keys);
   a.smax = reinterpret_cast<uint32_t*>(base + l.smax);
   a.ms = static_cast<int64_t>(align_up((static_cast<size_t>(S) + 15) / 16, 4));
   a.ks = static_cast<int64_t>(align_up(static_cast<size_t>(S), 16));
 
   const int nrb = (IH + 3) / 4;
-  kern_fn prep = nullptr, score = nullptr;
-  if (bits == 8) {
-    prep = IC == 64 ? idx_mfma_prep_kernel<8, 64> : idx_mfma_prep_kernel<8, 128>;
-    score = IC == 64 ? pick_score<8, 64>(nrb) : pick_score<8, 128>(nrb);
-  } else {
-    prep = IC == 64 ? idx_mfma_prep_kernel<4, 64> : idx_mfma_prep_kernel<4, 128>;
-    score = IC == 64 ? pick_score<4, 64>(nrb) : pick_score<4, 128>(nrb);
-  }
+  kern_fn score = nullptr;
+  if (bits == 8) score = IC == 64 ? pick_score<8, 64>(nrb) : pick_score<8, 128>(nrb);
+  else score = IC == 64 ? pick_score<4, 64>(nrb) : pick_score<4, 128>(nrb);
   if (!score) return fail(AEKV_ERR_UNSUPPORTED, "%s: no matrix-core indexer for IH=%d IC=%d", who, IH, IC);
   // slot-group size of the score kernel (must match SPW there) and groups per wave: enough
   // workgroups to fill the chip (~2048), at most 16 groups per wave
@@ -779,8 +748,6 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
     return fail(AEKV_ERR_UNSUPPORTED, "%s: B=%lld S=%lld exceed the launch grid", who, static_cast<long long>(B),
                 static_cast<long long>(S));
   const uint32_t by = static_cast<uint32_t>(B);
-  hipLaunchKernelGGL(prep, dim3(by), dim3(kThreads), 0, st, a);
-  if (int rc = check_launch(who)) return rc;
   hipLaunchKernelGGL(score, dim3(static_cast<uint32_t>(n_score), by), dim3(kThreads), 0, st, a);
   if (int rc = check_launch(who)) return rc;
   hipLaunchKernelGGL(idx_mfma_final_kernel, dim3(by), dim3(kSelThreads), 0, st, a, out_idx, out_score);

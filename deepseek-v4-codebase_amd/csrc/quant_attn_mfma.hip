@@ -5,7 +5,7 @@
 // indexer's selected blocks), both followed by the sink attention of aether_pipeline/serving.py:
 // 99-130 over [dequant(blocks), window] with K = V (serving.py:52-53).
 //
-// One workgroup owns a row (or a contiguous split of a long row's sources).  Per tile of 128
+// One workgroup (8 waves) owns a row (or a contiguous split of a long row's sources).  Per tile of 256
 // sources it decodes the gathered code rows exactly (same code path as PolarQuant.decode, rounded
 // to bf16 like the engine's dequantised cache) or copies window rows into an LDS tile, row-major.
 // Wave w owns tile keys 32w..32w+31 and works transposed, so that each lane owns one head
@@ -25,9 +25,10 @@
 namespace aekv {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
 constexpr int kD = 128;
-constexpr int kTile = 128;             // sources per tile, 32 per wave
+constexpr int kTile = 32 * kWaves;     // sources per tile, 32 per wave
 constexpr int kKP = kD + 8;            // row pitch of the staged tile (bf16)
 constexpr int kMaxTilesPerSplit = 4;
 constexpr float kNegInf = -__builtin_inff();
@@ -54,9 +55,9 @@ struct QAttnMfmaArgs {
 constexpr size_t kOffK = 0;
 constexpr size_t kOffOk = kOffK + sizeof(uint16_t) * kTile * kKP;
 constexpr size_t kOffSt = kOffOk + sizeof(float) * kTile;
-constexpr size_t kOffIdx = kOffSt + sizeof(float) * 4 * 16 * 2;
+constexpr size_t kOffIdx = kOffSt + sizeof(float) * kWaves * 16 * 2;
 constexpr size_t kLds = kOffIdx + sizeof(int32_t) * kMaxTilesPerSplit * kTile;
-static_assert(sizeof(float) * 4 * 16 * kD <= kOffOk, "the wave merge reuses the staged tile");
+static_assert(sizeof(float) * kWaves * 16 * kD <= kOffOk, "the wave merge reuses the staged tile");
 
 __device__ __forceinline__ uint16_t bf16_bits(float v) { return static_cast<uint16_t>(pack_bf16x2(v, 0.0f) & 0xffffu); }
 
@@ -121,8 +122,8 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
   __syncthreads();
 
   // Staging of a tile: wave wv fills tile rows 32wv .. 32wv+31, four sources per pass (one per
-  // 16-lane group).  The loads of a tile are issued together (and the next tile's before this
-  // tile's matrix work); kind: 0 empty, 1 code row, 2 window row.
+  // 16-lane group).  The loads of a tile are issued together; kind: 0 empty, 1 code row, 2 window
+  // row.
   constexpr int NB = LaneCodes<BITS, kD>::NB;  // code bytes per lane (4 or 8)
   uint32_t raw[8][4];
   float rsc[8];
@@ -176,12 +177,11 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
     }
   };
 
-  if (t0 < t1) load_tile(t0);
 #pragma unroll 1
   for (int64_t t = t0; t < t1; ++t) {
+    load_tile(t);
     store_tile();
     __syncthreads();
-    if (t + 1 < t1) load_tile(t + 1);
 
     // ---- this wave's 32 keys: S^T = K Q^T, then O^T += V^T P^T ----
     // A fragments: kf[kb][ks] = K[key 32wv + 16kb + c16][dims 32ks + 8g .. +7]
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
     __syncthreads();  // every wave is done with the tile before it is restaged
   }
 
-  // ---- merge the four waves (and the sink, unless this is one split of several) ----
+  // ---- merge the waves (and the sink, unless this is one split of several) ----
   float* Ob = reinterpret_cast<float*>(lds);  // [wave][head][128]
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb)
@@ -261,29 +261,49 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
     stat[(wv * 16 + c16) * 2 + 1] = l_run;
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < H * kD; p += kThreads) {
-    const int h = p / kD, d = p % kD;
+  // per head (one thread each): M = max(sink, wave maxima), the waves' factors e^{m_w - M}, and
+  // the normaliser L; the factors replace the maxima in stat, 1/L (or L for a split) is kept aside
+  float* inv = okf;  // the source flags are no longer needed
+  if (threadIdx.x < H) {
+    const int h = threadIdx.x;
     float M = a.n_split == 1 ? a.sink[h] : kNegInf;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, stat[(w * 16 + h) * 2]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, stat[(w * 16 + h) * 2]);
     float L = a.n_split == 1 ? __expf(a.sink[h] - M) : 0.0f;
-    float acc = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < kWaves; ++w) {
       const float mw = stat[(w * 16 + h) * 2];
       const float f = mw == kNegInf ? 0.0f : __expf(mw - M);
       L = fmaf(f, stat[(w * 16 + h) * 2 + 1], L);
-      acc = fmaf(f, Ob[(w * 16 + h) * kD + d], acc);
+      stat[(w * 16 + h) * 2] = f;
     }
     if (a.n_split == 1) {
-      a.out[(b * H + h) * kD + d] = bf16_bits(acc / L);
+      inv[h] = 1.0f / L;
     } else {
       float* dst = a.part + ((b * a.n_split + split) * H + h) * (kD + 2);
-      if (d == 0) {
-        dst[0] = M;
-        dst[1] = L;
-      }
-      dst[2 + d] = acc;
+      dst[0] = M;
+      dst[1] = L;
+    }
+  }
+  __syncthreads();
+  // every output: 4 consecutive dims per thread
+  for (int p = threadIdx.x; p < H * (kD / 4); p += kThreads) {
+    const int h = p / (kD / 4), d4 = 4 * (p % (kD / 4));
+    f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = stat[(w * 16 + h) * 2];
+      const f32x4_t o = *reinterpret_cast<const f32x4_t*>(Ob + (w * 16 + h) * kD + d4);
+      acc = f32x4_t{fmaf(f, o[0], acc[0]), fmaf(f, o[1], acc[1]), fmaf(f, o[2], acc[2]), fmaf(f, o[3], acc[3])};
+    }
+    if (a.n_split == 1) {
+      const float r = inv[h];
+      const uint2 v = make_uint2(pack_bf16x2(acc[0] * r, acc[1] * r), pack_bf16x2(acc[2] * r, acc[3] * r));
+      *reinterpret_cast<uint2*>(a.out + (b * H + h) * kD + d4) = v;
+    } else {
+      float* dst = a.part + ((b * a.n_split + split) * H + h) * (kD + 2) + 2 + d4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[e] = acc[e];
     }
   }
 }
