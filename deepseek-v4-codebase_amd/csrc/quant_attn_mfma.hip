@@ -1,23 +1,27 @@
 // Decode-step sink attention over TurboQuant-coded shared K=V blocks + a bf16 window, head_dim 128,
-// with the QK^T and PV contractions on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16).
+// entirely on the matrix cores.
 //
 // Reference: aether_2b/serving.py:507-525 (HCA: every visible block) and :597-625 (CSA: the
 // indexer's selected blocks), both followed by the sink attention of aether_pipeline/serving.py:
 // 99-130 over [dequant(blocks), window] with K = V (serving.py:52-53).
 //
-// One workgroup (8 waves) owns a row (or a contiguous split of a long row's sources).  Per tile of 256
-// sources it decodes the gathered code rows exactly (same code path as PolarQuant.decode, rounded
-// to bf16 like the engine's dequantised cache) or copies window rows into an LDS tile, row-major.
-// Wave w owns tile keys 32w..32w+31 and works transposed, so that each lane owns one head
-// (lane & 15):
-//   S^T = K Q^T        A = tile rows (16 keys x 32 dims), B = the row's queries;
+// A workgroup (8 waves) owns a row, or a split of 1024 of a long row's sources.  Each wave takes
+// groups of 32 sources (two blocks of 16 keys) and works in registers only:
+//   dequantise  y = H128 codes on the int8 matrix cores (v_mfma_i32_16x16x64_i8), exact in int32:
+//               H128 = [[H64, H64], [H64, -H64]], so two H64 products per 64-code half suffice;
+//               4-bit codes enter as 16*code (the nibble shifted to the top of its byte).  Then
+//               K = bf16(y * scale * c) — the engine attends the bf16 dequantised cache; this
+//               differs from PolarQuant.decode's fp32 butterfly rounding by at most one bf16 ulp,
+//               and only where y*scale*c lies within ~1e-7 relative of a bf16 rounding boundary.
+//               The +-1 diagonal is folded into the queries and the output (bf16 rounding is
+//               sign-symmetric), window rows get it on load.
+//   S^T = K Q^T  (v_mfma_f32_16x16x32_bf16): A = the keys as decoded (lane = key), B = queries;
+//               each lane then owns one head (lane & 15).
 //   online softmax of the lane's head over its 8 keys and across the 4 lane groups;
-//   V^T blocks         the same A fragments times a 0/1 column selector (exact), which lands the
-//                      values in the A layout of the next product with no LDS transpose;
-//   O^T += V^T P^T     B = P^T straight from the softmax registers (bf16, the usual operand).
-// The keys of a lane group appear in the same order in V^T and P^T, which is all the product
-// needs.  The four waves' (max, sum, acc) are merged at the end; the sink joins the normaliser
-// once, there or in the split combine.
+//   V^T blocks   the same K fragments times a 0/1 column selector (exact), landing in the A layout
+//               of O^T += V^T P^T, whose B = P^T comes straight from the softmax registers.
+// Waves never share data inside the loop; their (max, sum, acc) are merged at the end, where the
+// sink joins the normaliser once (or in the split combine).
 #include <mutex>
 
 #include "tq_device.h"
@@ -28,13 +32,13 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kD = 128;
-constexpr int kTile = 32 * kWaves;     // sources per tile, 32 per wave
-constexpr int kKP = kD + 8;            // row pitch of the staged tile (bf16)
-constexpr int kMaxTilesPerSplit = 4;
+constexpr int kGroup = 32;                    // sources per wave step
+constexpr int kSplitSrc = 1024;               // sources per workgroup when a row is split
 constexpr float kNegInf = -__builtin_inff();
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) int i32x4_t;
 
 struct QAttnMfmaArgs {
   const uint16_t* q;      // [B, H, 128] bf16
@@ -45,174 +49,242 @@ struct QAttnMfmaArgs {
   const float* sink;      // [H]
   const float* diag;      // [128]
   int64_t S, K, W, n_comp, n_src;
-  int H, n_split, tiles_per_split;
+  int H, n_split;
   float sm_scale, wscale;
   float* part;            // [B, n_split, H, 2 + 128] (split runs only)
   uint16_t* out;          // [B, H, 128] bf16
 };
 
-// LDS layout (bytes): staged tile | source flags | wave stats | the split's selected block ids
-constexpr size_t kOffK = 0;
-constexpr size_t kOffOk = kOffK + sizeof(uint16_t) * kTile * kKP;
-constexpr size_t kOffSt = kOffOk + sizeof(float) * kTile;
-constexpr size_t kOffIdx = kOffSt + sizeof(float) * kWaves * 16 * 2;
-constexpr size_t kLds = kOffIdx + sizeof(int32_t) * kMaxTilesPerSplit * kTile;
-static_assert(sizeof(float) * kWaves * 16 * kD <= kOffOk, "the wave merge reuses the staged tile");
+// LDS layout (bytes): wave outputs for the merge | wave stats | per-head factors | block ids
+constexpr size_t kOffOb = 0;
+constexpr size_t kOffSt = kOffOb + sizeof(float) * kWaves * 16 * kD;
+constexpr size_t kOffInv = kOffSt + sizeof(float) * kWaves * 16 * 2;
+constexpr size_t kOffIdx = kOffInv + sizeof(float) * 16;
+constexpr size_t kLds = kOffIdx + sizeof(int32_t) * kSplitSrc;
 
 __device__ __forceinline__ uint16_t bf16_bits(float v) { return static_cast<uint16_t>(pack_bf16x2(v, 0.0f) & 0xffffu); }
+
+// Code index (within a 64-code half) of element p of lane group g's 16-byte operand, matching how
+// the codes are loaded: 8-bit in byte order; 4-bit as (w << 4) & 0xF0F0F0F0 (even codes) and
+// w & 0xF0F0F0F0 (odd codes) for each of the lane's two code dwords.
+template <int BITS>
+__device__ __forceinline__ int code_index(int g, int p) {
+  if constexpr (BITS == 8) {
+    return 16 * g + p;
+  } else {
+    const int q4 = p >> 2, r = p & 3;
+    return 16 * g + 8 * (q4 >> 1) + 2 * r + (q4 & 1);
+  }
+}
 
 template <int BITS>
 __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
-  uint16_t* Kt = reinterpret_cast<uint16_t*>(lds + kOffK);
-  float* okf = reinterpret_cast<float*>(lds + kOffOk);
+  float* Ob = reinterpret_cast<float*>(lds + kOffOb);    // [wave][head][128]
   float* stat = reinterpret_cast<float*>(lds + kOffSt);  // [wave][head][m, l]
-  constexpr int RB = BITS == 8 ? kD : kD / 2;
+  float* inv = reinterpret_cast<float*>(lds + kOffInv);  // [head]
+  int32_t* sidx = reinterpret_cast<int32_t*>(lds + kOffIdx);
+  constexpr int RB = BITS == 8 ? kD : kD / 2;   // code bytes per row
+  constexpr int HB = RB / 2;                    // code bytes per 64-code half
 
   const int64_t b = blockIdx.y;
   const int split = blockIdx.x;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int H = a.H;
 
-  // queries as the A operand: lane (head c16, group g) holds dims 32ks + 8g .. +7
-  bf16x8_t qa[4];
+  // this workgroup's sources [src0, src1); the selected block ids go to LDS (-1: skipped)
+  const int64_t src0 = static_cast<int64_t>(split) * kSplitSrc;
+  const int64_t src1 = min<int64_t>(a.n_src, src0 + kSplitSrc);
+  if (a.sel) {
+    const int64_t nsel = min<int64_t>(src1, a.n_comp) - src0;
+    for (int64_t i = threadIdx.x; i < nsel; i += kThreads) {
+      const int64_t blk = a.sel[b * a.K + src0 + i];
+      sidx[i] = blk >= 0 && blk < a.S ? static_cast<int32_t>(blk) : -1;
+    }
+  }
+
+  // The lane's 32 dims, for every key it holds: element j of k-step ks (bf16x8) is dim
+  // 16*(2ks + (j >> 2)) + 4g + (j & 3).  dsign: the diagonal's sign bits for those dims, per
+  // packed bf16 pair (dword e of k-step ks).
+  uint32_t dsign[4][4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d0 = 16 * (2 * ks + (e >> 1)) + 4 * g + 2 * (e & 1);
+      dsign[ks][e] = (a.diag[d0] < 0.0f ? 0x8000u : 0u) | (a.diag[d0 + 1] < 0.0f ? 0x80000000u : 0u);
+    }
+  // queries (times the diagonal) as the B operand of S^T: lane (head c16), the lane's dims
+  bf16x8_t qb[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (c16 < H) v = *reinterpret_cast<const uint4*>(a.q + (b * H + c16) * kD + 32 * ks + 8 * g);
-    qa[ks] = __builtin_bit_cast(bf16x8_t, v);
+    uint2 lo = make_uint2(0u, 0u), hi = make_uint2(0u, 0u);
+    if (c16 < H) {
+      const uint16_t* qr = a.q + (b * H + c16) * kD + 4 * g;
+      lo = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks));
+      hi = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks + 1));
+    }
+    qb[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x ^ dsign[ks][0], lo.y ^ dsign[ks][1], hi.x ^ dsign[ks][2],
+                                                     hi.y ^ dsign[ks][3]));
   }
-  // decode: the 16 lanes of group g hold dims 8*c16 .. +7 of one source
-  float dg[8];
+  // H64 rows 16a + c16 as int8 +-1 over the lane's code indices (the A operand of the dequantise)
+  i32x4_t hA[4];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) dg[e] = a.diag[8 * c16 + e];
-
-  // softmax state and output of head c16 (replicated over the four lane groups)
-  float m_run = kNegInf, l_run = 0.0f;
-  f32x4_t O[8];
+  for (int a4 = 0; a4 < 4; ++a4)
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  // 0/1 selectors: esel[h] (lane column c16, element j of group g) = 1 iff 8g + j == c16 + 16h
+    for (int dw = 0; dw < 4; ++dw) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int by = 0; by < 4; ++by) {
+        const int c = code_index<BITS>(g, 4 * dw + by);
+        const bool neg = __builtin_popcount(static_cast<unsigned>((16 * a4 + c16) & c)) & 1;
+        word |= (neg ? 0xFFu : 0x01u) << (8 * by);
+      }
+      hA[a4][dw] = static_cast<int>(word);
+    }
+  // 0/1 selectors: esel[h] (lane column c16, element j of group g) = 1 iff g == c16 >> 2 and
+  // j == (c16 & 3) + 4h, i.e. column c16 picks dim 16*(2ks + h) + c16 of k-step ks
   bf16x8_t esel[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int k0 = 8 * g + 2 * e;
-      w[e] = (k0 == c16 + 16 * h ? 0x3F80u : 0u) | (k0 + 1 == c16 + 16 * h ? 0x3F800000u : 0u);
+      const int j0 = 2 * e;
+      const bool mine = g == (c16 >> 2);
+      w[e] = (mine && j0 == (c16 & 3) + 4 * h ? 0x3F80u : 0u) | (mine && j0 + 1 == (c16 & 3) + 4 * h ? 0x3F800000u : 0u);
     }
     esel[h] = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
   }
+  __syncthreads();  // sidx
 
-  const int64_t n_tiles = (a.n_src + kTile - 1) / kTile;
-  const int64_t t0 = static_cast<int64_t>(split) * a.tiles_per_split;
-  const int64_t t1 = min<int64_t>(n_tiles, t0 + a.tiles_per_split);
-
-  // block ids of this split's selected sources (-1: index outside [0, S), skipped)
-  int32_t* sidx = reinterpret_cast<int32_t*>(lds + kOffIdx);
-  const int64_t src0 = t0 * kTile;
-  if (a.sel) {
-    const int64_t nsel = min<int64_t>(t1 * kTile, a.n_comp) - src0;
-    for (int64_t i = threadIdx.x; i < nsel; i += kThreads) {
-      const int64_t blk = a.sel[b * a.K + src0 + i];
-      sidx[i] = blk >= 0 && blk < a.S ? static_cast<int32_t>(blk) : -1;
-    }
-  }
-  __syncthreads();
-
-  // Staging of a tile: wave wv fills tile rows 32wv .. 32wv+31, four sources per pass (one per
-  // 16-lane group).  The loads of a tile are issued together; kind: 0 empty, 1 code row, 2 window
-  // row.
-  constexpr int NB = LaneCodes<BITS, kD>::NB;  // code bytes per lane (4 or 8)
-  uint32_t raw[8][4];
-  float rsc[8];
-  int kind[8];
-  auto load_tile = [&](int64_t t) {
+  // softmax state and output of head c16 (replicated over the four lane groups)
+  float m_run = kNegInf, l_run = 0.0f;
+  f32x4_t O[8];
 #pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const int64_t si = t * kTile + 32 * wv + 4 * p + g;
-      kind[p] = 0;
-      raw[p][0] = raw[p][1] = raw[p][2] = raw[p][3] = 0u;
-      rsc[p] = 0.0f;
-      if (si < a.n_comp) {
-        const int64_t blk = a.sel ? sidx[si - src0] : si;
-        if (blk >= 0) {
-          kind[p] = 1;
-          const uint8_t* row = a.codes + (b * a.S + blk) * RB + c16 * NB;
-          if constexpr (NB == 4) {
-            raw[p][0] = *reinterpret_cast<const uint32_t*>(row);
-          } else {
-            const uint2 v = *reinterpret_cast<const uint2*>(row);
-            raw[p][0] = v.x;
-            raw[p][1] = v.y;
-          }
-          rsc[p] = a.scale[b * a.S + blk];
-        }
-      } else if (si < a.n_src) {
-        kind[p] = 2;
-        const uint4 v = *reinterpret_cast<const uint4*>(a.win + (b * a.W + (si - a.n_comp)) * kD + 8 * c16);
-        raw[p][0] = v.x;
-        raw[p][1] = v.y;
-        raw[p][2] = v.z;
-        raw[p][3] = v.w;
-      }
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const int jj = 32 * wv + 4 * p + g;
-      uint32_t w4[4] = {raw[p][0], raw[p][1], raw[p][2], raw[p][3]};
-      if (kind[p] == 1) {  // uniform within the 16-lane group (one source)
-        typename LaneCodes<BITS, kD>::type cb;
-        __builtin_memcpy(cb.b, raw[p], NB);
-        float v[8];
-        decode_lane_bytes<BITS, kD>(cb, rsc[p], c16, dg, a.wscale, v);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w4[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-      }
-      *reinterpret_cast<uint4*>(Kt + jj * kKP + 8 * c16) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-      if (c16 == 0) okf[jj] = kind[p] != 0 ? 1.0f : 0.0f;
-    }
-  };
+  for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const float kscale_unit = (BITS == 4 ? 1.0f / 16.0f : 1.0f) * a.wscale;
 
+  const int n_groups = static_cast<int>((src1 - src0 + kGroup - 1) / kGroup);
 #pragma unroll 1
-  for (int64_t t = t0; t < t1; ++t) {
-    load_tile(t);
-    store_tile();
-    __syncthreads();
-
-    // ---- this wave's 32 keys: S^T = K Q^T, then O^T += V^T P^T ----
-    // A fragments: kf[kb][ks] = K[key 32wv + 16kb + c16][dims 32ks + 8g .. +7]
+  for (int G = wv; G < n_groups; G += kWaves) {
     bf16x8_t kf[2][4];
+    bool okk[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb) {
+      // lane (key c16 of block kb): its source, code bytes (two halves) or window dims
+      const int64_t si = src0 + static_cast<int64_t>(G) * kGroup + 16 * kb + c16;
+      int kind = 0;  // 0 empty, 1 code row, 2 window row
+      int64_t blk = -1;
+      if (si < a.n_comp) {
+        blk = a.sel ? sidx[si - src0] : si;
+        kind = blk >= 0 ? 1 : 0;
+      } else if (si < src1) {
+        kind = 2;
+      }
+      okk[kb] = kind != 0;
+      uint32_t cw[2][BITS == 8 ? 4 : 2];
+      float fk = 0.0f;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        kf[kb][ks] = __builtin_bit_cast(
-            bf16x8_t, *reinterpret_cast<const uint4*>(Kt + (32 * wv + 16 * kb + c16) * kKP + 32 * ks + 8 * g));
-    // st[kb][i] = S[head c16][key 32wv + 16kb + 4g + i]
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < (BITS == 8 ? 4 : 2); ++e) cw[hh][e] = 0u;
+      uint2 wv2[4][2];
+      if (kind == 1) {
+        const uint8_t* row = a.codes + (b * a.S + blk) * RB;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          if constexpr (BITS == 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(row + HB * hh + 16 * g);
+            cw[hh][0] = v.x;
+            cw[hh][1] = v.y;
+            cw[hh][2] = v.z;
+            cw[hh][3] = v.w;
+          } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(row + HB * hh + 8 * g);
+            cw[hh][0] = v.x;
+            cw[hh][1] = v.y;
+          }
+        }
+        fk = a.scale[b * a.S + blk] * kscale_unit;
+      }
+      if (kind == 2) {
+        const uint16_t* wr = a.win + (b * a.W + (si - a.n_comp)) * kD + 4 * g;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          wv2[ks][0] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks));
+          wv2[ks][1] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks + 1));
+        }
+      }
+      // y = H64 codes per half (all lanes take part; lanes without a code row supply zeros)
+      i32x4_t P[2][4];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        i32x4_t Bop;
+        if constexpr (BITS == 8) {
+          Bop = i32x4_t{static_cast<int>(cw[hh][0]), static_cast<int>(cw[hh][1]), static_cast<int>(cw[hh][2]),
+                        static_cast<int>(cw[hh][3])};
+        } else {
+          const uint32_t x = cw[hh][0], y = cw[hh][1];
+          Bop = i32x4_t{static_cast<int>((x << 4) & 0xF0F0F0F0u), static_cast<int>(x & 0xF0F0F0F0u),
+                        static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
+        }
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4)
+          P[hh][a4] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hA[a4], Bop, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+      }
+      // P[hh][a4][i] = (H64 codes_half_hh)[16*a4 + 4g + i]; dims 16*blk + 4g + i of the full
+      // transform: blk < 4 -> P[0] + P[1], blk >= 4 -> P[0] - P[1]
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        uint32_t w4[4];
+        if (kind == 2) {
+          w4[0] = wv2[ks][0].x ^ dsign[ks][0];
+          w4[1] = wv2[ks][0].y ^ dsign[ks][1];
+          w4[2] = wv2[ks][1].x ^ dsign[ks][2];
+          w4[3] = wv2[ks][1].y ^ dsign[ks][3];
+        } else {
+          float v[8];
+#pragma unroll
+          for (int hv = 0; hv < 2; ++hv) {
+            const int blk8 = 2 * ks + hv;
+            const int a4 = blk8 & 3;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int y = blk8 < 4 ? P[0][a4][i] + P[1][a4][i] : P[0][a4][i] - P[1][a4][i];
+              v[4 * hv + i] = static_cast<float>(y) * fk;
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w4[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+        }
+        kf[kb][ks] = __builtin_bit_cast(bf16x8_t, make_uint4(w4[0], w4[1], w4[2], w4[3]));
+      }
+    }
+
+    // st[kb][i] = S[head c16][key 16kb + 4g + i of the group]
     f32x4_t st[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       st[kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb][ks], qa[ks], st[kb], 0, 0, 0);
+      for (int ks = 0; ks < 4; ++ks) st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb][ks], qb[ks], st[kb], 0, 0, 0);
     }
-    // online softmax of head c16 over the wave's keys (8 per lane, 4 lane groups)
     float pr[2][4];
     {
       float lg[2][4];
       float tm = kNegInf;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb) {
+        // okk[kb] belongs to key c16, so bit 4g+i of its ballot is the validity of row 4g+i
+        const uint64_t okm = __builtin_amdgcn_ballot_w64(okk[kb]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const bool ok = okf[32 * wv + 16 * kb + 4 * g + i] != 0.0f;
+          const bool ok = (okm >> (4 * g + i)) & 1u;
           lg[kb][i] = ok ? st[kb][i] * a.sm_scale : kNegInf;
           tm = fmaxf(tm, lg[kb][i]);
         }
+      }
       tm = fmaxf(tm, xor_lane<16>(tm));
       tm = fmaxf(tm, xor_lane<32>(tm));
       const float mnew = fmaxf(m_run, tm);
@@ -238,21 +310,19 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
                              pack_bf16x2(pr[1][0], pr[1][1]), pack_bf16x2(pr[1][2], pr[1][3])));
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) {
-      // V columns 16nb .. 16nb+15 of the 32 keys: K rows times a 0/1 selector (exact)
+      // V columns 16nb .. 16nb+15 of the 32 keys: K fragments times a 0/1 selector (exact)
       const f32x4_t v0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[0][nb >> 1], esel[nb & 1], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
       const f32x4_t v1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[1][nb >> 1], esel[nb & 1], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
       // A = V^T: lane (dim 16nb + c16), element 4kb + i <-> key 16kb + 4g + i (same order as pb)
       const bf16x8_t va = __builtin_bit_cast(
           bf16x8_t, make_uint4(pack_bf16x2(v0[0], v0[1]), pack_bf16x2(v0[2], v0[3]), pack_bf16x2(v1[0], v1[1]),
                                pack_bf16x2(v1[2], v1[3])));
-      // O^T[nb][i] = O[head c16][dim 16nb + 4g + i]
+      // O^T[nb][i] = O[head c16][dim 16nb + 4g + i] (times diag, removed at the end)
       O[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, O[nb], 0, 0, 0);
     }
-    __syncthreads();  // every wave is done with the tile before it is restaged
   }
 
   // ---- merge the waves (and the sink, unless this is one split of several) ----
-  float* Ob = reinterpret_cast<float*>(lds);  // [wave][head][128]
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb)
     *reinterpret_cast<f32x4_t*>(Ob + (wv * 16 + c16) * kD + 16 * nb + 4 * g) = O[nb];
@@ -263,7 +333,6 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
   __syncthreads();
   // per head (one thread each): M = max(sink, wave maxima), the waves' factors e^{m_w - M}, and
   // the normaliser L; the factors replace the maxima in stat, 1/L (or L for a split) is kept aside
-  float* inv = okf;  // the source flags are no longer needed
   if (threadIdx.x < H) {
     const int h = threadIdx.x;
     float M = a.n_split == 1 ? a.sink[h] : kNegInf;
@@ -286,7 +355,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
     }
   }
   __syncthreads();
-  // every output: 4 consecutive dims per thread
+  // every output: 4 consecutive dims per thread; the diagonal folded into the keys comes off here
   for (int p = threadIdx.x; p < H * (kD / 4); p += kThreads) {
     const int h = p / (kD / 4), d4 = 4 * (p % (kD / 4));
     f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -296,6 +365,8 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
       const f32x4_t o = *reinterpret_cast<const f32x4_t*>(Ob + (w * 16 + h) * kD + d4);
       acc = f32x4_t{fmaf(f, o[0], acc[0]), fmaf(f, o[1], acc[1]), fmaf(f, o[2], acc[2]), fmaf(f, o[3], acc[3])};
     }
+    const float4 dg = *reinterpret_cast<const float4*>(a.diag + d4);
+    acc = f32x4_t{acc[0] * dg.x, acc[1] * dg.y, acc[2] * dg.z, acc[3] * dg.w};
     if (a.n_split == 1) {
       const float r = inv[h];
       const uint2 v = make_uint2(pack_bf16x2(acc[0] * r, acc[1] * r), pack_bf16x2(acc[2] * r, acc[3] * r));
@@ -335,16 +406,10 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_combine_kernel(QAttn
 
 bool quant_attn_mfma_supported(int64_t H, int64_t D) { return D == kD && H >= 1 && H <= 16; }
 
-// Splits: one workgroup per row up to kMaxTilesPerSplit tiles (no combine); longer rows take
-// kMaxTilesPerSplit tiles per workgroup and the split combine.
-static int64_t split_count(int64_t n_tiles, int64_t& tiles_per_split) {
-  tiles_per_split = n_tiles < kMaxTilesPerSplit ? n_tiles : kMaxTilesPerSplit;
-  return tiles_per_split > 0 ? ceil_div(n_tiles, tiles_per_split) : 1;
-}
-
+// Rows of up to kSplitSrc sources take one workgroup; longer rows one per kSplitSrc sources plus
+// the split combine.
 size_t quant_attn_mfma_workspace(int64_t B, int64_t H, int64_t n_src) {
-  int64_t tps = 1;
-  const int64_t n_split = split_count(ceil_div(n_src, kTile), tps);
+  const int64_t n_split = n_src > 0 ? ceil_div(n_src, kSplitSrc) : 1;
   return n_split > 1 ? align_up(static_cast<size_t>(B * n_split * H * (kD + 2)) * 4, 256) : 0;
 }
 
@@ -366,11 +431,9 @@ int launch_quant_attn_mfma(const void* q, const void* codes, const float* scale,
   a.n_comp = all_blocks ? S : K;
   a.n_src = a.n_comp + W;
   a.H = static_cast<int>(H);
-  int64_t tps = 1;
-  const int64_t n_split = split_count(ceil_div(a.n_src, kTile), tps);
+  const int64_t n_split = a.n_src > 0 ? ceil_div(a.n_src, kSplitSrc) : 1;
   if (n_split > 65535) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many sources", who);
   a.n_split = static_cast<int>(n_split);
-  a.tiles_per_split = static_cast<int>(tps);
   a.sm_scale = softmax_scale;
   a.wscale = wht_scale(kD);
   a.part = static_cast<float*>(ws);
