@@ -36,7 +36,7 @@ constexpr int kThreads = 256;
 constexpr int kSelThreads = 1024;
 constexpr int kHistBins = 4096;      // top 12 bits of the order key
 constexpr int kCandCap = 4096;       // candidates a row's workgroup collects in LDS (fast route)
-constexpr int kSortCap = 2048;       // at most this many candidates are sorted outright
+constexpr int kSortCap = 1024;       // at most this many candidates are sorted outright (one per thread)
 constexpr int kMaxMfmaK = 1024;
 constexpr int kMaxNrb = 4;           // row blocks of 4 heads (IH <= 16)
 constexpr int64_t kMaxKeys = int64_t(1) << 30;
@@ -99,6 +99,21 @@ __device__ __forceinline__ int cmap(int ks, int g, int p) {
     const int q4 = p >> 2, r = p & 3;
     return 64 * ks + 16 * g + 8 * (q4 >> 1) + 2 * r + (q4 & 1);
   }
+}
+
+// 64-bit lane exchange with partner lane ^ j (j a power of two below 64, constant after unrolling).
+__device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v, int j) {
+  float lo = __builtin_bit_cast(float, static_cast<uint32_t>(v));
+  float hi = __builtin_bit_cast(float, static_cast<uint32_t>(v >> 32));
+  switch (j) {
+    case 1: lo = xor_lane<1>(lo); hi = xor_lane<1>(hi); break;
+    case 2: lo = xor_lane<2>(lo); hi = xor_lane<2>(hi); break;
+    case 4: lo = xor_lane<4>(lo); hi = xor_lane<4>(hi); break;
+    case 8: lo = xor_lane<8>(lo); hi = xor_lane<8>(hi); break;
+    case 16: lo = xor_lane<16>(lo); hi = xor_lane<16>(hi); break;
+    default: lo = xor_lane<32>(lo); hi = xor_lane<32>(hi); break;
+  }
+  return (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, hi)) << 32) | __builtin_bit_cast(uint32_t, lo);
 }
 
 // Threshold search over a histogram: the largest bin t with sum_{u >= t} h[u] >= need, and
@@ -527,41 +542,41 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
   const int n = fast ? static_cast<int>(n_cand) : 0;
 
   // ---- 2a. up to kSortCap candidates (the usual case): sort them all, emit the first kk ----
+  // Wave w sorts candidates 64w .. 64w+63 in registers (bitonic network over lane exchanges);
+  // the runs go to LDS and every candidate's final position is its index in its run plus, for
+  // each other run, the number of smaller words there (binary search).  Words are distinct.
   if (fast && n <= kSortCap) {
-    int P = 64;
-    while (P < n) P <<= 1;
-    uint64_t w[kSortCap / kSelThreads];
+    uint64_t w = tid < n ? sort_word(ck[tid], ci[tid]) : ~0ull;
 #pragma unroll
-    for (int r = 0; r < kSortCap / kSelThreads; ++r) {
-      const int i = tid + r * kSelThreads;
-      w[r] = i < n ? sort_word(ck[i], ci[i]) : ~0ull;
-    }
-    __syncthreads();
+    for (int kq = 2; kq <= 64; kq <<= 1) {
 #pragma unroll
-    for (int r = 0; r < kSortCap / kSelThreads; ++r) {
-      const int i = tid + r * kSelThreads;
-      if (i < P) cbuf[i] = w[r];
-    }
-    __syncthreads();
-    for (int size = 2; size <= P; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int i = tid; i < P / 2; i += kSelThreads) {
-          const int pos = 2 * i - (i & (stride - 1));
-          const int partner = pos + stride;
-          const bool up = (pos & size) == 0;
-          const uint64_t x = cbuf[pos], y = cbuf[partner];
-          if ((x > y) == up) {
-            cbuf[pos] = y;
-            cbuf[partner] = x;
-          }
-        }
-        __syncthreads();
+      for (int j = kq >> 1; j > 0; j >>= 1) {
+        const uint64_t o = xor_lane_u64(w, j);
+        const bool keep_min = ((lane & j) == 0) == ((lane & kq) == 0);
+        w = keep_min ? (o < w ? o : w) : (o > w ? o : w);
       }
     }
-    for (int i = tid; i < static_cast<int>(kk); i += kSelThreads) {
-      const uint64_t v = cbuf[i];
-      orow[i] = static_cast<int64_t>(static_cast<uint32_t>(v & 0xffffffffu));
-      if (srow) srow[i] = order_key_inv(~static_cast<uint32_t>(v >> 32));
+    __syncthreads();  // ck/ci are read
+    cbuf[tid] = w;    // run wv at cbuf[64 wv .. 64 wv + 63], ascending
+    __syncthreads();
+    const int n_runs = (n + 63) >> 6;
+    if (tid < n) {
+      uint32_t pos = static_cast<uint32_t>(lane);
+#pragma unroll
+      for (int r = 0; r < kSortCap / 64; ++r) {
+        if (r >= n_runs || r == wv) continue;
+        const uint64_t* run = cbuf + 64 * r;
+        int lo = 0;  // number of words in run r below w (the steps reach 63; the last compare 64)
+#pragma unroll
+        for (int step = 32; step > 0; step >>= 1)
+          if (run[lo + step - 1] < w) lo += step;
+        if (run[lo] < w) ++lo;
+        pos += static_cast<uint32_t>(lo);
+      }
+      if (pos < kk) {
+        orow[pos] = static_cast<int64_t>(static_cast<uint32_t>(w & 0xffffffffu));
+        if (srow) srow[pos] = order_key_inv(~static_cast<uint32_t>(w >> 32));
+      }
     }
     return;
   }
