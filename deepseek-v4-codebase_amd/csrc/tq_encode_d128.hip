@@ -4,28 +4,34 @@
 // aether_2b/turbo_quant.py:127-166 (rot = _wht(x*diag); m = max(max|rot|, 1e-8); scale = m/7;
 // q = clamp(rne(rot/m*7)); nibble pack), with about half the VALU work:
 //
-// * Layout.  A wave handles 16 vectors; lane l = 16*g + v holds elements [32g, 32g+32) of vector
-//   v (four 16-byte loads).  Butterfly stages h = 1..16 run in registers.  Stage h = 32 pairs lane
-//   rows g0 = 0/1 and stage h = 64 pairs lane halves g1 = 0/1: one v_permlane16_swap /
-//   v_permlane32_swap exchanges two registers so that every lane ends up holding (lower, upper)
-//   of one pair and applies the same add/sub.  After both swaps lane (g1, g0) holds elements
-//   e = 64*R4 + 32*g1 + 16*g0 + (R & 15) in register R, so its codes are two runs of 8 bytes.
-// * x * diag and the first butterfly stage: per packed bf16 word, lo = w << 16, hi*diag = the
-//   high half with its sign flipped by diag (one bitwise op), and a + b / a - b =
-//   fma(lo, diag_lo, +-hi*diag) — an exact product and one rounding, i.e. the reference's fp32
-//   add/sub.  (v_dot2_f32_bf16 computes the same sum but does not round it like an fp32 add when
-//   the two halves are more than 2^16 apart, so it is not used.)
+// * Layout.  A wave handles 16 vectors; lane l = 4v + g holds elements [32g, 32g+32) of vector v
+//   of its group: a wave reads 4 KiB and writes 1 KiB of codes, contiguous, 64 and 16 bytes per
+//   lane.  Butterfly stages h = 1..16 run in registers; stage h = 32 pairs lanes g ^ 1 and stage
+//   h = 64 lanes g ^ 2 of the same quad.
+// * Cross-lane stages.  Each is one v_fmac_f32 per element whose src0 reads the partner through
+//   DPP quad_perm: own + s * partner with s = -1 on the upper lane, i.e. x + y on the lower lane
+//   and y - x = -(x - y) on the upper one (an exact product and one rounding; RNE is symmetric, so
+//   the magnitude is the reference's x - y bit for bit).  After both stages lane g holds its
+//   elements times sigma = (-1)^(g0 + g1); the sign is folded into the quantiser's factor.
+// * x * diag and the first butterfly stage: per packed bf16 word w and its diag sign mask M (bit
+//   31: the high element's diag is negative, bit 15: the low one's), lo*diag = (w + M) << 16 (one
+//   v_add_lshl_u32: adding 0x8000 flips bit 15 and the carry out of it is shifted away),
+//   hi*diag = (w ^ M) & 0xFFFF0000 (one v_bitop3), and the reference's fp32 add and sub of the
+//   two.  (v_dot2_f32_bf16 computes the same sum but does not round it like an fp32 add when the
+//   two halves are more than 2^16 apart, so it is not used.)
 // * Scale folding.  max|rot| = RN(c * max|raw|) because rounding is monotonic (raw = butterfly
-//   output before the * c, c = fp32(128^-0.5)), so the per-element work uses the exact product
-//   P = raw * K with K = RN(RN(7c) * rcp(m)) (v_rcp_f32, relative error <= 2^-23) instead of
-//   RN(RN(RN(raw*c)/m)*7).  |P/T - 1| <= 4 * 2^-24 and |t_exact/T - 1| <= 3 * 2^-24 for
-//   T = raw*7c/m, |T| <= 7, so |P - t_exact| <= 49 * 2^-24 < 2.95e-6, and
-//   rne(P) = rne(t_exact) unless P lies within that distance of a half-integer.  The kernel checks
-//   max |P - rne(P)| over the wave and, if any element is within kDelta = 5e-6 of a tie, redoes
-//   the wave's elements with the reference's exact operation sequence (~1e-5 per element).
-// * rne(P) and the nibble come from one FMA with the magic constant M8 = 1.5 * 2^23 + 8:
-//   RN(raw*K + M8) = M8 + rne(P), whose low byte is rne(P) + 8 (offset binary); a nibble pair is
-//   one shift-or and one XOR with 0x88888888 per dword restores two's complement.
+//   output before the * c, c = fp32(128^-0.5)), so the per-element work uses the exact products
+//   raw * K-, raw * K+ with K+- = K (1 +- 2^-20), K = RN(RN(7c) * rcp(m)) (v_rcp_f32, relative
+//   error <= 2^-23), instead of t = RN(RN(RN(raw*c)/m)*7).  |K / (7c/m) - 1| <= 2^-22 and
+//   |t / (raw*7c/m) - 1| <= 3 * 2^-24, so t lies between raw*K- and raw*K+, and since rne is
+//   monotonic, rne(raw*K-) == rne(raw*K+) implies rne(t) equals both.  A wave in which any element
+//   has the two apart (a tie within ~7 * 2^-19 of the product) re-encodes its 16 vectors with the
+//   reference's exact operation sequence (about 1e-5 of the elements on Gaussian data).
+// * rne and the nibble come from one FMA with the magic constant M8 = 1.5 * 2^23 + 8:
+//   RN(p + M8) = M8 + rne(p) for |p| <= 2^22, whose low byte is rne(p) + 8 (offset binary); a
+//   nibble pair is one shift-or and one XOR with 0x88888888 per dword restores two's complement.
+// * The next group's 4 KiB are requested before the current group is transformed, so every wave
+//   keeps one group of loads in flight while it computes.
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
@@ -36,21 +42,43 @@ namespace aekv {
 namespace {
 
 constexpr int kThreads = 256;
+#ifndef AEKV_ENC4_MAX_BLOCKS
+#define AEKV_ENC4_MAX_BLOCKS 2048
+#endif
+#ifndef AEKV_ENC4_MIN_WAVES
+#define AEKV_ENC4_MIN_WAVES 4  // waves per SIMD the register allocation must allow
+#endif
+constexpr int64_t kMaxBlocks = AEKV_ENC4_MAX_BLOCKS;  // grid-stride beyond this many workgroups
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 constexpr float kMagic8 = 12582920.0f;  // 1.5 * 2^23 + 8: RN(t + kMagic8) = kMagic8 + rne(t), ulp 1
-constexpr float kDelta = 5e-6f;
 
-__device__ __forceinline__ void swap16(float& a, float& b) {
-  auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), false,
-                                            false);
-  a = __builtin_bit_cast(float, static_cast<uint32_t>(r[0]));
-  b = __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
-}
-
-__device__ __forceinline__ void swap32(float& a, float& b) {
-  auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), false,
-                                            false);
-  a = __builtin_bit_cast(float, static_cast<uint32_t>(r[0]));
-  b = __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+// Stages h = 32 and h = 64 on eight registers: a += s * a(partner), the partner's value read by
+// v_fmac_f32 through DPP quad_perm [1,0,3,2] (lane ^ 1), then [2,3,0,1] (lane ^ 2).  Written as
+// inline asm because the compiler only forms v_fmac from its VOP3 FMA after the pass that folds
+// DPP moves, and VOP3 has no DPP form on gfx950.  A DPP read of a VGPR needs two wait states after
+// the VALU write of it: s_nop 1 covers the code before the block, and inside it every register is
+// read through DPP eight instructions after its write.
+__device__ __forceinline__ void quad_stages8(float& a0, float& a1, float& a2, float& a3, float& a4, float& a5,
+                                             float& a6, float& a7, float s32, float s64) {
+  asm("s_nop 1\n"
+      "v_fmac_f32_dpp %0, %0, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %1, %1, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %2, %2, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %3, %3, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %4, %4, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %5, %5, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %6, %6, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %7, %7, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %0, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %1, %1, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %2, %2, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %3, %3, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %4, %4, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %5, %5, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %6, %6, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %7, %7, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf"
+      : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(a4), "+v"(a5), "+v"(a6), "+v"(a7)
+      : "v"(s32), "v"(s64));
 }
 
 // ue, uo: bit patterns of M8 + n (n in [-7, 7]), whose low byte is n + 8 in [1, 15].
@@ -72,125 +100,192 @@ __device__ __forceinline__ float max3_abs(float acc, float x, float y) {
   return r;
 }
 
-__global__ __launch_bounds__(kThreads) void tq_encode4_d128_bf16_kernel(const uint32_t* __restrict__ x,
-                                                                        int64_t n_vec,
-                                                                        const float* __restrict__ diag, float c,
-                                                                        float c7, uint8_t* __restrict__ codes,
-                                                                        float* __restrict__ scale) {
+// Loads the lane's 64 bytes of group `grp`: a wave-uniform base (scalar registers) plus a 32-bit
+// lane offset.  Lanes past the end of a partial last group re-read its last vector (never stored),
+// so every lane runs the same code.
+__device__ __forceinline__ void load_group(const uint4* __restrict__ x, int64_t grp, int64_t n_vec, int v, int g,
+                                           uint4 (&t)[4]) {
+  const char* base = reinterpret_cast<const char*>(x + grp * 256);
+  const int64_t rem = n_vec - grp * 16;
+  const uint32_t vv = static_cast<uint32_t>(v < rem ? v : rem - 1);
+  const uint32_t off = vv * 256u + static_cast<uint32_t>(g) * 64u;  // bytes
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t[i] = *reinterpret_cast<const uint4*>(base + (off + 16u * i));
+  __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the transform that follows
+}
+
+// The reference's exact operation sequence for the 16 vectors of group `grp`, re-read from x:
+// tq_forward_kernel's per-lane code (16 lanes x 8 elements per vector, four passes of four
+// vectors).  Used when the fast quantiser cannot decide a rounding; it needs few registers, so it
+// does not raise the kernel's register budget.
+__device__ __forceinline__ void encode_group_exact(const uint4* __restrict__ x, int64_t grp, int64_t n_vec,
+                                                             const float* __restrict__ diag, float c,
+                                                             uint8_t* __restrict__ codes, float* __restrict__ scale) {
+  constexpr int D = 128, EPL = 8, LPV = 16;
   const int lane = threadIdx.x & 63;
-  const int v = lane & 15, g = lane >> 4, g0 = g & 1, g1 = g >> 1;
-
-  // diag of the packed words this lane loads: diag[32g + 2k] as +-1, diag[32g + 2k + 1] as a sign mask
-  float dlo[16];
-  uint32_t shi[16];
+  const int sub = lane % LPV, slot = lane / LPV;
+  float dg[EPL];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    dlo[k] = diag[32 * g + 2 * k];
-    shi[k] = diag[32 * g + 2 * k + 1] < 0.0f ? 0x80000000u : 0u;
-  }
-
-  const int64_t n_groups = (n_vec + 15) >> 4;
-  const int64_t wave = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> 6;
-  const int64_t n_waves = (static_cast<int64_t>(gridDim.x) * kThreads) >> 6;
-  for (int64_t grp = wave; grp < n_groups; grp += n_waves) {
-    const int64_t vec = grp * 16 + v;
-    const bool ok = vec < n_vec;
-    // lanes past the end re-read the last vector (never stored) so every lane runs the same code
-    const uint4* p = reinterpret_cast<const uint4*>(x + (ok ? vec : n_vec - 1) * 64 + g * 16);
-    uint32_t w[16];
+  for (int e = 0; e < EPL; ++e) dg[e] = diag[sub * EPL + e];
+#pragma unroll 1
+  for (int pass = 0; pass < 4; ++pass) {
+    const int64_t v = grp * 16 + pass * 4 + slot;
+    const bool ok = v < n_vec;
+    float a[EPL];
+    load_elems<AEKV_BF16, EPL>(x, v * D + sub * EPL, ok, a);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 t = p[i];
-      w[4 * i] = t.x;
-      w[4 * i + 1] = t.y;
-      w[4 * i + 2] = t.z;
-      w[4 * i + 3] = t.w;
-    }
-    float a[32];
+    for (int e = 0; e < EPL; ++e) a[e] = a[e] * dg[e];
+    wht_butterflies<D, EPL, true>(a, sub);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      // stage h = 1 on x * diag: lo + hi, lo - hi
-      const float lo = __builtin_bit_cast(float, w[k] << 16);
-      const float hs = __builtin_bit_cast(float, (w[k] & 0xFFFF0000u) ^ shi[k]);
-      a[2 * k] = fmaf(lo, dlo[k], hs);
-      a[2 * k + 1] = fmaf(lo, dlo[k], -hs);
-    }
-    // stages h = 2, 4, 8, 16 in registers
+    for (int e = 0; e < EPL; ++e) a[e] = a[e] * c;
+    const float m = fmaxf(group_absmax<D, EPL, true>(a), 1e-8f);
+    uint32_t w = 0u;
 #pragma unroll
-    for (int h = 2; h < 32; h <<= 1) {
-#pragma unroll
-      for (int blk = 0; blk < 32; blk += 2 * h) {
-#pragma unroll
-        for (int i = 0; i < h; ++i) {
-          const float p = a[blk + i], q = a[blk + h + i];
-          a[blk + i] = p + q;
-          a[blk + h + i] = p - q;
-        }
-      }
-    }
-    // stage h = 32 (element bit 5 = lane bit 4): afterwards reg r + 16s holds element 32s + 16g0 + r
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      swap16(a[r], a[r + 16]);
-      const float p = a[r], q = a[r + 16];
-      a[r] = p + q;
-      a[r + 16] = p - q;
-    }
-    // stage h = 64 (element bit 6 = lane bit 5): afterwards reg R holds 64*R4 + 32g1 + 16g0 + (R&15)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      swap32(a[r], a[r + 16]);
-      const float p = a[r], q = a[r + 16];
-      a[r] = p + q;
-      a[r + 16] = p - q;
-    }
-
-    // m = max(RN(c * max|raw|), 1e-8) over the 4 lanes of the vector
-    float mr = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 32; r += 2) mr = max3_abs(mr, a[r], a[r + 1]);
-    mr = fmaxf(mr, xor_lane<16>(mr));
-    mr = fmaxf(mr, xor_lane<32>(mr));
-    const float m = fmaxf(mr * c, 1e-8f);
-    const float K = c7 * __builtin_amdgcn_rcpf(m);  // v_rcp_f32: 1 ulp; only feeds the checked fast path
-
-    // fast path: u = RN(a*K + M8) = M8 + rne(a*K) (exact product, one rounding), d = a*K - n
-    uint32_t o[4];
-    float md = 0.0f;
-#pragma unroll
-    for (int dw = 0; dw < 4; ++dw) {
-      uint32_t b[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float x0 = a[8 * dw + 2 * j], x1 = a[8 * dw + 2 * j + 1];
-        const float u0 = fmaf(x0, K, kMagic8), u1 = fmaf(x1, K, kMagic8);
-        md = max3_abs(md, fmaf(x0, K, kMagic8 - u0), fmaf(x1, K, kMagic8 - u1));
-        b[j] = nib_pair(__builtin_bit_cast(uint32_t, u0), __builtin_bit_cast(uint32_t, u1));
-      }
-      o[dw] = pack4(b[0], b[1], b[2], b[3]);
-    }
-    if (__builtin_amdgcn_ballot_w64(md > 0.5f - kDelta) != 0) {
-      // a tie is within reach of the fast path's error: the reference's exact sequence
-#pragma unroll
-      for (int dw = 0; dw < 4; ++dw) {
-        uint32_t b[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float t0 = (a[8 * dw + 2 * j] * c) / m, t1 = (a[8 * dw + 2 * j + 1] * c) / m;
-          t0 = t0 * 7.0f;
-          t1 = t1 * 7.0f;
-          b[j] = nib_pair(__builtin_bit_cast(uint32_t, rintf(t0) + kMagic8),
-                          __builtin_bit_cast(uint32_t, rintf(t1) + kMagic8));
-        }
-        o[dw] = pack4(b[0], b[1], b[2], b[3]);
-      }
+    for (int e = 0; e < EPL; ++e) {
+      float t = a[e] / m;  // correctly rounded division (-fhip-fp32-correctly-rounded-divide-sqrt)
+      t = fminf(fmaxf(rintf(t * 7.0f), -7.0f), 7.0f);
+      w |= (static_cast<uint32_t>(static_cast<int>(t)) & 15u) << (4 * e);
     }
     if (ok) {
-      if (g == 0) scale[vec] = m / 7.0f;
-      uint8_t* cp = codes + vec * 64 + 8 * (g0 + 2 * g1);
-      *reinterpret_cast<uint2*>(cp) = make_uint2(o[0], o[1]);       // elements 16g' .. 16g'+15
-      *reinterpret_cast<uint2*>(cp + 32) = make_uint2(o[2], o[3]);  // elements 64 + 16g' ..
+      if (sub == 0) scale[v] = m / 7.0f;
+      *reinterpret_cast<uint32_t*>(codes + v * (D / 2) + sub * (EPL / 2)) = w;
     }
+  }
+}
+
+// Encodes the 16 vectors of group `grp` from the lane's 64 loaded bytes `t`.
+__device__ __forceinline__ void encode_group(const uint4 (&t)[4], const uint4* __restrict__ x, int64_t grp,
+                                             int64_t n_vec, int v, int g, const uint4* dm_lds, float s32,
+                                             float s64, float sigma, const float* __restrict__ diag, float c,
+                                             float c7, uint4* __restrict__ codes, float* __restrict__ scale) {
+  uint32_t w[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[4 * i] = t[i].x;
+    w[4 * i + 1] = t[i].y;
+    w[4 * i + 2] = t[i].z;
+    w[4 * i + 3] = t[i].w;
+  }
+  // the lane's diag sign masks, read from LDS each group (keeping them in registers would cost 16)
+  uint32_t dm[16];
+  asm volatile("" ::: "memory");  // not hoisted out of the group loop
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 d = dm_lds[i];
+    dm[4 * i] = d.x;
+    dm[4 * i + 1] = d.y;
+    dm[4 * i + 2] = d.z;
+    dm[4 * i + 3] = d.w;
+  }
+  float a[32];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    // stage h = 1 on x * diag: lo + hi, lo - hi
+    const float lo = __builtin_bit_cast(float, (w[k] + dm[k]) << 16);
+    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_bitop3_b32(w[k], 0xFFFF0000u, dm[k], 0x48));
+    a[2 * k] = lo + hi;
+    a[2 * k + 1] = lo - hi;
+  }
+  // stages h = 2, 4, 8, 16 in registers
+#pragma unroll
+  for (int h = 2; h < 32; h <<= 1) {
+#pragma unroll
+    for (int blk = 0; blk < 32; blk += 2 * h) {
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const float p = a[blk + i], q = a[blk + h + i];
+        a[blk + i] = p + q;
+        a[blk + h + i] = p - q;
+      }
+    }
+  }
+  // stages h = 32 and h = 64 across the quad
+#pragma unroll
+  for (int r = 0; r < 32; r += 8)
+    quad_stages8(a[r], a[r + 1], a[r + 2], a[r + 3], a[r + 4], a[r + 5], a[r + 6], a[r + 7], s32, s64);
+
+  // m = max(RN(c * max|raw|), 1e-8) over the 4 lanes of the vector
+  float mr = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 32; r += 2) mr = max3_abs(mr, a[r], a[r + 1]);
+  mr = fmaxf(mr, xor_lane<1>(mr));
+  mr = fmaxf(mr, xor_lane<2>(mr));
+  const float m = fmaxf(mr * c, 1e-8f);
+  const float K = c7 * __builtin_amdgcn_rcpf(m);  // v_rcp_f32: 1 ulp; only feeds the checked fast path
+  const float klo = (K - K * 0x1p-20f) * sigma, khi = (K + K * 0x1p-20f) * sigma;
+
+  // fast path: u = RN(a*K- + M8) = M8 + rne(a*K-); any bit of u(K-) ^ u(K+) flags a tie in reach
+  uint32_t o[4];
+  uint32_t diff = 0u;
+#pragma unroll
+  for (int dw = 0; dw < 4; ++dw) {
+    uint32_t b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x0 = a[8 * dw + 2 * j], x1 = a[8 * dw + 2 * j + 1];
+      const uint32_t u0 = __builtin_bit_cast(uint32_t, fmaf(x0, klo, kMagic8));
+      const uint32_t u1 = __builtin_bit_cast(uint32_t, fmaf(x1, klo, kMagic8));
+      // diff | (u ^ u(K+)) as one v_bitop3 (truth table 0xF0 | (0xCC ^ 0xAA))
+      diff = __builtin_amdgcn_bitop3_b32(diff, u0, __builtin_bit_cast(uint32_t, fmaf(x0, khi, kMagic8)), 0xF6);
+      diff = __builtin_amdgcn_bitop3_b32(diff, u1, __builtin_bit_cast(uint32_t, fmaf(x1, khi, kMagic8)), 0xF6);
+      b[j] = nib_pair(u0, u1);
+    }
+    o[dw] = pack4(b[0], b[1], b[2], b[3]);
+  }
+  if (__builtin_amdgcn_ballot_w64(diff != 0u) != 0) {  // a tie is within reach of the fast path's error
+    encode_group_exact(x, grp, n_vec, diag, c, reinterpret_cast<uint8_t*>(codes), scale);
+    return;
+  }
+  if (v < n_vec - grp * 16) {  // streaming stores: the outputs are not read again by this kernel
+    if (g == 0)
+      __builtin_nontemporal_store(m / 7.0f, reinterpret_cast<float*>(reinterpret_cast<char*>(scale + grp * 16) +
+                                                                     4u * static_cast<uint32_t>(v)));
+    const u32x4_t ov = {o[0], o[1], o[2], o[3]};
+    __builtin_nontemporal_store(ov, reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(codes + grp * 64) +
+                                                              16u * static_cast<uint32_t>(4 * v + g)));
+  }
+}
+
+__global__ __launch_bounds__(kThreads, AEKV_ENC4_MIN_WAVES) void tq_encode4_d128_bf16_kernel(
+    const uint4* __restrict__ x, int64_t n_vec, const float* __restrict__ diag, float c, float c7,
+    uint4* __restrict__ codes, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int v = lane >> 2, g = lane & 3;
+
+  // diag signs of the packed words lane part g loads: bit 15 for diag[32g + 2k], bit 31 for the next
+  __shared__ uint4 dm_tab[4][4];  // [g][i]: masks of words 4i .. 4i+3 of lane part g
+  if (threadIdx.x < 64) {
+    const int gg = threadIdx.x >> 4, k = threadIdx.x & 15;
+    reinterpret_cast<uint32_t*>(dm_tab[gg])[k] = (diag[32 * gg + 2 * k] < 0.0f ? 0x8000u : 0u) |
+                                                (diag[32 * gg + 2 * k + 1] < 0.0f ? 0x80000000u : 0u);
+  }
+  __syncthreads();
+  const uint4* dm = dm_tab[g];
+  const float s32 = (g & 1) ? -1.0f : 1.0f;  // stage 32: upper lane of the pair
+  const float s64 = (g & 2) ? -1.0f : 1.0f;  // stage 64
+  const float sigma = s32 * s64;             // the lane holds its elements times sigma afterwards
+
+  const int64_t n_groups = (n_vec + 15) >> 4;
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * (kThreads / 64);
+  // wave index in a scalar register: the loop below is wave-uniform
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) +
+                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  // two load buffers, alternating, so that the next group's loads are in flight during the
+  // current group's transform without register copies.  The loads are unconditional (a wave's
+  // last prefetch re-reads its own group, a cache hit) so that no wait has to cover a skipped load.
+  uint4 ta[4], tb[4];
+  int64_t grp = wave;
+  if (grp >= n_groups) return;
+  load_group(x, grp, n_vec, v, g, ta);
+  while (true) {
+    load_group(x, grp + n_waves < n_groups ? grp + n_waves : grp, n_vec, v, g, tb);
+    encode_group(ta, x, grp, n_vec, v, g, dm, s32, s64, sigma, diag, c, c7, codes, scale);
+    grp += n_waves;
+    if (grp >= n_groups) break;
+    load_group(x, grp + n_waves < n_groups ? grp + n_waves : grp, n_vec, v, g, ta);
+    encode_group(tb, x, grp, n_vec, v, g, dm, s32, s64, sigma, diag, c, c7, codes, scale);
+    grp += n_waves;
+    if (grp >= n_groups) break;
   }
 }
 
@@ -222,13 +317,14 @@ namespace aekv {
 // Launches the specialised kernel; returns false when the shape is not the specialised one.
 bool launch_encode4_d128_bf16(const void* x, int64_t n_vec, const float* diag, float c, void* codes, float* scale,
                               hipStream_t st) {
-  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(codes) & 7)) return false;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(codes) & 15)) return false;
+  if (n_vec <= 0) return true;
   const int64_t n_groups = (n_vec + 15) / 16;
   int64_t blocks = ceil_div(n_groups, kThreads / 64);
-  if (blocks > 8192) blocks = 8192;  // grid-stride beyond 32768 waves
+  if (blocks > kMaxBlocks) blocks = kMaxBlocks;
   const float c7 = c * 7.0f;
   hipLaunchKernelGGL(tq_encode4_d128_bf16_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st,
-                     static_cast<const uint32_t*>(x), n_vec, diag, c, c7, static_cast<uint8_t*>(codes), scale);
+                     static_cast<const uint4*>(x), n_vec, diag, c, c7, static_cast<uint4*>(codes), scale);
   return true;
 }
 
