@@ -49,6 +49,23 @@ __device__ __forceinline__ int mbcnt64(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
 }
 
+// Reserves v (< 2^NB) slots per active lane from the LDS counter *cnt with one atomic per wave
+// (per-lane atomics on one LDS address serialise) and returns the lane's first slot.  The
+// exclusive prefix sum over the active lanes comes from NB ballots.
+template <int NB>
+__device__ __forceinline__ uint32_t wave_reserve(uint32_t* cnt, uint32_t v) {
+  uint32_t pre = 0u, tot = 0u;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const uint64_t m = __builtin_amdgcn_ballot_w64(((v >> b) & 1u) != 0u);
+    pre += static_cast<uint32_t>(mbcnt64(m)) << b;
+    tot += static_cast<uint32_t>(__builtin_popcountll(m)) << b;
+  }
+  uint32_t base = 0u;
+  if (mbcnt64(__builtin_amdgcn_ballot_w64(true)) == 0 && tot != 0u) base = atomicAdd(cnt, tot);
+  return __builtin_amdgcn_readfirstlane(base) + pre;
+}
+
 struct MfmaIdxArgs {
   const float* q;        // [B, IH, IC]
   const float* w;        // [B, IH]
@@ -102,6 +119,20 @@ __device__ __forceinline__ int cmap(int ks, int g, int p) {
 }
 
 // 64-bit lane exchange with partner lane ^ j (j a power of two below 64, constant after unrolling).
+template <int HL>
+__device__ __forceinline__ uint32_t max_xor_u32(uint32_t v) {
+  const uint32_t o = __builtin_bit_cast(uint32_t, xor_lane<HL>(__builtin_bit_cast(float, v)));
+  return v > o ? v : o;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max_xor_u32<1>(v);
+  v = max_xor_u32<2>(v);
+  v = max_xor_u32<4>(v);
+  v = max_xor_u32<8>(v);
+  v = max_xor_u32<16>(v);
+  return max_xor_u32<32>(v);
+}
+
 __device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v, int j) {
   float lo = __builtin_bit_cast(float, static_cast<uint32_t>(v));
   float hi = __builtin_bit_cast(float, static_cast<uint32_t>(v >> 32));
@@ -425,8 +456,11 @@ __device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
 // One workgroup per row.
 //  1. Slot bound: every 16-key slot's max is one of its keys, so if kk slot maxima are >= tau
 //     then the kk-th largest key is >= tau, and every top-kk key lies in a slot whose max is >=
-//     tau.  tau is the floor of the 12-bit bin holding the kk-th largest slot max (LDS histogram
-//     of the maxima); only the slots with max >= tau are read, and their keys >= tau collected.
+//     tau.  tau is the floor of the bin holding the kk-th largest slot max in an LDS histogram of
+//     the maxima whose 4096 bins are the values of key >> 16 just below the row's largest slot
+//     max (1/128 of a binade each; the lowest bin also takes everything further down, and tau is
+//     0 if it holds the kk-th).  Only the slots with max >= tau are read, and their keys >= tau
+//     collected.
 //  2. Three radix levels over the candidates (bits 31..20, 19..8, 7..0; LDS histograms) give
 //     the kk-th largest key T; keys > T are taken with the lowest-index keys == T and the kk words
 //     placed by rank.  If the candidates overflow LDS (many equal keys), the levels run over all
@@ -472,13 +506,29 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
       mx[r] = sl < n_slots ? mrow[sl] : 0u;
     }
   };
-  load_max(0);
-  __syncthreads();
+  // the row's largest slot max anchors the histogram
+  uint32_t mloc = 0u;
   for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
-    if (c0 > 0) load_max(c0);
+    load_max(c0);
 #pragma unroll
-    for (int r = 0; r < kSlotPer; ++r)
-      if (c0 + tid + static_cast<int64_t>(r) * kSelThreads < n_slots) atomicAdd(&h[mx[r] >> 20], 1u);
+    for (int r = 0; r < kSlotPer; ++r) mloc = mloc > mx[r] ? mloc : mx[r];  // mx is 0 past the end
+  }
+  mloc = wave_max_u32(mloc);
+  if (lane == 0) s_tot[wv] = mloc;
+  __syncthreads();  // also orders the zeroing of h before the histogram
+  uint32_t top = 0u;
+#pragma unroll
+  for (int w2 = 0; w2 < NW; ++w2) top = top > s_tot[w2] ? top : s_tot[w2];
+  top >>= 16;
+  // bin 4095 - d holds the maxima with key >> 16 == top - d (d < 4095); bin 0 everything lower
+  for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
+    if (n_slots > kSlotPass) load_max(c0);  // otherwise mx still holds the only pass
+#pragma unroll
+    for (int r = 0; r < kSlotPer; ++r) {
+      const uint32_t d = top - (mx[r] >> 16);
+      if (c0 + tid + static_cast<int64_t>(r) * kSelThreads < n_slots)
+        atomicAdd(&h[kHistBins - 1 - (d < kHistBins - 1 ? d : kHistBins - 1)], 1u);
+    }
   }
   __syncthreads();
   uint32_t tau = 0u;
@@ -487,25 +537,34 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
     block_threshold<kSelThreads, kHistBins / kSelThreads>(h, kk, s_tot, s_res, t, ab, ct);
     (void)ab;
     (void)ct;
-    tau = t << 20;
+    tau = t > 0u ? (top - (kHistBins - 1 - t)) << 16 : 0u;
   }
   // qualifying slots (max >= tau) are compacted into a list (in h, free until the radix levels),
   // then one thread per listed slot reads its 16 keys and appends those >= tau
   for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
-    if (n_slots > kSlotPass) load_max(c0);
+    if (n_slots > kSlotPass) load_max(c0);  // otherwise mx still holds the only pass
     __syncthreads();  // h and s_cnt[1] are free
     if (tid == 0) s_cnt[1] = 0u;
     __syncthreads();
+    {  // one reservation per wave for all of its slot columns
+      bool q[kSlotPer];
+      uint64_t m[kSlotPer];
+      uint32_t tot = 0u;
 #pragma unroll
-    for (int r = 0; r < kSlotPer; ++r) {
-      const int64_t sl = c0 + tid + static_cast<int64_t>(r) * kSelThreads;
-      const bool q = sl < n_slots && mx[r] >= tau;
-      const uint64_t m = __builtin_amdgcn_ballot_w64(q);
-      if (m == 0) continue;  // wave-uniform
-      uint32_t base = 0;
-      if (lane == 0) base = atomicAdd(&s_cnt[1], static_cast<uint32_t>(__builtin_popcountll(m)));
+      for (int r = 0; r < kSlotPer; ++r) {
+        const int64_t sl = c0 + tid + static_cast<int64_t>(r) * kSelThreads;
+        q[r] = sl < n_slots && mx[r] >= tau;
+        m[r] = __builtin_amdgcn_ballot_w64(q[r]);
+        tot += static_cast<uint32_t>(__builtin_popcountll(m[r]));
+      }
+      uint32_t base = 0u;
+      if (lane == 0 && tot != 0u) base = atomicAdd(&s_cnt[1], tot);
       base = __builtin_amdgcn_readfirstlane(base);
-      if (q) h[base + static_cast<uint32_t>(mbcnt64(m))] = static_cast<uint32_t>(sl - c0);
+#pragma unroll
+      for (int r = 0; r < kSlotPer; ++r) {
+        if (q[r]) h[base + static_cast<uint32_t>(mbcnt64(m[r]))] = static_cast<uint32_t>(tid + r * kSelThreads);
+        base += static_cast<uint32_t>(__builtin_popcountll(m[r]));
+      }
     }
     __syncthreads();
     const int n_list = static_cast<int>(s_cnt[1]);
@@ -523,7 +582,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
       uint32_t c = 0;
 #pragma unroll
       for (int e = 0; e < 16; ++e) c += (16 * sl + e < nv && kw[e] >= tau) ? 1u : 0u;
-      uint32_t p = atomicAdd(&s_cnt[0], c);
+      uint32_t p = wave_reserve<5>(&s_cnt[0], c);  // c <= 16
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         if (16 * sl + e < nv && kw[e] >= tau) {
@@ -547,31 +606,40 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
   // each other run, the number of smaller words there (binary search).  Words are distinct.
   if (fast && n <= kSortCap) {
     uint64_t w = tid < n ? sort_word(ck[tid], ci[tid]) : ~0ull;
+    if (64 * wv < n) {  // wave-uniform: waves past the candidates only pad
 #pragma unroll
-    for (int kq = 2; kq <= 64; kq <<= 1) {
+      for (int kq = 2; kq <= 64; kq <<= 1) {
 #pragma unroll
-      for (int j = kq >> 1; j > 0; j >>= 1) {
-        const uint64_t o = xor_lane_u64(w, j);
-        const bool keep_min = ((lane & j) == 0) == ((lane & kq) == 0);
-        w = keep_min ? (o < w ? o : w) : (o > w ? o : w);
+        for (int j = kq >> 1; j > 0; j >>= 1) {
+          const uint64_t o = xor_lane_u64(w, j);
+          const bool keep_min = ((lane & j) == 0) == ((lane & kq) == 0);
+          w = keep_min ? (o < w ? o : w) : (o > w ? o : w);
+        }
       }
     }
     __syncthreads();  // ck/ci are read
-    cbuf[tid] = w;    // run wv at cbuf[64 wv .. 64 wv + 63], ascending
+    cbuf[tid] = w;    // run wv at cbuf[64 wv .. 64 wv + 63], ascending; runs past n_runs all ~0
     __syncthreads();
     const int n_runs = (n + 63) >> 6;
     if (tid < n) {
-      uint32_t pos = static_cast<uint32_t>(lane);
+      // position = number of smaller words over all runs (the own run gives the lane); the binary
+      // searches of 8 runs are interleaved so that their LDS reads overlap
+      uint32_t pos = 0u;
+      for (int r0 = 0; r0 < n_runs; r0 += 8) {
+        int lo[8];
 #pragma unroll
-      for (int r = 0; r < kSortCap / 64; ++r) {
-        if (r >= n_runs || r == wv) continue;
-        const uint64_t* run = cbuf + 64 * r;
-        int lo = 0;  // number of words in run r below w (the steps reach 63; the last compare 64)
+        for (int q = 0; q < 8; ++q) lo[q] = 0;
 #pragma unroll
-        for (int step = 32; step > 0; step >>= 1)
-          if (run[lo + step - 1] < w) lo += step;
-        if (run[lo] < w) ++lo;
-        pos += static_cast<uint32_t>(lo);
+        for (int step = 32; step > 0; step >>= 1) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            if (cbuf[64 * (r0 + q) + lo[q] + step - 1] < w) lo[q] += step;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {  // the steps reach 63; the last compare 64
+          if (cbuf[64 * (r0 + q) + lo[q]] < w) ++lo[q];
+          pos += static_cast<uint32_t>(lo[q]);
+        }
       }
       if (pos < kk) {
         orow[pos] = static_cast<int64_t>(static_cast<uint32_t>(w & 0xffffffffu));
@@ -634,13 +702,13 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
     const bool all_eq = n_eq == need;
     for (int i = tid; i < n; i += kSelThreads) {
       const uint32_t key = ck[i], idx = ci[i];
+      const uint32_t pg = wave_reserve<1>(&s_cnt[0], key > T ? 1u : 0u);
+      const uint32_t pe = wave_reserve<1>(&s_cnt[1], key == T && all_eq ? 1u : 0u);
       if (key > T) {
-        const uint32_t p = atomicAdd(&s_cnt[0], 1u);
-        if (p < n_gt) sel[p] = sort_word(key, idx);
+        if (pg < n_gt) sel[pg] = sort_word(key, idx);
       } else if (key == T) {
         if (all_eq) {
-          const uint32_t p = atomicAdd(&s_cnt[1], 1u);
-          if (p < need) sel[n_gt + p] = sort_word(key, idx);
+          if (pe < need) sel[n_gt + pe] = sort_word(key, idx);
         } else {  // ties at T: rank among the equal keys by index
           uint32_t r = 0;
           for (int j = 0; j < n; ++j) r += (ck[j] == T && ci[j] < idx) ? 1u : 0u;
@@ -655,10 +723,8 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
       const uint32_t key = j < nv ? krow[j] : 0u;
       const bool gt = j < nv && key > T;
       const bool eq = j < nv && key == T;
-      if (gt) {
-        const uint32_t p = atomicAdd(&s_cnt[0], 1u);
-        if (p < n_gt) sel[p] = sort_word(key, static_cast<uint32_t>(j));
-      }
+      const uint32_t pg = wave_reserve<1>(&s_cnt[0], gt ? 1u : 0u);
+      if (gt && pg < n_gt) sel[pg] = sort_word(key, static_cast<uint32_t>(j));
       const uint64_t m = __builtin_amdgcn_ballot_w64(eq);
       if (lane == 0) s_wave_eq[wv] = static_cast<uint32_t>(__builtin_popcountll(m));
       __syncthreads();
