@@ -168,64 +168,72 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
   const int n_groups = static_cast<int>((src1 - src0 + kGroup - 1) / kGroup);
 #pragma unroll 1
   for (int G = wv; G < n_groups; G += kWaves) {
-    bf16x8_t kf[2][4];
-    bool okk[2];
+    // both blocks' rows are requested before either is decoded (two gathers in flight)
+    int kind[2];  // 0 empty, 1 code row, 2 window row
+    uint32_t cw[2][2][BITS == 8 ? 4 : 2];
+    float sraw[2];
+    uint2 wv2[2][4][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       // lane (key c16 of block kb): its source, code bytes (two halves) or window dims
       const int64_t si = src0 + static_cast<int64_t>(G) * kGroup + 16 * kb + c16;
-      int kind = 0;  // 0 empty, 1 code row, 2 window row
+      kind[kb] = 0;
       int64_t blk = -1;
       if (si < a.n_comp) {
         blk = a.sel ? sidx[si - src0] : si;
-        kind = blk >= 0 ? 1 : 0;
+        kind[kb] = blk >= 0 ? 1 : 0;
       } else if (si < src1) {
-        kind = 2;
+        kind[kb] = 2;
       }
-      okk[kb] = kind != 0;
-      uint32_t cw[2][BITS == 8 ? 4 : 2];
-      float fk = 0.0f;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int e = 0; e < (BITS == 8 ? 4 : 2); ++e) cw[hh][e] = 0u;
-      uint2 wv2[4][2];
-      if (kind == 1) {
+        for (int e = 0; e < (BITS == 8 ? 4 : 2); ++e) cw[kb][hh][e] = 0u;
+      sraw[kb] = 0.0f;
+      if (kind[kb] == 1) {
         const uint8_t* row = a.codes + (b * a.S + blk) * RB;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           if constexpr (BITS == 8) {
             const uint4 v = *reinterpret_cast<const uint4*>(row + HB * hh + 16 * g);
-            cw[hh][0] = v.x;
-            cw[hh][1] = v.y;
-            cw[hh][2] = v.z;
-            cw[hh][3] = v.w;
+            cw[kb][hh][0] = v.x;
+            cw[kb][hh][1] = v.y;
+            cw[kb][hh][2] = v.z;
+            cw[kb][hh][3] = v.w;
           } else {
             const uint2 v = *reinterpret_cast<const uint2*>(row + HB * hh + 8 * g);
-            cw[hh][0] = v.x;
-            cw[hh][1] = v.y;
+            cw[kb][hh][0] = v.x;
+            cw[kb][hh][1] = v.y;
           }
         }
-        fk = a.scale[b * a.S + blk] * kscale_unit;
+        sraw[kb] = a.scale[b * a.S + blk];
       }
-      if (kind == 2) {
+      if (kind[kb] == 2) {
         const uint16_t* wr = a.win + (b * a.W + (si - a.n_comp)) * kD + 4 * g;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          wv2[ks][0] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks));
-          wv2[ks][1] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks + 1));
+          wv2[kb][ks][0] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks));
+          wv2[kb][ks][1] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks + 1));
         }
       }
+    }
+
+    bf16x8_t kf[2][4];
+    bool okk[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      okk[kb] = kind[kb] != 0;
+      const float fk = sraw[kb] * kscale_unit;
       // y = H64 codes per half (all lanes take part; lanes without a code row supply zeros)
       i32x4_t P[2][4];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         i32x4_t Bop;
         if constexpr (BITS == 8) {
-          Bop = i32x4_t{static_cast<int>(cw[hh][0]), static_cast<int>(cw[hh][1]), static_cast<int>(cw[hh][2]),
-                        static_cast<int>(cw[hh][3])};
+          Bop = i32x4_t{static_cast<int>(cw[kb][hh][0]), static_cast<int>(cw[kb][hh][1]),
+                        static_cast<int>(cw[kb][hh][2]), static_cast<int>(cw[kb][hh][3])};
         } else {
-          const uint32_t x = cw[hh][0], y = cw[hh][1];
+          const uint32_t x = cw[kb][hh][0], y = cw[kb][hh][1];
           Bop = i32x4_t{static_cast<int>((x << 4) & 0xF0F0F0F0u), static_cast<int>(x & 0xF0F0F0F0u),
                         static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
         }
@@ -238,11 +246,11 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         uint32_t w4[4];
-        if (kind == 2) {
-          w4[0] = wv2[ks][0].x ^ dsign[ks][0];
-          w4[1] = wv2[ks][0].y ^ dsign[ks][1];
-          w4[2] = wv2[ks][1].x ^ dsign[ks][2];
-          w4[3] = wv2[ks][1].y ^ dsign[ks][3];
+        if (kind[kb] == 2) {
+          w4[0] = wv2[kb][ks][0].x ^ dsign[ks][0];
+          w4[1] = wv2[kb][ks][0].y ^ dsign[ks][1];
+          w4[2] = wv2[kb][ks][1].x ^ dsign[ks][2];
+          w4[3] = wv2[kb][ks][1].y ^ dsign[ks][3];
         } else {
           float v[8];
 #pragma unroll
