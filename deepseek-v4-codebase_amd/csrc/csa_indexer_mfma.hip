@@ -19,10 +19,12 @@
 //          scores every visible key, stores its order-preserving uint32 key and the max of every
 //          16-key slot.
 //   final  (one workgroup per row)  bounds the k-th largest key from below by the k-th largest
-//          slot max (12-bit resolution), reads only the slots that can hold a top-k key, and
-//          selects exactly among their keys with three LDS radix levels; keys > T and the
-//          lowest-index keys == T are taken and placed by rank under (key desc, index asc).  If
-//          the candidates overflow LDS (many equal keys), the levels run over all of the row's
+//          slot max (a histogram of the slot maxima in 1/128-binade bins below the row's largest),
+//          reads only the slots that can hold a top-k key and keeps their keys above the bound.
+//          Up to 1024 candidates (the usual case: a few hundred) are sorted outright, 64 per wave
+//          in registers, the runs placed by binary search; more go through three LDS radix levels
+//          (keys > T and the lowest-index keys == T, placed by rank under (key desc, index asc)).
+//          If the candidates overflow LDS (many equal keys), the levels run over all of the row's
 //          stored keys, read in index order.
 // Both routes return the top-k under the total order (score desc, index asc).
 #include <algorithm>
@@ -34,7 +36,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kSelThreads = 1024;
-constexpr int kHistBins = 4096;      // top 12 bits of the order key
+constexpr int kHistBins = 4096;      // slot-max histogram bins (key >> 16 below the row maximum)
 constexpr int kCandCap = 4096;       // candidates a row's workgroup collects in LDS (fast route)
 constexpr int kSortCap = 1024;       // at most this many candidates are sorted outright (one per thread)
 constexpr int kMaxMfmaK = 1024;
