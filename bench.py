@@ -11,7 +11,9 @@ The same line carries, under "secondary", cfg2 decode GB/s, CSA sparse decode to
 cfg3), HCA decode tokens/s (cfg4) and the reference microbenchmark shape of sparse_sink_attention.
 
 Timing: W untimed warmup steps, then K steps bracketed by torch.cuda.synchronize() and HIP events
-recorded on the stream the kernels run on (torch's current stream).
+recorded on the stream the kernels run on (torch's current stream).  Decode steps (indexer +
+attention) are captured 8 at a time in a HIP graph and replayed, as a serving loop would run them;
+the eager (per-call Python) step time is reported beside it.
 
 cpu_baseline: the CPU oracle (oracle/liboracle.so, a C restatement of turbo_quant.py's encode)
 timed on this host's cores over the cfg2 layer (median of 3 passes).
@@ -58,6 +60,29 @@ def timed(fn, steps: int, warmup: int):
     e1.record(st)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+GRAPH_STEPS = 8  # decode steps captured per HIP graph
+
+
+def timed_graph(fn, steps: int, warmup: int, inner: int = GRAPH_STEPS):
+    """Average ms per fn call when `inner` consecutive calls are captured in one HIP graph and the
+    graph is replayed, the way a serving loop replays its decode step (every replay runs every
+    kernel of every call); same events and synchronisation as timed()."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(inner):
+            fn()
+    ms = timed(g.replay, steps, warmup) / inner
+    del g
+    return ms
 
 
 def cpu_cores() -> int:
@@ -175,17 +200,19 @@ def bench_csa(args, dev, B, S, bits, seed, outliers, name):
         index_only()
         attn_only()
 
-    ms = timed(step, args.steps, args.warmup)
-    ms_i = timed(index_only, args.steps, args.warmup)
-    ms_a = timed(attn_only, args.steps, args.warmup)
+    ms_eager = timed(step, args.steps, args.warmup)
+    ms = timed_graph(step, args.steps, args.warmup)
+    ms_i = timed_graph(index_only, args.steps, args.warmup)
+    ms_a = timed_graph(attn_only, args.steps, args.warmup)
     row_bytes = (D if bits == 8 else D // 2) + 4
     ix_bytes = (64 if bits == 8 else 32) + 4
     step_bytes = B * (S * ix_bytes + k * row_bytes + 128 * D * 2 + H * D * 2 * 2)
     res = {"B": B, "S": S, "bits": bits, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / ms * 1e3, 1),
+           "ms_per_step_eager": round(ms_eager, 5), "timing": f"HIP graph of {GRAPH_STEPS} steps, replayed",
            "indexer_ms": round(ms_i, 5), "attention_ms": round(ms_a, 5), "bytes_per_step": step_bytes,
            "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    log(f"{name}: {ms * 1e3:.1f} us/step ({ms_i * 1e3:.1f} indexer + {ms_a * 1e3:.1f} attention) "
-        f"-> {res['tokens_per_s']:.0f} tok/s, {res['hbm_frac'] * 100:.1f}% of HBM peak")
+    log(f"{name}: {ms * 1e3:.1f} us/step ({ms_i * 1e3:.1f} indexer + {ms_a * 1e3:.1f} attention; graph replay; "
+        f"eager {ms_eager * 1e3:.1f}) -> {res['tokens_per_s']:.0f} tok/s, {res['hbm_frac'] * 100:.1f}% of HBM peak")
     del inp
     torch.cuda.empty_cache()
     return res
@@ -206,14 +233,18 @@ def bench_hca(args, dev):
     sink = normal((H,), 6, dtype=torch.float32, device=dev)
     ws = attention_workspace(B, H, D, S, W, dev)
     out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
-    ms = timed(lambda: quant_sink_attention(q, codes, scale, None, win, sink, D ** -0.5, quant=pq, workspace=ws,
-                                            out=out), args.steps, args.warmup)
+    def step():
+        quant_sink_attention(q, codes, scale, None, win, sink, D ** -0.5, quant=pq, workspace=ws, out=out)
+
+    ms_eager = timed(step, args.steps, args.warmup)
+    ms = timed_graph(step, args.steps, args.warmup)
     flops = 2 * 2 * B * H * (S + W) * D
     step_bytes = B * (S * (D // 2 + 4) + W * D * 2 + H * D * 4)
     res = {"B": B, "S": S, "bits": 4, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / ms * 1e3, 1),
+           "ms_per_step_eager": round(ms_eager, 5), "timing": f"HIP graph of {GRAPH_STEPS} steps, replayed",
            "tflops": round(flops / ms / 1e9, 3), "mfma_frac": round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 5),
            "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    log(f"cfg4: {ms * 1e3:.1f} us/step -> {res['tokens_per_s']:.0f} tok/s")
+    log(f"cfg4: {ms * 1e3:.1f} us/step (graph replay; eager {ms_eager * 1e3:.1f}) -> {res['tokens_per_s']:.0f} tok/s")
     return res
 
 
