@@ -7,6 +7,9 @@ Drop-in modules (same names and signatures as the reference):
   aetherkv.backends          <- aether_pipeline/serving.py backend protocol
 New fused decode path over quantised KV:
   aetherkv.decode            csa_indexer_topk_quant, quant_sink_attention, csa_decode, hca_decode
+  aetherkv.cache             the engine's cache state types and quant helpers (drop-in), and CodeRing:
+                             preallocated code storage appended in place and read by csa_decode_ring /
+                             hca_decode_ring
 All compute runs in libaetherkv.so (hand-written HIP for gfx950, C ABI in include/aetherkv.h).
 """
 from .loader import cuda_build_environment, cuda_extension_unavailable_reason, load_aether_cuda_kernels
