@@ -276,6 +276,9 @@ extern "C" int aekv_tq_decode(const void* codes, const float* scale, int64_t n_v
   const size_t out_al = epl * dtype_size(out_dtype) > 16 ? 16 : epl * dtype_size(out_dtype);
   if (!is_aligned(codes, in_al) || !is_aligned(out, out_al) || !is_aligned(scale, 4) || !is_aligned(diag, 4))
     return fail(AEKV_ERR_ALIGN, "aekv_tq_decode: misaligned pointer (codes needs %zu, out %zu bytes)", in_al, out_al);
+  if (bits == 4 && d == 128 && out_dtype == AEKV_BF16 && use_specialised_codec() &&
+      launch_decode4_d128_bf16(codes, scale, n_vec, diag, wht_scale(d), out, as_stream(stream)))
+    return check_launch("aekv_tq_decode");
   dec_fn fn = bits == 8 ? pick_dec_dt<8>(out_dtype, d) : pick_dec_dt<4>(out_dtype, d);
   hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(grid_for(n_vec, d))), dim3(kThreads), 0, as_stream(stream),
                      codes, scale, n_vec, diag, wht_scale(d), out);

@@ -1,5 +1,6 @@
-// Fast TurboQuant 4-bit encode for the production shape: D = 128, bf16 input (gfx950).
+// Fast TurboQuant 4-bit encode and decode for the production shape: D = 128, bf16 (gfx950).
 //
+// ENCODE
 // Same result, bit for bit, as tq_forward_kernel<BF16, 128, ENC4> and as
 // aether_2b/turbo_quant.py:127-166 (rot = _wht(x*diag); m = max(max|rot|, 1e-8); scale = m/7;
 // q = clamp(rne(rot/m*7)); nibble pack), with about half the VALU work:
@@ -289,6 +290,166 @@ __global__ __launch_bounds__(kThreads, AEKV_ENC4_MIN_WAVES) void tq_encode4_d128
   }
 }
 
+// ---- decode: 4-bit codes -> bf16, D = 128 ------------------------------------------------------
+// Same result, bit for bit, as tq_decode_kernel<4, 128, BF16> and aether_2b/turbo_quant.py:187-211
+// (rot = code * scale; x = _wht(rot) * diag; bf16 RNE).
+//  * Layout: 16 lanes per vector, four vectors per wave and pass; lane l of a vector's row holds
+//    the 8 elements of chunk pi(l) = l ^ f(l bit 2, l bit 3) with f = 0, 3, 4, 7.  Its code dword
+//    and its 16 output bytes are where chunk pi(l) lives, so a load instruction covers 256
+//    contiguous bytes and a store 1 KiB.  Butterfly stages h = 1, 2, 4 run in the lane; stages
+//    8 / 16 / 32 / 64 act on chunk bits 0 / 1 / 2 / 3, which pi turns into the DPP patterns
+//    quad_perm [1,0,3,2] (l ^ 1), quad_perm [2,3,0,1] (l ^ 2), row_half_mirror (l ^ 7) and
+//    row_mirror (l ^ 15), each one v_fmac_f32_dpp per element (own + s * partner, s = -1 on the
+//    lane whose chunk has the stage's bit set).
+//  * Unpack: (w ^ 0x88888888) & 0x0F0F0F0F (one v_bitop3) turns the nibbles of a word into n + 8
+//    in bytes (low nibbles; the high ones after a shift), v_cvt_f32_ubyte converts, and
+//    rot = fma(n + 8, s, -8s) = RN(n*s) exactly (8s is exact, so the fma's one rounding is the
+//    reference's product rounding).
+//  * After the cross stages a lane holds sigma * raw (sigma = -1 per stage in which it was the
+//    upper lane; RNE is sign-symmetric), and fma(sigma*raw, sigma*c, +0) = RN(raw * c): the +0
+//    addend turns a zero of either sign into +0, which is what the reference's butterflies give
+//    for a zero when every scale is positive (its zeros come from exact cancellation or 0 * s).
+//    The sign of diag is then XORed into the packed bf16 pair.
+//  * A pass with any scale outside (0, 2^124) (zero, negative, NaN, or too large for -8s to be
+//    exact) decodes its vectors with the generic per-lane sequence instead.
+
+// Stages h = 8, 16, 32, 64 on the lane's eight elements: a += s * a(partner) with the partner read
+// by v_fmac_f32 through DPP (inline asm for the reason given at quad_stages8; s_nop 1 covers the
+// DPP read-after-VALU-write hazard of the code before the block, and inside it each register is
+// read through DPP eight instructions after its write).
+__device__ __forceinline__ void row_stages8(float (&a)[8], float s8, float s16, float s32, float s64) {
+  asm("s_nop 1\n"
+      "v_fmac_f32_dpp %0, %0, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %1, %1, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %2, %2, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %3, %3, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %4, %4, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %5, %5, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %6, %6, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %7, %7, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %0, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %1, %1, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %2, %2, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %3, %3, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %4, %4, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %5, %5, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %6, %6, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %7, %7, %9 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %0, %10 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %1, %1, %10 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %2, %2, %10 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %3, %3, %10 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %4, %4, %10 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %5, %5, %10 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %6, %6, %10 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %7, %7, %10 row_half_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %0, %0, %11 row_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %1, %1, %11 row_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %2, %2, %11 row_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %3, %3, %11 row_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %4, %4, %11 row_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %5, %5, %11 row_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %6, %6, %11 row_mirror row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %7, %7, %11 row_mirror row_mask:0xf bank_mask:0xf"
+      : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7])
+      : "v"(s8), "v"(s16), "v"(s32), "v"(s64));
+}
+
+// Decodes the four vectors of pass `pv` (vectors 4pv .. 4pv+3) from the lane's code dword `w` and
+// its vector's scale `s`.
+__device__ __forceinline__ void decode_pass(uint32_t w, float s, int64_t pv, int64_t n_vec, int row, int chunk,
+                                            const float (&sg)[4], float sc, uint32_t dsig0, uint32_t dsig1,
+                                            uint32_t dsig2, uint32_t dsig3, const uint8_t* __restrict__ codes,
+                                            const float* __restrict__ scale, const float* __restrict__ diag,
+                                            float c, uint16_t* __restrict__ out) {
+  const int64_t v = pv * 4 + row;
+  if (__builtin_amdgcn_ballot_w64(!(s > 0.0f && s < 0x1p124f)) != 0) {  // wave-uniform, rare
+    // the generic kernel's per-lane sequence: lane l of the row holds elements 8l .. 8l+7
+    const int sub = threadIdx.x & 15;
+    float dg[8], a[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dg[e] = diag[8 * sub + e];
+    const int64_t vr = v < n_vec ? v : n_vec - 1;
+    decode_lane<4, 128, true>(codes + vr * 64, scale[vr], sub, dg, c, a);
+    if (v < n_vec)
+      *reinterpret_cast<uint4*>(out + v * 128 + 8 * sub) =
+          make_uint4(pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(a[4], a[5]), pack_bf16x2(a[6], a[7]));
+    return;
+  }
+  const uint32_t lo = __builtin_amdgcn_bitop3_b32(w, 0x88888888u, 0x0F0F0F0Fu, 0x28);  // (x ^ y) & z
+  const uint32_t hi = __builtin_amdgcn_bitop3_b32(w >> 4, 0x88888888u, 0x0F0F0F0Fu, 0x28);
+  const float m8s = -8.0f * s;
+  float a[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // n + 8 converts exactly
+    a[2 * k] = fmaf(static_cast<float>((lo >> (8 * k)) & 0xFFu), s, m8s);
+    a[2 * k + 1] = fmaf(static_cast<float>((hi >> (8 * k)) & 0xFFu), s, m8s);
+  }
+#pragma unroll
+  for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+    for (int blk = 0; blk < 8; blk += 2 * h) {
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const float p = a[blk + i], q = a[blk + h + i];
+        a[blk + i] = p + q;
+        a[blk + h + i] = p - q;
+      }
+    }
+  }
+  row_stages8(a, sg[0], sg[1], sg[2], sg[3]);
+  const uint32_t o0 = pack_bf16x2(fmaf(a[0], sc, 0.0f), fmaf(a[1], sc, 0.0f)) ^ dsig0;
+  const uint32_t o1 = pack_bf16x2(fmaf(a[2], sc, 0.0f), fmaf(a[3], sc, 0.0f)) ^ dsig1;
+  const uint32_t o2 = pack_bf16x2(fmaf(a[4], sc, 0.0f), fmaf(a[5], sc, 0.0f)) ^ dsig2;
+  const uint32_t o3 = pack_bf16x2(fmaf(a[6], sc, 0.0f), fmaf(a[7], sc, 0.0f)) ^ dsig3;
+  if (v < n_vec) *reinterpret_cast<uint4*>(out + v * 128 + 8 * chunk) = make_uint4(o0, o1, o2, o3);
+}
+
+__global__ __launch_bounds__(kThreads) void tq_decode4_d128_bf16_kernel(const uint32_t* __restrict__ codes,
+                                                                        const float* __restrict__ scale,
+                                                                        int64_t n_vec, const float* __restrict__ diag,
+                                                                        float c, uint16_t* __restrict__ out) {
+  const int l = threadIdx.x & 15, row = (threadIdx.x >> 4) & 3;
+  const int chunk = l ^ (((l >> 2) & 1) ? 3 : 0) ^ (((l >> 3) & 1) ? 4 : 0);  // pi(l)
+  float sg[4];  // stage factors: -1 on the lane whose chunk has the stage's bit set
+#pragma unroll
+  for (int k = 0; k < 4; ++k) sg[k] = ((chunk >> k) & 1) ? -1.0f : 1.0f;
+  const float sc = ((__builtin_popcount(static_cast<unsigned>(chunk)) & 1) ? -c : c);  // sigma * c
+  uint32_t dsig[4];  // diag sign bits of the packed output pairs
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    dsig[k] = (diag[8 * chunk + 2 * k] < 0.0f ? 0x8000u : 0u) | (diag[8 * chunk + 2 * k + 1] < 0.0f ? 0x80000000u : 0u);
+
+  const int64_t n_pass = (n_vec + 3) >> 2;
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * (kThreads / 64);
+  int64_t pv = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) +
+               __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  if (pv >= n_pass) return;
+  const uint8_t* cb = reinterpret_cast<const uint8_t*>(codes);
+  // lanes past the end read the last vector (never stored)
+  auto load = [&](int64_t p, uint32_t& w, float& s) {
+    const int64_t v = p * 4 + row;
+    const int64_t vr = v < n_vec ? v : n_vec - 1;
+    w = codes[vr * 16 + chunk];
+    s = scale[vr];
+  };
+  // the next pass's codes and scales are requested before the current pass is transformed
+  uint32_t w;
+  float s;
+  load(pv, w, s);
+  while (true) {
+    uint32_t wn;
+    float sn;
+    load(pv + n_waves < n_pass ? pv + n_waves : pv, wn, sn);
+    __builtin_amdgcn_sched_barrier(0);
+    decode_pass(w, s, pv, n_vec, row, chunk, sg, sc, dsig[0], dsig[1], dsig[2], dsig[3], cb, scale, diag, c, out);
+    pv += n_waves;
+    if (pv >= n_pass) break;
+    w = wn;
+    s = sn;
+  }
+}
+
 }  // namespace
 
 namespace {
@@ -325,6 +486,22 @@ bool launch_encode4_d128_bf16(const void* x, int64_t n_vec, const float* diag, f
   const float c7 = c * 7.0f;
   hipLaunchKernelGGL(tq_encode4_d128_bf16_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st,
                      static_cast<const uint4*>(x), n_vec, diag, c, c7, static_cast<uint4*>(codes), scale);
+  return true;
+}
+
+
+// Launches the specialised decode; returns false when the shape or alignment is not the specialised one.
+bool launch_decode4_d128_bf16(const void* codes, const float* scale, int64_t n_vec, const float* diag, float c,
+                              void* out, hipStream_t st) {
+  if ((reinterpret_cast<uintptr_t>(codes) & 15) || (reinterpret_cast<uintptr_t>(out) & 15) ||
+      (reinterpret_cast<uintptr_t>(scale) & 3))
+    return false;
+  if (n_vec <= 0) return true;
+  const int64_t n_pass = (n_vec + 3) / 4;
+  int64_t blocks = ceil_div(n_pass, kThreads / 64);
+  if (blocks > kMaxBlocks) blocks = kMaxBlocks;
+  hipLaunchKernelGGL(tq_decode4_d128_bf16_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st,
+                     static_cast<const uint32_t*>(codes), scale, n_vec, diag, c, static_cast<uint16_t*>(out));
   return true;
 }
 

@@ -148,10 +148,12 @@ __device__ __forceinline__ void decode_lane(const uint8_t* __restrict__ row, flo
   decode_lane_bytes<BITS, D, LDS_PIPE>(w, s, sub, dg, c, a);
 }
 
-// Specialised production-shape kernels (tq_encode_d128.hip).  Each returns false (and launches
+// Specialised production-shape kernels (tq_codec_d128.hip).  Each returns false (and launches
 // nothing) when its alignment requirements are not met, so the caller falls back to the generic
 // kernel.  AETHERKV_CODEC=generic in the environment forces the generic kernels (testing aid).
 bool launch_encode4_d128_bf16(const void* x, int64_t n_vec, const float* diag, float c, void* codes, float* scale,
                               hipStream_t st);
+bool launch_decode4_d128_bf16(const void* codes, const float* scale, int64_t n_vec, const float* diag, float c,
+                              void* out, hipStream_t st);
 
 }  // namespace aekv

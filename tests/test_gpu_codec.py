@@ -195,6 +195,36 @@ def test_specialised_and_generic_encode_agree(dev):
     np.testing.assert_array_equal(cs.cpu().numpy(), want_c)
 
 
+@pytest.mark.parametrize("n", [1, 15, 16, 4097])
+def test_specialised_and_generic_decode_agree(dev, n):
+    """4-bit D=128 bf16 decode: the quad-layout kernel against the generic one and the oracle,
+    including scales of 2^124 and above (the kernel's exact-product fallback) and tiny scales."""
+    import aetherkv._lib as L
+
+    rng = np.random.default_rng(n)
+    codes = rng.integers(0, 256, (n, 64)).astype(np.uint8)
+    scale = (rng.random((n, 1)) * 0.5 + 1e-3).astype(np.float32)
+    scale[::7] = np.float32(3e37)   # above 2^124: the fallback path; one small code keeps the row finite
+    codes[::7] = 0
+    codes[::7, 5] = 0x3D
+    scale[3::11] = np.float32(1.5e-38)
+    scale[5::13] = np.float32(0.0)
+    pq = PolarQuant(4)
+    c, s = torch.from_numpy(codes).to(dev), torch.from_numpy(scale).to(dev)
+    prev = L.lib().aekv_set_generic_kernels(1)
+    try:
+        gen = pq.decode(c, s)
+    finally:
+        L.lib().aekv_set_generic_kernels(prev)
+    spec = pq.decode(c, s)
+    assert torch.equal(bf16_bits_t(spec), bf16_bits_t(gen))
+    np.testing.assert_array_equal(bf16_bits(spec), O.decode(codes, scale, 4, O.diag(42, 128), "bf16"))
+
+
+def bf16_bits_t(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.int16)
+
+
 def test_empty_and_misaligned_inputs(dev):
     pq = PolarQuant(4)
     c, s = pq.encode(torch.empty(0, 128, dtype=torch.bfloat16, device=dev))
