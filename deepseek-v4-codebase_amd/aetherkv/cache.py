@@ -8,6 +8,10 @@ Drop-in (same names, fields and behaviour as the reference):
   compressed_to_bf16_for_paging      aether_2b/serving.py:378-398
 The engine's helpers are methods that read `self._polar_quant`; here the quantiser is an argument.
 
+Block emission (aether_2b/serving.py:495-505 _hca_emit, :557-576 _emit_csa_block): emit_block
+pools a block's token entries, applies RoPE and kv_norm and encodes the result in one kernel,
+into a CodeRing slot (CodeRing.append_emitted) or into fresh tensors.
+
 CodeRing is the storage the decode path reads instead: codes [B, capacity, D or D/2] and scales
 [B, capacity, 1] allocated ahead, a block append encodes straight into the next slots (capacity
 doubles when full, so appends are amortised O(1) instead of the O(S) torch.cat of _append_seq),
@@ -21,6 +25,7 @@ from typing import Dict, Optional, Tuple
 
 import torch
 
+from . import _lib
 from .decode import csa_indexer_topk_quant, quant_sink_attention
 from .turbo_quant import PolarQuant
 
@@ -175,6 +180,63 @@ def compressed_to_bf16_for_paging(quant: Optional[PolarQuant], data: Optional[to
     return quant.decode(part.contiguous(), scale[:, start:end].contiguous(), out_dtype=out_dtype)
 
 
+# ---- block emission ------------------------------------------------------------------------------
+
+def rope_inv_freq(rope_dim: int, theta: float, device=None) -> torch.Tensor:
+    """RoPE frequencies without a config: 1 / theta^(2i / rope_dim) (modeling.py:137-139).  With a
+    config (linear / YaRN scaling) pass the model's get_rope_freqs(...)[: rope_dim // 2] instead."""
+    freqs = torch.arange(0, rope_dim, 2, dtype=torch.float32)
+    return (1.0 / (theta ** (freqs / rope_dim))).to(device)
+
+
+def emit_block(quant: PolarQuant, c: torch.Tensor, z: torch.Tensor, *, bias: Optional[torch.Tensor] = None,
+               rope_dim: int = 0, positions=None, inv_freq: Optional[torch.Tensor] = None,
+               norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+               out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+               return_vector: bool = False):
+    """Pool one block per row and encode it: c, z [B, L, D] bf16 (the buffered kv_proj / z_proj
+    entries, z with its slot bias already added as the engine does, or `bias` [L, D] added here);
+    RoPE on the last `rope_dim` dims at `positions` [B] (int or tensor); RMSNorm with
+    `norm_weight` [D] (kv_norm) and `eps`.  Writes the codes/scales into `out` = (codes [B, ·],
+    scale [B, 1]) views (e.g. a ring slot) or fresh tensors [B, 1, ·] / [B, 1, 1].  Returns
+    (codes, scale) or (codes, scale, vector [B, D] bf16)."""
+    _lib.require_device("c", c, z, bias, norm_weight)
+    if c.dtype != torch.bfloat16 or z.dtype != torch.bfloat16 or c.shape != z.shape or c.dim() != 3:
+        raise RuntimeError(f"emit_block expects bf16 c, z of one shape [B, L, D], got {c.dtype} {tuple(c.shape)}, "
+                           f"{z.dtype} {tuple(z.shape)}")
+    B, L, D = c.shape
+    dev = c.device
+    bits = quant.bits
+    rb = D if bits == 8 else D // 2
+    cc, zz = c.contiguous(), z.contiguous()
+    bb = None if bias is None else bias.to(torch.bfloat16).reshape(L, D).contiguous()
+    nw = None if norm_weight is None else norm_weight.to(torch.bfloat16).reshape(D).contiguous()
+    pos = None
+    inv = None
+    if rope_dim:
+        if positions is None or inv_freq is None:
+            raise RuntimeError("emit_block: rope_dim needs positions and inv_freq")
+        pos = torch.as_tensor(positions, dtype=torch.int64, device=dev).reshape(-1).expand(B).contiguous()
+        inv = inv_freq.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    if out is None:
+        codes = torch.empty((B, 1, rb), dtype=torch.int8 if bits == 8 else torch.uint8, device=dev)
+        scale = torch.empty((B, 1, 1), dtype=torch.float32, device=dev)
+        row_stride = 1
+    else:
+        codes, scale = out
+        row_stride = codes.stride(0) // rb
+        if codes.stride(0) != scale.stride(0) * rb or codes.stride(-1) != 1:
+            raise RuntimeError("emit_block: out codes/scale must be slots of one [B, n, ·] ring")
+    vec = torch.empty((B, D), dtype=torch.bfloat16, device=dev) if return_vector else None
+    diag = quant._diag(D, dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().aekv_emit_block(
+            _lib.ptr(cc), _lib.ptr(zz), _lib.ptr(bb), B, L, D, int(rope_dim), _lib.ptr(pos), _lib.ptr(inv),
+            _lib.ptr(nw), float(eps), bits, _lib.ptr(diag), _lib.ptr(codes), _lib.ptr(scale), row_stride,
+            _lib.ptr(vec), _lib.stream_of(c)), "aekv_emit_block")
+    return (codes, scale, vec) if return_vector else (codes, scale)
+
+
 # ---- preallocated code ring -------------------------------------------------------------------
 
 class CodeRing:
@@ -241,6 +303,15 @@ class CodeRing:
         self._codes[:, self.n:self.n + m].copy_(codes)
         self._scale[:, self.n:self.n + m].copy_(scale)
         self.n += m
+        self._visible = None
+
+    def append_emitted(self, c: torch.Tensor, z: torch.Tensor, **emit_kwargs) -> None:
+        """Pool, RoPE, normalise and encode one block per row (emit_block) straight into slot n."""
+        if c.dim() != 3 or c.size(0) != self.batch or c.size(2) != self.dim:
+            raise RuntimeError(f"CodeRing.append_emitted expects [{self.batch}, L, {self.dim}], got {tuple(c.shape)}")
+        self.reserve(self.n + 1)
+        emit_block(self.quant, c, z, out=(self._codes[:, self.n], self._scale[:, self.n]), **emit_kwargs)
+        self.n += 1
         self._visible = None
 
     def visible(self) -> torch.Tensor:

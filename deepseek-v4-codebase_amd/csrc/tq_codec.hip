@@ -44,50 +44,23 @@ __global__ __launch_bounds__(kThreads) void tq_forward_kernel(const void* __rest
     const bool ok = v < n_vec;
     float a[EPL];
     load_elems<DT, EPL>(x, v * D + sub * EPL, ok, a);
-    if constexpr (MODE != kModeWht) {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) a[e] = a[e] * dg[e];  // x.float() * diag (exact sign flip)
-    }
-    wht_butterflies<D, EPL, true>(a, sub);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) a[e] = a[e] * c;  // * fp32(d ** -0.5)
-
     if constexpr (MODE == kModeWht) {
+      wht_butterflies<D, EPL, true>(a, sub);
       if (ok) {
         float* o = static_cast<float*>(out) + v * D + sub * EPL;
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) o[e] = a[e];
+        for (int e = 0; e < EPL; ++e) o[e] = a[e] * c;  // * fp32(d ** -0.5)
       }
     } else {
-      constexpr float Q = MODE == kModeEnc8 ? 127.0f : 7.0f;
-      float m = group_absmax<D, EPL, true>(a);
-      m = fmaxf(m, 1e-8f);  // clamp_(min=1e-8)
-      int q[EPL];
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        float t = a[e] / m;  // correctly rounded division (-fhip-fp32-correctly-rounded-divide-sqrt)
-        t = t * Q;
-        t = rintf(t);        // round half to even
-        t = fminf(fmaxf(t, -Q), Q);
-        q[e] = static_cast<int>(t);
-      }
+      for (int e = 0; e < EPL; ++e) a[e] = a[e] * dg[e];  // x.float() * diag (exact sign flip)
+      constexpr int BITS = MODE == kModeEnc8 ? 8 : 4;
+      constexpr int NB = BITS == 8 ? EPL : EPL / 2;
+      float m;
+      const Bytes<NB> w = encode_lane<BITS, D, true>(a, sub, c, &m);
       if (ok) {
-        if (sub == 0) out_scale[v] = m / Q;
-        if constexpr (MODE == kModeEnc8) {
-          uint8_t* o = static_cast<uint8_t*>(out) + v * D + sub * EPL;
-          Bytes<EPL> w;
-#pragma unroll
-          for (int e = 0; e < EPL; ++e) w.b[e] = static_cast<uint8_t>(q[e] & 0xff);
-          *reinterpret_cast<Bytes<EPL>*>(o) = w;
-        } else {
-          constexpr int NB = EPL / 2;
-          uint8_t* o = static_cast<uint8_t*>(out) + v * (D / 2) + sub * NB;
-          Bytes<NB> w;
-#pragma unroll
-          for (int i = 0; i < NB; ++i)
-            w.b[i] = static_cast<uint8_t>((q[2 * i] & 0x0f) | ((q[2 * i + 1] & 0x0f) << 4));
-          *reinterpret_cast<Bytes<NB>*>(o) = w;
-        }
+        if (sub == 0) out_scale[v] = m / (BITS == 8 ? 127.0f : 7.0f);
+        *reinterpret_cast<Bytes<NB>*>(static_cast<uint8_t*>(out) + v * (BITS == 8 ? D : D / 2) + sub * NB) = w;
       }
     }
   }

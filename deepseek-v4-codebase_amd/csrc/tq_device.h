@@ -106,6 +106,40 @@ __device__ __forceinline__ float group_absmax(const float (&a)[EPL]) {
 }
 
 
+// Encode of the EPL elements of one vector held by this lane, from x * diag (turbo_quant.py:
+// 127-166): WHT, * c, m = max(max|rot|, 1e-8) over the vector's lanes, q = clamp(rne(rot/m * Q)),
+// Q = 127 (8-bit) or 7 (4-bit).  Returns the lane's code bytes; *m_out = m (the scale is m / Q).
+template <int BITS, int D, bool LDS_PIPE>
+__device__ __forceinline__ Bytes<(BITS == 8 ? (D < 8 ? D : 8) : (D < 8 ? D : 8) / 2)> encode_lane(
+    float (&a)[(D < 8 ? D : 8)], int sub, float c, float* m_out) {
+  constexpr int EPL = D < 8 ? D : 8;
+  constexpr float Q = BITS == 8 ? 127.0f : 7.0f;
+  wht_butterflies<D, EPL, LDS_PIPE>(a, sub);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) a[e] = a[e] * c;  // * fp32(d ** -0.5)
+  float m = group_absmax<D, EPL, LDS_PIPE>(a);
+  m = fmaxf(m, 1e-8f);  // clamp_(min=1e-8)
+  int q[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    float t = a[e] / m;  // correctly rounded division (-fhip-fp32-correctly-rounded-divide-sqrt)
+    t = t * Q;
+    t = rintf(t);  // round half to even
+    t = fminf(fmaxf(t, -Q), Q);
+    q[e] = static_cast<int>(t);
+  }
+  *m_out = m;
+  Bytes<(BITS == 8 ? EPL : EPL / 2)> w;
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) w.b[e] = static_cast<uint8_t>(q[e] & 0xff);
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPL / 2; ++i) w.b[i] = static_cast<uint8_t>((q[2 * i] & 0x0f) | ((q[2 * i + 1] & 0x0f) << 4));
+  }
+  return w;
+}
+
 // Code bytes a lane holds for its EPL elements of one vector.
 template <int BITS, int D>
 struct LaneCodes {

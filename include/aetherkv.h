@@ -23,6 +23,8 @@
  *   aekv_quant_sink_attention        aether_2b/serving.py:507-525 (HCA) and :597-625 (CSA): dequantise,
  *                                    gather, concat window, aether_pipeline/serving.py:99-130 attention
  *   aekv_hca_compress                aether_kernels/sparse_attention.py:70-83   hca_compress(...)
+ *   aekv_emit_block                  aether_2b/serving.py:495-505 (_hca_emit) and :557-576
+ *                                    (_emit_csa_block): pool + RoPE + kv_norm + _quant_append
  *   aekv_tiled_prefill_attention     aether_kernels/sparse_attention.py:19-42   tiled_prefill_attention(...)
  */
 #ifndef AETHERKV_H_
@@ -156,6 +158,22 @@ int aekv_quant_sink_attention(const void* q, const void* codes, const float* sca
  * F32/F16/BF16, out [B,D] same dtype (hca_compress_cuda.cu:18-68; serving.py:495-497). */
 int aekv_hca_compress(const void* c, const void* z, int32_t dtype, int64_t B, int64_t M, int64_t D,
                       void* out, void* stream);
+
+/* Block emission into a code ring: for each row b, pool the block's len token entries
+ *   x = sum_m bf16(softmax_m(bf16(z + z_bias)) * c_m)      (c, z [B, len, d] bf16; z_bias [len, d]
+ *                                                           bf16 or NULL; fp32 softmax and sums)
+ * apply RoPE on the last rope_dim dims at positions[b] with frequencies inv_freq[rope_dim/2]
+ * (rope_dim 0: none), RMSNorm with norm_weight[d] bf16 and eps (NULL: none), and write the
+ * TurboQuant code of the result (bits 4/8, diag [d]) to out_codes + b*out_row_stride rows and
+ * out_scale[b*out_row_stride] — i.e. out_codes/out_scale point at the block's slot of row 0 of a
+ * [B, out_row_stride, ...] ring.  out_vec [B, d] bf16 (nullable) receives the vector before
+ * encoding.  d = 64 or 128.  Rounding points as the reference's bf16 torch ops (softmax in fp32,
+ * bf16 weights and products, fp32 sums, bf16 RoPE terms, fp32 RMSNorm); the encode is exactly
+ * aekv_tq_encode's. */
+int aekv_emit_block(const void* c, const void* z, const void* z_bias, int64_t B, int64_t len, int32_t d,
+                    int32_t rope_dim, const int64_t* positions, const float* inv_freq,
+                    const void* norm_weight, float eps, int32_t bits, const float* diag, void* out_codes,
+                    float* out_scale, int64_t out_row_stride, void* out_vec, void* stream);
 
 /* tiled_prefill_attention drop-in: sink attention of every target over all S sources,
  * oracle aether_2b/modeling.py:158-178 (sink counted once in the normaliser). */

@@ -486,3 +486,67 @@ int aekvo_hca_compress(const float* c, const float* z, int64_t B, int64_t M, int
   }
   return 0;
 }
+
+/* ------------------------------------------------------------------------------------------ */
+/* Block emission — aether_2b/serving.py:495-505 (_hca_emit) and :557-576 (_emit_csa_block,     */
+/* main and index parts), modeling.py:122-155 (apply_rope), :32-41 (RMSNorm).  bf16 tensors in  */
+/* and out, at torch CPU's rounding points (tests/test_oracle.py pins this against torch):       */
+/*   zz  = bf16(z + bias)                         (bias optional: the CSA per-slot biases)       */
+/*   w_m = bf16(exp(zz_m - max) * (1 / sum_m exp(zz_m - max)))   fp32, sums in m order          */
+/*   x   = bf16(sum_m float(bf16(w_m * c_m)))      fp32 sum in m order                          */
+/*   RoPE on the last rope_dim dims (pairs (2i, 2i+1) of that part), cos/sin =                   */
+/*     bf16(cos/sin(fp32(pos) * inv_freq[i])): even bf16(bf16(a cos) + bf16(-b sin)),            */
+/*     odd bf16(bf16(b cos) + bf16(a sin))                                                        */
+/*   RMSNorm: r = 1 / sqrt(mean(x^2) + eps) (fp32, sum in d order); y = bf16((x * r) * w)        */
+/* ------------------------------------------------------------------------------------------ */
+static inline float bf(float v) { return aekvo_bf16_to_f32(aekvo_f32_to_bf16(v)); }
+
+int aekvo_emit_block(const uint16_t* c, const uint16_t* z, const uint16_t* bias, int64_t B, int64_t L, int64_t D,
+                     int rope_dim, const int64_t* pos, const float* inv_freq, const uint16_t* norm_w, float eps,
+                     uint16_t* out) {
+  if (B < 0 || L < 1 || D < 1 || rope_dim < 0 || rope_dim > D || (rope_dim & 1)) return 1;
+  float* x = (float*)malloc(sizeof(float) * (size_t)D);
+  float* e = (float*)malloc(sizeof(float) * (size_t)L);
+  if (!x || !e) { free(x); free(e); return 2; }
+  for (int64_t b = 0; b < B; ++b) {
+    for (int64_t d = 0; d < D; ++d) {
+      float mx = -INFINITY;
+      for (int64_t m = 0; m < L; ++m) {
+        float zz = aekvo_bf16_to_f32(z[(b * L + m) * D + d]);
+        if (bias) zz = bf(zz + aekvo_bf16_to_f32(bias[m * D + d]));
+        e[m] = zz;
+        if (zz > mx) mx = zz;
+      }
+      float sum = 0.0f;
+      for (int64_t m = 0; m < L; ++m) { e[m] = expf(e[m] - mx); sum += e[m]; }
+      const float inv = 1.0f / sum;
+      float acc = 0.0f;
+      for (int64_t m = 0; m < L; ++m) {
+        const float w = bf(e[m] * inv);
+        acc += bf(w * aekvo_bf16_to_f32(c[(b * L + m) * D + d]));
+      }
+      x[d] = bf(acc);
+    }
+    if (rope_dim > 0) {
+      const int64_t r0 = D - rope_dim;
+      const float p = (float)pos[b];
+      for (int i = 0; i < rope_dim / 2; ++i) {
+        const float ang = p * inv_freq[i];
+        const float cs = bf(cosf(ang)), sn = bf(sinf(ang));
+        const float a = x[r0 + 2 * i], bb = x[r0 + 2 * i + 1];
+        x[r0 + 2 * i] = bf(bf(a * cs) + bf(-bb * sn));
+        x[r0 + 2 * i + 1] = bf(bf(bb * cs) + bf(a * sn));
+      }
+    }
+    if (norm_w) {
+      float ss = 0.0f;
+      for (int64_t d = 0; d < D; ++d) ss += x[d] * x[d];
+      const float r = 1.0f / sqrtf(ss / (float)D + eps);
+      for (int64_t d = 0; d < D; ++d) x[d] = bf((x[d] * r) * aekvo_bf16_to_f32(norm_w[d]));
+    }
+    for (int64_t d = 0; d < D; ++d) out[b * D + d] = aekvo_f32_to_bf16(x[d]);
+  }
+  free(x);
+  free(e);
+  return 0;
+}

@@ -51,6 +51,7 @@ def lib():
         L.aekvo_quant_attention.argtypes = [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I32,
                                             F64, P, I32]
         L.aekvo_hca_compress.argtypes = [P, P, I64, I64, I64, P]
+        L.aekvo_emit_block.argtypes = [P, P, P, I64, I64, I64, I32, P, P, P, ctypes.c_float, P]
         L.aekvo_wht_scale.argtypes = [I32]
         L.aekvo_wht_scale.restype = ctypes.c_float
         L.aekvo_softplus.argtypes = [F64]
@@ -201,6 +202,25 @@ def hca_compress(c: np.ndarray, z: np.ndarray) -> np.ndarray:
     B, M, D = c.shape
     out = np.empty((B, D), dtype=np.float32)
     lib().aekvo_hca_compress(_p(c), _p(z), B, M, D, _p(out))
+    return out
+
+
+def emit_block(c: np.ndarray, z: np.ndarray, bias: Optional[np.ndarray] = None, rope_dim: int = 0,
+               pos: Optional[np.ndarray] = None, inv_freq: Optional[np.ndarray] = None,
+               norm_w: Optional[np.ndarray] = None, eps: float = 1e-6) -> np.ndarray:
+    """Block emission (serving.py:495-505, :557-576): bf16 bit patterns (uint16) in and out.
+    c, z [B, L, D]; bias [L, D]; pos int64 [B]; inv_freq fp32 [rope_dim/2]; norm_w [D]."""
+    c, z = _c(c, np.uint16), _c(z, np.uint16)
+    B, L, D = c.shape
+    out = np.empty((B, D), dtype=np.uint16)
+    bias = None if bias is None else _c(bias, np.uint16)
+    pos = None if pos is None else _c(pos, np.int64)
+    inv_freq = None if inv_freq is None else _c(inv_freq, np.float32)
+    norm_w = None if norm_w is None else _c(norm_w, np.uint16)
+    rc = lib().aekvo_emit_block(_p(c), _p(z), _p(bias), B, L, D, int(rope_dim), _p(pos), _p(inv_freq), _p(norm_w),
+                                ctypes.c_float(eps), _p(out))
+    if rc != 0:
+        raise ValueError(f"aekvo_emit_block failed ({rc})")
     return out
 
 

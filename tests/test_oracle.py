@@ -394,3 +394,72 @@ def test_hca_compress_matches_softmax_weighted_sum():
     z = rng.standard_normal((2, 128, 16)).astype(np.float32) * 2
     w = scipy.special.softmax(z.astype(np.float64), axis=1)
     np.testing.assert_allclose(O.hca_compress(c, z), (w * c).sum(1), rtol=1e-6, atol=1e-7)
+
+
+# ---- block emission (serving.py:495-505 _hca_emit, :557-576 _emit_csa_block) ---------------------
+
+def _bits16(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _torch_emit(c, z, bias, rope_dim, pos, inv_freq, norm_w, eps):
+    """The engine's op sequence in torch (CPU): softmax(z.float()) -> bf16 weights -> (w * c).sum
+    -> apply_rope(config=None shape) -> F.rms_norm; bf16 tensors as in the engine."""
+    import torch.nn.functional as F
+    zz = z if bias is None else z + bias
+    w = torch.softmax(zz.float(), dim=1).to(c.dtype)
+    comp = (w * c).sum(dim=1, keepdim=True)
+    if rope_dim:
+        B = comp.size(0)
+        pp, rp = comp[..., :-rope_dim], comp[..., -rope_dim:]
+        ang = pos.float().unsqueeze(-1) * inv_freq
+        cos = torch.repeat_interleave(ang.cos(), 2, dim=-1).to(comp.dtype).view(B, 1, rope_dim)
+        sin = torch.repeat_interleave(ang.sin(), 2, dim=-1).to(comp.dtype).view(B, 1, rope_dim)
+        x1, x2 = rp[..., ::2], rp[..., 1::2]
+        rot = torch.stack((-x2, x1), dim=-1).flatten(-2)
+        comp = torch.cat([pp, rp * cos + rot * sin], dim=-1)
+    if norm_w is not None:
+        comp = F.rms_norm(comp, (comp.size(-1),), norm_w.to(comp.dtype), eps)
+    return comp.squeeze(1)
+
+
+@pytest.mark.parametrize("case", ["hca", "csa_main_first", "csa_main", "csa_index"])
+def test_emit_block_matches_torch_op_sequence(case):
+    g = torch.Generator().manual_seed({"hca": 1, "csa_main_first": 2, "csa_main": 3, "csa_index": 4}[case])
+    B, m = 5, 128
+    D = 64 if case == "csa_index" else 128
+    L = m if case == "hca" else 2 * m
+    c = torch.randn(B, L, D, generator=g).to(torch.bfloat16)
+    z = (torch.randn(B, L, D, generator=g) * 2).to(torch.bfloat16)
+    bias = None if case == "hca" else (torch.randn(L, D, generator=g) * 0.5).to(torch.bfloat16)
+    if case == "csa_main_first":  # first CSA block: prev_b_c = 0, prev_b_z = -inf (serving.py:548-552)
+        c[:, m:] = 0
+        z[:, m:] = float("-inf")
+    rope = 0 if case == "csa_index" else 64
+    pos = torch.tensor([0, 127, 4095, 65535, 262143][:B], dtype=torch.int64)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))
+    nw = None if case == "csa_index" else (torch.rand(D, generator=g) * 2).to(torch.bfloat16)
+    want = _torch_emit(c, z, bias, rope, pos, inv, nw, 1e-6)
+    got = O.emit_block(_bits16(c), _bits16(z), None if bias is None else _bits16(bias), rope,
+                       pos.numpy() if rope else None, inv.numpy() if rope else None,
+                       None if nw is None else _bits16(nw), 1e-6)
+    # libm exp/cos/sin and the order of the RMS sum may move an fp32 value by an ulp before a bf16
+    # rounding: allow one bf16 ulp (same sign), and require nearly all bits equal
+    w16 = _bits16(want).astype(np.int32)
+    g16 = got.astype(np.int32)
+    assert np.all(np.abs(g16 - w16) <= 1)
+    assert np.mean(g16 == w16) > 0.995
+
+
+def test_emit_block_pooling_reduces_to_hca_compress_and_plain_values():
+    # no RoPE / norm: the pooled value is the softmax-weighted sum (hca_compress in exact math) up to
+    # the bf16 roundings; one entry (L = 1) gives back c exactly
+    g = torch.Generator().manual_seed(3)
+    c = torch.randn(3, 128, 64, generator=g).to(torch.bfloat16)
+    z = torch.randn(3, 128, 64, generator=g).to(torch.bfloat16)
+    got = O.emit_block(_bits16(c), _bits16(z))
+    gf = torch.from_numpy(got.view(np.int16)).view(torch.bfloat16).float().numpy()
+    exact = O.hca_compress(c.float().numpy(), z.float().numpy())
+    np.testing.assert_allclose(gf, exact, rtol=2e-2, atol=2e-3)
+    one = O.emit_block(_bits16(c[:, :1]), _bits16(z[:, :1]))
+    np.testing.assert_array_equal(one, _bits16(c[:, 0]))
