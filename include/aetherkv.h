@@ -144,8 +144,10 @@ int aekv_sparse_sink_attention(const void* q, const void* kv, const void* topk, 
  *   (n_sel < 0: all S blocks in order, i.e. HCA, sel ignored; entries outside [0,S) are skipped);
  *   window [B,W,D] bf16 (W may be 0); sink fp32 [H]; out [B,H,D] bf16.
  *   Sources = [dequant(blocks[sel]), window]; K = V = source (aether_2b/serving.py:52-53).
- * Gathered code rows are dequantised on load to exactly the bf16 values PolarQuant.decode returns
- * (the engine attends its bf16 dequantised cache); logits and the value sum accumulate in fp32. */
+ * Gathered code rows are dequantised on load to the bf16 values the engine attends (its bf16
+ * dequantised cache): exactly PolarQuant.decode's values on the generic path; on the matrix-core
+ * path (D = 128, H <= 16) the transform runs as an exact int32 product and one fp32 scaling, at
+ * most one bf16 ulp from PolarQuant.decode.  Logits and the value sum accumulate in fp32. */
 size_t aekv_quant_attention_workspace_size(int64_t B, int64_t H, int64_t D, int64_t n_comp,
                                            int64_t W);
 int aekv_quant_sink_attention(const void* q, const void* codes, const float* scale,
