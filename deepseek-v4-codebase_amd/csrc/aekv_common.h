@@ -31,8 +31,8 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 bool mfma_indexer_supported(int IH, int IC, int k, int64_t S);
 size_t mfma_indexer_workspace(int64_t B, int64_t S, int32_t k);
 int launch_mfma_indexer(const float* q, const float* w, const void* codes, const float* kscale, const float* diag,
-                        const int32_t* valid, int64_t B, int64_t S, int IH, int IC, int bits, int k, int mode, void* ws,
-                        int64_t* out_idx, float* out_score, hipStream_t st, const char* who);
+                        const int32_t* valid, int64_t B, int64_t T, int64_t S, int IH, int IC, int bits, int k,
+                        int mode, void* ws, int64_t* out_idx, float* out_score, hipStream_t st, const char* who);
 bool use_specialised_codec();
 // Matrix-core decode attention for head_dim 128 (quant_attn_mfma.hip).
 bool quant_attn_mfma_supported(int64_t H, int64_t D);
@@ -41,6 +41,13 @@ int launch_quant_attn_mfma(const void* q, const void* codes, const float* scale,
                            const void* window, const float* sink, const float* diag, int64_t B, int64_t H, int64_t S,
                            int64_t K, bool all_blocks, int64_t W, int bits, float softmax_scale, void* ws,
                            void* out, hipStream_t st, const char* who);
+// Rows are targets (T per cache row) with per-row compressed counts vis and window slices
+// [wstart, wstart + wlen) of a [B / T, Wt, 128] window buffer (any of the three may be null).
+int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* scale, const int64_t* sel,
+                                const int32_t* vis, const void* window, const int32_t* wstart, const int32_t* wlen,
+                                const float* sink, const float* diag, int64_t rows, int64_t T, int64_t H, int64_t S,
+                                int64_t K, bool all_blocks, int64_t Wt, int bits, float softmax_scale, void* ws,
+                                void* out, hipStream_t st, const char* who);
 
 // ---- device helpers ------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __builtin_bit_cast(float, bits16 << 16); }

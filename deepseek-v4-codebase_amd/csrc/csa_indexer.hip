@@ -134,6 +134,7 @@ struct IndexerArgs {
   const float* diag;     // [IC] (quantised keys)
   const int32_t* valid;  // [B] or null
   int64_t S;
+  int64_t T;             // rows per key row: row b scores the keys of key row b / T
   int IH, IC, k, mode, n_chunks;
   float wscale;          // fp32(IC ** -0.5) for the query rotation
   uint32_t* cand_key;    // [B, n_chunks, k]
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void idx_score_chunk_kernel(IndexerArgs a
   // scores
   for (int t = threadIdx.x; t < n; t += kThreads) {
     const int64_t j = j0 + t;
-    const int64_t row = static_cast<int64_t>(b) * S + j;
+    const int64_t row = static_cast<int64_t>(b) / a.T * S + j;
     float acc = 0.0f;
     for (int h = 0; h < IH; ++h) {
       const float* qh = qs + h * IC;
@@ -392,6 +393,7 @@ extern "C" int aekv_csa_indexer_topk(const float* index_q, const float* index_kv
   a.w = index_weight;
   a.keys = index_kv;
   a.valid = valid;
+  a.T = 1;
   a.IH = IH;
   a.IC = IC;
   a.k = k;
@@ -399,18 +401,25 @@ extern "C" int aekv_csa_indexer_topk(const float* index_q, const float* index_kv
   return launch_indexer(kKeyF32, a, B, S, ws, out_idx, out_score, as_stream(stream), who);
 }
 
-extern "C" int aekv_csa_indexer_topk_quant(const float* index_q, const float* index_weight, const void* key_codes,
-                                           const float* key_scale, const float* diag, const int32_t* valid, int64_t B,
-                                           int64_t S, int32_t IH, int32_t IC, int32_t bits, int32_t k, int32_t mode,
-                                           void* ws, size_t ws_bytes, int64_t* out_idx, float* out_score,
-                                           void* stream) {
-  const char* who = "aekv_csa_indexer_topk_quant";
+namespace {
+
+// rows = B * T query rows; row r scores the codes of key row r / T
+int topk_quant_rows(const float* index_q, const float* index_weight, const void* key_codes, const float* key_scale,
+                    const float* diag, const int32_t* valid, int64_t B, int64_t T, int64_t S, int32_t IH, int32_t IC,
+                    int32_t bits, int32_t k, int32_t mode, void* ws, size_t ws_bytes, int64_t* out_idx,
+                    float* out_score, void* stream, const char* who) {
   if (bits != 4 && bits != 8) return fail(AEKV_ERR_VALUE, "bits must be 4 or 8, got %d", bits);
   if (!is_pow2(IC)) return fail(AEKV_ERR_VALUE, "WHT requires last dim to be a power of 2, got %d", IC);
   if (bits == 4 && IC < 2) return fail(AEKV_ERR_VALUE, "4-bit packing needs an even last dim, got %d", IC);
-  if (int rc = validate_common(index_q, index_weight, B, S, IH, IC, k, mode, ws, ws_bytes, out_idx, who)) return rc;
-  if (B == 0) return AEKV_OK;
+  if (B < 0 || T < 1) return fail(AEKV_ERR_SHAPE, "%s: B=%lld T=%lld", who, (long long)B, (long long)T);
+  if (B > 0 && T > 65535 / B) return fail(AEKV_ERR_UNSUPPORTED, "%s: B*T exceeds 65535", who);
+  const int64_t rows = B * T;
+  if (int rc = validate_common(index_q, index_weight, rows, S, IH, IC, k, mode, ws, ws_bytes, out_idx, who)) return rc;
+  if (rows == 0) return AEKV_OK;
   if (S > 0 && (!key_codes || !key_scale || !diag)) return fail(AEKV_ERR_VALUE, "%s: null key pointer", who);
+  if (use_specialised_codec() && mfma_indexer_supported(IH, IC, k, S))
+    return launch_mfma_indexer(index_q, index_weight, key_codes, key_scale, diag, valid, rows, T, S, IH, IC, bits, k,
+                               mode, ws, out_idx, out_score, as_stream(stream), who);
   IndexerArgs a{};
   a.q = index_q;
   a.w = index_weight;
@@ -418,12 +427,31 @@ extern "C" int aekv_csa_indexer_topk_quant(const float* index_q, const float* in
   a.kscale = key_scale;
   a.diag = diag;
   a.valid = valid;
+  a.T = T;
   a.IH = IH;
   a.IC = IC;
   a.k = k;
   a.mode = mode;
-  if (use_specialised_codec() && mfma_indexer_supported(IH, IC, k, S))
-    return launch_mfma_indexer(index_q, index_weight, key_codes, key_scale, diag, valid, B, S, IH, IC, bits, k, mode, ws,
-                               out_idx, out_score, as_stream(stream), who);
-  return launch_indexer(bits == 8 ? kKeyQ8 : kKeyQ4, a, B, S, ws, out_idx, out_score, as_stream(stream), who);
+  return launch_indexer(bits == 8 ? kKeyQ8 : kKeyQ4, a, rows, S, ws, out_idx, out_score, as_stream(stream), who);
+}
+
+}  // namespace
+
+extern "C" int aekv_csa_indexer_topk_quant(const float* index_q, const float* index_weight, const void* key_codes,
+                                           const float* key_scale, const float* diag, const int32_t* valid, int64_t B,
+                                           int64_t S, int32_t IH, int32_t IC, int32_t bits, int32_t k, int32_t mode,
+                                           void* ws, size_t ws_bytes, int64_t* out_idx, float* out_score,
+                                           void* stream) {
+  return topk_quant_rows(index_q, index_weight, key_codes, key_scale, diag, valid, B, 1, S, IH, IC, bits, k, mode, ws,
+                         ws_bytes, out_idx, out_score, stream, "aekv_csa_indexer_topk_quant");
+}
+
+extern "C" int aekv_csa_prefill_indexer_topk_quant(const float* index_q, const float* index_weight,
+                                                   const void* key_codes, const float* key_scale, const float* diag,
+                                                   const int32_t* valid, int64_t B, int64_t T, int64_t S, int32_t IH,
+                                                   int32_t IC, int32_t bits, int32_t k, int32_t mode, void* ws,
+                                                   size_t ws_bytes, int64_t* out_idx, float* out_score,
+                                                   void* stream) {
+  return topk_quant_rows(index_q, index_weight, key_codes, key_scale, diag, valid, B, T, S, IH, IC, bits, k, mode, ws,
+                         ws_bytes, out_idx, out_score, stream, "aekv_csa_prefill_indexer_topk_quant");
 }

@@ -76,6 +76,7 @@ struct MfmaIdxArgs {
   const float* diag;     // [IC]
   const int32_t* valid;  // [B] or null
   int64_t S;
+  int64_t T;             // rows per key row: row b scores the keys of key row b / T
   int IH, k, mode;
   int gpw;               // slot groups per wave in the score kernel
   float wscale;
@@ -362,8 +363,9 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a)
   float f[NRB][4], lo[NRB], hi[NRB];
   query_fragments<BITS, IC, NRB>(a, b, dig, hf, hb, A, f, lo, hi);
 
-  const uint8_t* crow = a.codes + static_cast<int64_t>(b) * S * RB;
-  const float* srow = a.kscale + static_cast<int64_t>(b) * S;
+  const int64_t kr = static_cast<int64_t>(b) / a.T;
+  const uint8_t* crow = a.codes + kr * S * RB;
+  const float* srow = a.kscale + kr * S;
   uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.ks;
   uint32_t* mrow = a.smax + static_cast<int64_t>(b) * a.ms;
   constexpr int64_t kGroupKeys = SPW * 64;
@@ -792,9 +794,10 @@ bool mfma_indexer_supported(int IH, int IC, int k, int64_t S) {
 }
 
 int launch_mfma_indexer(const float* q, const float* w, const void* codes, const float* kscale, const float* diag,
-                        const int32_t* valid, int64_t B, int64_t S, int IH, int IC, int bits, int k, int mode, void* ws,
-                        int64_t* out_idx, float* out_score, hipStream_t st, const char* who) {
+                        const int32_t* valid, int64_t B, int64_t T, int64_t S, int IH, int IC, int bits, int k,
+                        int mode, void* ws, int64_t* out_idx, float* out_score, hipStream_t st, const char* who) {
   MfmaIdxArgs a{};
+  a.T = T;
   a.q = q;
   a.w = w;
   a.codes = static_cast<const uint8_t*>(codes);

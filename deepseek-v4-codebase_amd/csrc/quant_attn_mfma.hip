@@ -45,10 +45,18 @@ struct QAttnMfmaArgs {
   const uint8_t* codes;   // [B, S, 128 or 64]
   const float* scale;     // [B, S]
   const int64_t* sel;     // [B, K] or null (every block)
-  const uint16_t* win;    // [B, W, 128] bf16
+  const uint16_t* win;    // [B / T, Wt, 128] bf16
   const float* sink;      // [H]
   const float* diag;      // [128]
-  int64_t S, K, W, n_comp, n_src;
+  // Rows are targets: row r reads cache row r / T (codes, scale, window); q, sel, out are per row.
+  // Per-row sources: vis[r] compressed blocks (null: n_comp), window entries
+  // [wstart[r], wstart[r] + wlen[r]) of its cache row (null: wstart 0, wlen to the end of the
+  // Wt entries); all clamped to the buffers.
+  const int32_t* vis;
+  const int32_t* wstart;
+  const int32_t* wlen;
+  int64_t T, Wt;
+  int64_t S, K, n_comp, n_src;
   int H, n_split;
   float sm_scale, wscale;
   float* part;            // [B, n_split, H, 2 + 128] (split runs only)
@@ -92,11 +100,16 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int H = a.H;
 
+  // the row's sources: n_comp compressed blocks, then wl window entries from w0 of its cache row
+  const int64_t cb = b / a.T;
+  const int64_t n_comp = a.vis ? min<int64_t>(max(a.vis[b], 0), a.n_comp) : a.n_comp;
+  const int64_t w0 = a.wstart ? min<int64_t>(max(a.wstart[b], 0), a.Wt) : 0;
+  const int64_t wl = a.wlen ? min<int64_t>(max(a.wlen[b], 0), a.Wt - w0) : a.Wt - w0;
   // this workgroup's sources [src0, src1); the selected block ids go to LDS (-1: skipped)
   const int64_t src0 = static_cast<int64_t>(split) * kSplitSrc;
-  const int64_t src1 = min<int64_t>(a.n_src, src0 + kSplitSrc);
+  const int64_t src1 = min<int64_t>(n_comp + wl, src0 + kSplitSrc);
   if (a.sel) {
-    const int64_t nsel = min<int64_t>(src1, a.n_comp) - src0;
+    const int64_t nsel = min<int64_t>(src1, n_comp) - src0;
     for (int64_t i = threadIdx.x; i < nsel; i += kThreads) {
       const int64_t blk = a.sel[b * a.K + src0 + i];
       sidx[i] = blk >= 0 && blk < a.S ? static_cast<int32_t>(blk) : -1;
@@ -165,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
   for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const float kscale_unit = (BITS == 4 ? 1.0f / 16.0f : 1.0f) * a.wscale;
 
-  const int n_groups = static_cast<int>((src1 - src0 + kGroup - 1) / kGroup);
+  const int n_groups = src1 > src0 ? static_cast<int>((src1 - src0 + kGroup - 1) / kGroup) : 0;
 #pragma unroll 1
   for (int G = wv; G < n_groups; G += kWaves) {
     // both blocks' rows are requested before either is decoded (two gathers in flight)
@@ -179,7 +192,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
       const int64_t si = src0 + static_cast<int64_t>(G) * kGroup + 16 * kb + c16;
       kind[kb] = 0;
       int64_t blk = -1;
-      if (si < a.n_comp) {
+      if (si < n_comp) {
         blk = a.sel ? sidx[si - src0] : si;
         kind[kb] = blk >= 0 ? 1 : 0;
       } else if (si < src1) {
@@ -191,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
         for (int e = 0; e < (BITS == 8 ? 4 : 2); ++e) cw[kb][hh][e] = 0u;
       sraw[kb] = 0.0f;
       if (kind[kb] == 1) {
-        const uint8_t* row = a.codes + (b * a.S + blk) * RB;
+        const uint8_t* row = a.codes + (cb * a.S + blk) * RB;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           if constexpr (BITS == 8) {
@@ -206,10 +219,10 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
             cw[kb][hh][1] = v.y;
           }
         }
-        sraw[kb] = a.scale[b * a.S + blk];
+        sraw[kb] = a.scale[cb * a.S + blk];
       }
       if (kind[kb] == 2) {
-        const uint16_t* wr = a.win + (b * a.W + (si - a.n_comp)) * kD + 4 * g;
+        const uint16_t* wr = a.win + (cb * a.Wt + w0 + (si - n_comp)) * kD + 4 * g;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           wv2[kb][ks][0] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks));
@@ -421,26 +434,33 @@ size_t quant_attn_mfma_workspace(int64_t B, int64_t H, int64_t n_src) {
   return n_split > 1 ? align_up(static_cast<size_t>(B * n_split * H * (kD + 2)) * 4, 256) : 0;
 }
 
-int launch_quant_attn_mfma(const void* q, const void* codes, const float* scale, const int64_t* sel,
-                           const void* window, const float* sink, const float* diag, int64_t B, int64_t H, int64_t S,
-                           int64_t K, bool all_blocks, int64_t W, int bits, float softmax_scale, void* ws,
-                           void* out, hipStream_t st, const char* who) {
+int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* scale, const int64_t* sel,
+                                const int32_t* vis, const void* window, const int32_t* wstart, const int32_t* wlen,
+                                const float* sink, const float* diag, int64_t rows, int64_t T, int64_t H, int64_t S,
+                                int64_t K, bool all_blocks, int64_t Wt, int bits, float softmax_scale, void* ws,
+                                void* out, hipStream_t st, const char* who) {
   QAttnMfmaArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.codes = static_cast<const uint8_t*>(codes);
   a.scale = scale;
   a.sel = all_blocks ? nullptr : sel;
+  a.vis = vis;
   a.win = static_cast<const uint16_t*>(window);
+  a.wstart = wstart;
+  a.wlen = wlen;
   a.sink = sink;
   a.diag = diag;
+  a.T = T;
+  a.Wt = Wt;
   a.S = S;
   a.K = K;
-  a.W = W;
   a.n_comp = all_blocks ? S : K;
-  a.n_src = a.n_comp + W;
+  a.n_src = a.n_comp + Wt;  // an upper bound of every row's sources
   a.H = static_cast<int>(H);
   const int64_t n_split = a.n_src > 0 ? ceil_div(a.n_src, kSplitSrc) : 1;
-  if (n_split > 65535) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many sources", who);
+  if (n_split > 65535 || rows > 65535)
+    return fail(AEKV_ERR_UNSUPPORTED, "%s: %lld rows x %lld sources exceed the launch grid", who,
+                static_cast<long long>(rows), static_cast<long long>(a.n_src));
   a.n_split = static_cast<int>(n_split);
   a.sm_scale = softmax_scale;
   a.wscale = wht_scale(kD);
@@ -452,13 +472,22 @@ int launch_quant_attn_mfma(const void* q, const void* codes, const float* scale,
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                               static_cast<int>(kLds));
   });
-  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(n_split), static_cast<uint32_t>(B)), dim3(kThreads), kLds, st, a);
+  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(n_split), static_cast<uint32_t>(rows)), dim3(kThreads), kLds, st,
+                     a);
   if (int rc = check_launch(who)) return rc;
   if (n_split > 1) {
-    hipLaunchKernelGGL(quant_attn_mfma_combine_kernel, dim3(static_cast<uint32_t>(B)), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(quant_attn_mfma_combine_kernel, dim3(static_cast<uint32_t>(rows)), dim3(kThreads), 0, st, a);
     return check_launch(who);
   }
   return AEKV_OK;
+}
+
+int launch_quant_attn_mfma(const void* q, const void* codes, const float* scale, const int64_t* sel,
+                           const void* window, const float* sink, const float* diag, int64_t B, int64_t H, int64_t S,
+                           int64_t K, bool all_blocks, int64_t W, int bits, float softmax_scale, void* ws,
+                           void* out, hipStream_t st, const char* who) {
+  return launch_quant_attn_mfma_rows(q, codes, scale, sel, nullptr, window, nullptr, nullptr, sink, diag, B, 1, H, S,
+                                     K, all_blocks, W, bits, softmax_scale, ws, out, st, who);
 }
 
 }  // namespace aekv

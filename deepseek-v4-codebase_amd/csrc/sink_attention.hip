@@ -484,6 +484,41 @@ extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const
   return check_launch(who);
 }
 
+extern "C" size_t aekv_quant_prefill_workspace_size(int64_t B, int64_t T, int64_t H, int64_t n_comp, int64_t Wt) {
+  if (B <= 0 || T <= 0 || H <= 0) return 256;
+  return std::max<size_t>(256, quant_attn_mfma_workspace(B * T, H, std::max<int64_t>(n_comp, 0) + std::max<int64_t>(Wt, 0)));
+}
+
+extern "C" int aekv_quant_prefill_attention(const void* q, const void* codes, const float* scale, const int64_t* sel,
+                                            const int32_t* visible, const void* window, const int32_t* win_start,
+                                            const int32_t* win_len, const float* sink, const float* diag, int64_t B,
+                                            int64_t T, int64_t H, int64_t D, int64_t S, int64_t n_sel, int64_t Wt,
+                                            int32_t bits, float softmax_scale, void* ws, size_t ws_bytes, void* out,
+                                            void* stream) {
+  const char* who = "aekv_quant_prefill_attention";
+  if (bits != 4 && bits != 8) return fail(AEKV_ERR_VALUE, "bits must be 4 or 8, got %d", bits);
+  if (!quant_attn_mfma_supported(H, D))
+    return fail(AEKV_ERR_UNSUPPORTED, "%s: head_dim %lld with %lld heads (128 and at most 16 supported)", who,
+                (long long)D, (long long)H);
+  if (B < 0 || T < 1 || S < 0 || Wt < 0) return fail(AEKV_ERR_SHAPE, "%s: bad sizes", who);
+  if (B > 0 && T > 65535 / B) return fail(AEKV_ERR_UNSUPPORTED, "%s: B*T exceeds 65535", who);
+  const bool all_blocks = n_sel < 0;  // HCA: blocks 0 .. visible-1 in order
+  const int64_t K = all_blocks ? 0 : n_sel;
+  const int64_t n_comp = all_blocks ? S : K;
+  if (B == 0) return AEKV_OK;
+  if (!q || !sink || !diag || !out || (n_comp > 0 && (!codes || !scale)) || (Wt > 0 && !window) || (K > 0 && !sel))
+    return fail(AEKV_ERR_VALUE, "%s: null pointer", who);
+  if (!is_aligned(q, 16) || !is_aligned(out, 8) || !is_aligned(diag, 16) || (n_comp > 0 && !is_aligned(codes, 16)) ||
+      (Wt > 0 && !is_aligned(window, 16)) || !is_aligned(sink, 4) || (scale && !is_aligned(scale, 4)))
+    return fail(AEKV_ERR_ALIGN, "%s: misaligned pointer", who);
+  const size_t need = quant_attn_mfma_workspace(B * T, H, n_comp + Wt);
+  if (need > 0 && (!ws || ws_bytes < need))
+    return fail(AEKV_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who, need, ws_bytes);
+  // without per-target window slices every target sees the whole [0, Wt) window
+  return launch_quant_attn_mfma_rows(q, codes, scale, sel, visible, window, win_start, win_len, sink, diag, B * T, T,
+                                     H, S, K, all_blocks, Wt, bits, softmax_scale, ws, out, as_stream(stream), who);
+}
+
 extern "C" int aekv_hca_compress(const void* c, const void* z, int32_t dtype, int64_t B, int64_t M, int64_t D, void* out,
                                  void* stream) {
   const char* who = "aekv_hca_compress";

@@ -125,6 +125,17 @@ int aekv_csa_indexer_topk_quant(const float* index_q, const float* index_weight,
                                 int32_t bits, int32_t k, int32_t mode, void* ws, size_t ws_bytes,
                                 int64_t* out_idx, float* out_score, void* stream);
 
+/* Chunked-prefill variant: T targets per sequence (modeling.py:496-534, the per-target indexer of
+ * _forward_tiled_prefill).  index_q [B,T,IH,IC], index_weight [B,T,IH], valid [B,T] (target t of
+ * row b scores blocks j < valid[b,t] of key row b: its causally visible blocks), out_idx
+ * [B,T,k], out_score [B,T,k]; keys as aekv_csa_indexer_topk_quant.  Workspace:
+ * aekv_csa_indexer_workspace_size(B * T, S, k).  B * T <= 65535. */
+int aekv_csa_prefill_indexer_topk_quant(const float* index_q, const float* index_weight,
+                                        const void* key_codes, const float* key_scale, const float* diag,
+                                        const int32_t* valid, int64_t B, int64_t T, int64_t S, int32_t IH,
+                                        int32_t IC, int32_t bits, int32_t k, int32_t mode, void* ws,
+                                        size_t ws_bytes, int64_t* out_idx, float* out_score, void* stream);
+
 /* ---- attention ----------------------------------------------------------------------------- */
 /* Drop-in sparse sink attention (sparse_sink_attention_cuda.cu semantics, oracle
  * aether_pipeline/serving.py:99-130):
@@ -155,6 +166,26 @@ int aekv_quant_sink_attention(const void* q, const void* codes, const float* sca
                               const float* diag, int64_t B, int64_t H, int64_t D, int64_t S,
                               int64_t n_sel, int64_t W, int32_t bits, float softmax_scale,
                               void* ws, size_t ws_bytes, void* out, void* stream);
+
+/* Chunked prefill through the quantised reader (modeling.py:293-337 HCA and :496-550 CSA
+ * _forward_tiled_prefill, whose per-target tiled_prefill_attention calls, sparse_attention.py:19-42,
+ * become one launch): target t of row b attends
+ *   [dequant(blocks of its selection), window[b, win_start[b,t] : win_start[b,t] + win_len[b,t]]]
+ * with K = V and the per-head sink.  Its blocks: sel[b,t,0 : visible[b,t]] (n_sel >= 0; entries
+ * outside [0,S) skipped) or blocks 0 .. visible[b,t]-1 in order (n_sel < 0, HCA); visible NULL means
+ * n_sel (or S).  win_start / win_len NULL mean 0 / the rest of the Wt entries; every count is
+ * clamped to its buffer.  q [B,T,H,D] bf16, codes [B,S,D or D/2] + scale [B,S], window [B,Wt,D]
+ * bf16, sink fp32 [H], out [B,T,H,D] bf16; a target with no sources gets zeros.  Dequantised values
+ * as the matrix-core path of aekv_quant_sink_attention (D = 128, H <= 16 only; pointers 16-byte
+ * aligned, out 8-byte).  Workspace: aekv_quant_prefill_workspace_size(B, T, H, n_comp, Wt) with
+ * n_comp = n_sel (or S).  B * T <= 65535. */
+size_t aekv_quant_prefill_workspace_size(int64_t B, int64_t T, int64_t H, int64_t n_comp, int64_t Wt);
+int aekv_quant_prefill_attention(const void* q, const void* codes, const float* scale, const int64_t* sel,
+                                 const int32_t* visible, const void* window, const int32_t* win_start,
+                                 const int32_t* win_len, const float* sink, const float* diag, int64_t B,
+                                 int64_t T, int64_t H, int64_t D, int64_t S, int64_t n_sel, int64_t Wt,
+                                 int32_t bits, float softmax_scale, void* ws, size_t ws_bytes, void* out,
+                                 void* stream);
 
 /* hca_compress drop-in: out[b,d] = sum_m softmax_m(z[b,:,d]) * c[b,m,d], c/z [B,M,D], dtype
  * F32/F16/BF16, out [B,D] same dtype (hca_compress_cuda.cu:18-68; serving.py:495-497). */

@@ -1,0 +1,164 @@
+"""GPU tests of chunked prefill through the quantised reader (aetherkv.prefill).
+
+Each target of a chunk is checked three ways:
+  * against the oracle's decode-step attention on that target's own sources (its visible blocks or
+    its indexer selection, and its window slice; modeling.py:316-325 / :521-539), within the bf16
+    tolerance of the quantised attention tests;
+  * bit for bit against the decode entry point called once per target on the same sources (the
+    prefill launch must reproduce the per-target launches exactly);
+  * the multi-target indexer bit for bit against the single-target indexer per target, and its
+    selection against the oracle's exact top-k up to fp32 near-ties.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from aetherkv import PolarQuant
+from aetherkv.decode import csa_indexer_topk_quant, quant_sink_attention
+from aetherkv.prefill import (csa_prefill, csa_prefill_indexer_topk_quant, hca_prefill, prefill_sources,
+                              quant_prefill_attention)
+from aetherkv.synthetic import normal
+from conftest import to_np_f32
+from topk_check import assert_topk_matches, score_error_bound
+
+pytestmark = pytest.mark.gpu
+
+QUANT_RTOL, QUANT_ATOL = 1e-2, 2e-3  # bf16 output, as the decode-step quantised attention tests
+
+
+def _inputs(dev, B, T, H, S, Wt, bits, seed, D=128):
+    pq = PolarQuant(bits)
+    codes, scale = pq.encode(normal((B, S, D), seed).to(dev))
+    q = normal((B, T, H, D), seed + 1).to(dev)
+    win = normal((B, Wt, D), seed + 2).to(dev)
+    sink = normal((H,), seed + 3, dtype=torch.float32).to(dev)
+    return pq, codes, scale, q, win, sink
+
+
+def _oracle_target(pq, codes, scale, sel_np, q_t, win_t, sink, sm):
+    B, H, D = q_t.shape
+    return O.quant_attention(to_np_f32(q_t), codes.cpu().numpy(), scale.cpu().numpy(), sel_np, to_np_f32(win_t),
+                             to_np_f32(sink), O.diag(42, D), pq.bits, sm)
+
+
+@pytest.mark.parametrize("bits,B,T,H,start,M,W,nb,S", [
+    (4, 2, 40, 12, 100, 8, 16, 17, 24),     # capacity past the emitted blocks; targets cross block edges
+    (8, 3, 33, 16, 0, 4, 8, 8, 8),          # first chunk: the early targets see no block
+    (4, 2, 6, 12, 9000, 8, 128, 1130, 1200),  # ~1250 sources per target: split rows + combine
+])
+def test_hca_prefill_matches_oracle_and_decode(dev, bits, B, T, H, start, M, W, nb, S):
+    Wt = W - 1 + T
+    pq, codes, scale, q, win, sink = _inputs(dev, B, T, H, S, Wt, bits, 7 + T)
+    sm = 128 ** -0.5
+    print(f"hca prefill bits={bits} B={B} T={T} H={H} start={start} nb={nb}", flush=True)
+    out = hca_prefill(q, codes, scale, win, sink, sm, kv_quant=pq, start=start, n_blocks=nb, compression=M,
+                      sliding_window=W)
+    torch.cuda.synchronize()
+    assert out.shape == (B, T, H, 128) and out.dtype == torch.bfloat16
+    vis, ws, wl = prefill_sources(T, start, nb, compression=M, sliding_window=W, window_base=start + T - Wt,
+                                  window_len=Wt)
+    for t in range(T):
+        g, s0, n = int(vis[t]), int(ws[t]), int(wl[t])
+        win_t = win[:, s0:s0 + n].contiguous()
+        sel = np.tile(np.arange(g, dtype=np.int64), (B, 1))
+        want = _oracle_target(pq, codes, scale, sel, q[:, t], win_t, sink, sm)
+        np.testing.assert_allclose(to_np_f32(out[:, t]), want, rtol=QUANT_RTOL, atol=QUANT_ATOL,
+                                   err_msg=f"target {t}")
+        # the decode entry point on the same sources (blocks 0..g-1 in order, the same window slice)
+        dec = quant_sink_attention(q[:, t], codes[:, :g].contiguous(), scale[:, :g].contiguous(), None, win_t, sink,
+                                   sm, quant=pq)
+        assert torch.equal(out[:, t], dec), f"target {t} differs from the decode launch"
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_csa_prefill_matches_oracle_and_decode(dev, bits):
+    B, T, H, IH, IC, M, W, top_k = 2, 48, 12, 4, 64, 4, 16, 5
+    start, nb = 20, 17  # positions 20..67: 5..16 visible blocks, more than top_k from position 24 on
+    Wt = W - 1 + T
+    pq, codes, scale, q, win, sink = _inputs(dev, B, T, H, 24, Wt, bits, 50 + bits)
+    ix_codes, ix_scale = pq.encode(normal((B, 24, IC), 60 + bits).to(dev))
+    index_q = normal((B, T, IH, IC), 61, dtype=torch.float32).to(dev)
+    index_w = normal((B, T, IH), 62, dtype=torch.float32).to(dev)
+    sm = 128 ** -0.5
+    print(f"csa prefill bits={bits}", flush=True)
+    out, idx = csa_prefill(q, index_q, index_w, ix_codes, ix_scale, codes, scale, win, sink, sm, kv_quant=pq,
+                           start=start, n_blocks=nb, compression=M, sliding_window=W, top_k=top_k)
+    torch.cuda.synchronize()
+    assert idx.shape == (B, T, top_k) and out.shape == (B, T, H, 128)
+    vis, ws, wl = prefill_sources(T, start, nb, compression=M, sliding_window=W, window_base=start + T - Wt,
+                                  window_len=Wt)
+    keys = O.decode(ix_codes.cpu().numpy(), ix_scale.cpu().numpy(), bits, O.diag(42, IC), "f32")
+    for t in range(T):
+        g, s0, n = int(vis[t]), int(ws[t]), int(wl[t])
+        k_eff = min(top_k, g)
+        # the target's selection: one indexer row per target vs the single-target indexer
+        one = csa_indexer_topk_quant(index_q[:, t], index_w[:, t], ix_codes, ix_scale, top_k, quant=pq,
+                                     valid=torch.full((B,), g, dtype=torch.int32, device=dev))
+        assert torch.equal(idx[:, t], one), f"target {t}: selection differs from the single-target indexer"
+        qn, wn = index_q[:, t].cpu().numpy(), index_w[:, t].cpu().numpy()
+        scores = O.index_scores(qn, wn, keys, valid=np.full(B, g, np.int32))
+        wa = np.log1p(np.exp(wn.astype(np.float64)))
+        tol = score_error_bound(qn, wa, keys, extra_rel=16 * math.log2(IC) * 2.0 ** -24)
+        assert_topk_matches(idx[:, t].cpu().numpy(), scores, top_k, tol, np.full(B, g))
+        # attention over the selected blocks and the window slice
+        sel = idx[:, t, :k_eff].contiguous()
+        win_t = win[:, s0:s0 + n].contiguous()
+        want = _oracle_target(pq, codes, scale, sel.cpu().numpy(), q[:, t], win_t, sink, sm)
+        np.testing.assert_allclose(to_np_f32(out[:, t]), want, rtol=QUANT_RTOL, atol=QUANT_ATOL,
+                                   err_msg=f"target {t}")
+        dec = quant_sink_attention(q[:, t], codes, scale, sel, win_t, sink, sm, quant=pq)
+        assert torch.equal(out[:, t], dec), f"target {t} differs from the decode launch"
+
+
+def test_multi_target_indexer_ragged_valid(dev):
+    # per-(row, target) visible counts, including 0 and counts below k
+    B, T, S, IH, IC, k = 3, 7, 3000, 4, 64, 64
+    pq = PolarQuant(4)
+    codes, scale = pq.encode(normal((B, S, IC), 71).to(dev))
+    index_q = normal((B, T, IH, IC), 72, dtype=torch.float32).to(dev)
+    index_w = normal((B, T, IH), 73, dtype=torch.float32).to(dev)
+    valid = torch.tensor([[0, 1, 63, 64, 65, 2999, 3000], [5, 5, 5, 5, 5, 5, 5], [3000, 0, 1000, 17, 64, 1, 2]],
+                         dtype=torch.int32)
+    print("multi-target indexer ragged", flush=True)
+    idx, sc = csa_prefill_indexer_topk_quant(index_q, index_w, codes, scale, k, quant=pq, valid=valid,
+                                             return_scores=True)
+    torch.cuda.synchronize()
+    for t in range(T):
+        one, sc1 = csa_indexer_topk_quant(index_q[:, t], index_w[:, t], codes, scale, k, quant=pq,
+                                          valid=valid[:, t].to(dev), return_scores=True)
+        assert torch.equal(idx[:, t], one), f"target {t}"
+        assert torch.equal(sc[:, t], sc1), f"target {t} scores"
+    assert bool((idx[0, 0] == -1).all()) and int((idx[1] >= 0).sum(-1).max()) == 5
+
+
+def test_prefill_attention_defaults_and_empty_targets(dev):
+    # visible / window slices omitted: every target sees all n_sel blocks and the whole window; a
+    # target with no source at all gets zeros (serving.py:451-452)
+    B, T, H, S, Wt = 2, 3, 4, 40, 6
+    pq, codes, scale, q, win, sink = _inputs(dev, B, T, H, S, Wt, 8, 91)
+    sel = torch.randint(0, S, (B, T, 9), generator=torch.Generator().manual_seed(1)).to(dev)
+    sel[0, 1, :4] = -1
+    sm = 0.2
+    print("prefill defaults and empty targets", flush=True)
+    out = quant_prefill_attention(q, codes, scale, sel, win, sink, sm, quant=pq)
+    for t in range(T):
+        dec = quant_sink_attention(q[:, t], codes, scale, sel[:, t].contiguous(), win, sink, sm, quant=pq)
+        assert torch.equal(out[:, t], dec), f"target {t}"
+    zeros = torch.zeros(T, dtype=torch.int32)
+    out = quant_prefill_attention(q, codes, scale, sel, win, sink, sm, quant=pq, visible=zeros, win_len=zeros)
+    torch.cuda.synchronize()
+    assert not bool(out.float().abs().sum())
+
+
+def test_prefill_rejects_unsupported_shapes(dev):
+    pq = PolarQuant(4)
+    q = torch.zeros(1, 2, 17, 128, dtype=torch.bfloat16, device=dev)  # 17 heads: above the matrix-core limit
+    codes = torch.zeros(1, 3, 64, dtype=torch.uint8, device=dev)
+    with pytest.raises(RuntimeError, match="16 supported"):
+        quant_prefill_attention(q, codes, torch.ones(1, 3, device=dev), None, None, torch.zeros(17, device=dev),
+                                0.1, quant=pq)
