@@ -8,7 +8,9 @@ Metric: "KV quant GB/s (4-bit, 262K ctx) + CSA sparse-decode tokens/s, 1 GPU".
 algorithmic bytes (805,306,368 read + 201,326,592 codes + 12,582,912 scales = 1,019,215,872 B per
 step), inputs resident in HBM.  One step = one encode of the whole layer (one kernel launch).
 The same line carries, under "secondary", cfg2 decode GB/s, CSA sparse decode tokens/s (cfg5 and
-cfg3), HCA decode tokens/s (cfg4) and the reference microbenchmark shape of sparse_sink_attention.
+cfg3), HCA decode tokens/s (cfg4), chunked-prefill targets/s through the quantised reader (a chunk of
+256 targets per sequence over cfg3's and cfg4's caches) and the reference microbenchmark shape of
+sparse_sink_attention.
 
 Timing: W untimed warmup steps, then K steps bracketed by torch.cuda.synchronize() and HIP events
 recorded on the stream the kernels run on (torch's current stream).  Decode steps (indexer +
@@ -248,6 +250,79 @@ def bench_hca(args, dev):
     return res
 
 
+def bench_prefill(args, dev, kind):
+    """One chunk of T = 256 prefill targets per sequence at the end of a long prompt, through the
+    quantised reader (modeling.py:293-337 HCA, :496-550 CSA): CSA over cfg3's cache (B=8, 65536-token
+    prompt -> 16384 8-bit blocks, top-256), HCA over cfg4's (262144-token prompt -> 2048 4-bit
+    blocks, B=8).  Window W=128: the buffer holds the W-1 entries before the chunk and its T."""
+    from aetherkv import PolarQuant
+    from aetherkv.decode import indexer_workspace
+    from aetherkv.prefill import (csa_prefill_indexer_topk_quant, prefill_sources, prefill_workspace,
+                                  quant_prefill_attention)
+    from aetherkv.synthetic import normal
+
+    B, T, H, D, W, IH, IC = 8, 256, 12, 128, 128, 4, 64
+    M, bits, seed = (4, 8, 2) if kind == "csa" else (128, 4, 3)
+    S = 16384 if kind == "csa" else 2048
+    start = S * M - T  # the prompt's last chunk
+    Wt = W - 1 + T
+    log(f"prefill {kind}: B={B} T={T} targets at positions {start}..{start + T - 1}, {S} {bits}-bit blocks")
+    pq = PolarQuant(bits)
+    codes, scale = pq.encode(normal((B, S, D), seed, device=dev))
+    q = normal((B, T, H, D), seed + 1, device=dev)
+    win = normal((B, Wt, D), seed + 4, device=dev)
+    sink = normal((H,), seed + 5, dtype=torch.float32, device=dev)
+    vis, ws, wl = prefill_sources(T, start, S, compression=M, sliding_window=W, window_base=start - (W - 1),
+                                  window_len=Wt)
+    vis, ws, wl = (x.to(dev).expand(B, T).contiguous() for x in (vis, ws, wl))
+    out = torch.empty((B, T, H, D), dtype=torch.bfloat16, device=dev)
+    res = {"B": B, "T": T, "positions": [start, start + T - 1], "blocks": S, "bits": bits, "window": W}
+    if kind == "csa":
+        k = 256
+        ix_codes, ix_scale = pq.encode(normal((B, S, IC), seed + 1000, device=dev))
+        index_q = normal((B, T, IH, IC), seed + 2, dtype=torch.float32, device=dev)
+        index_w = normal((B, T, IH), seed + 3, dtype=torch.float32, device=dev)
+        idx = torch.empty((B, T, k), dtype=torch.int64, device=dev)
+        ws_i = indexer_workspace(B * T, S, k, dev)
+        n_sel = torch.clamp(vis, max=k)
+        ws_a = prefill_workspace(B, T, H, k, Wt, dev)
+
+        def index_only():
+            csa_prefill_indexer_topk_quant(index_q, index_w, ix_codes, ix_scale, k, quant=pq, valid=vis,
+                                           workspace=ws_i, out=idx)
+
+        def attn_only():
+            quant_prefill_attention(q, codes, scale, idx, win, sink, D ** -0.5, quant=pq, visible=n_sel,
+                                    win_start=ws, win_len=wl, workspace=ws_a, out=out)
+
+        def step():
+            index_only()
+            attn_only()
+
+        res["indexer_ms"] = round(timed(index_only, args.steps, args.warmup), 5)
+        res["attention_ms"] = round(timed(attn_only, args.steps, args.warmup), 5)
+        n_src = k + W
+    else:
+        ws_a = prefill_workspace(B, T, H, S, Wt, dev)
+
+        def step():
+            quant_prefill_attention(q, codes, scale, None, win, sink, D ** -0.5, quant=pq, visible=vis,
+                                    win_start=ws, win_len=wl, workspace=ws_a, out=out)
+
+        n_src = S + W
+    ms = timed(step, args.steps, args.warmup)
+    flops = 2 * 2 * B * T * H * n_src * D  # QK^T and PV over every target's sources
+    res.update({"ms_per_chunk": round(ms, 5), "targets_per_s": round(B * T / ms * 1e3, 1),
+                "attention_tflops": round(flops / (res.get("attention_ms", ms)) / 1e9, 3)})
+    res["mfma_frac"] = round(res["attention_tflops"] / MFMA_BF16_PEAK_TFLOPS, 5)
+    log(f"prefill {kind}: {ms * 1e3:.1f} us/chunk -> {res['targets_per_s']:.0f} targets/s "
+        + (f"({res['indexer_ms'] * 1e3:.1f} indexer + {res['attention_ms'] * 1e3:.1f} attention) " if kind == "csa"
+           else "") + f"attention {res['attention_tflops']:.1f} TFLOP/s")
+    del codes, scale, q, win, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_sparse_report_shape(args, dev):
     from aetherkv import sparse_sink_attention
 
@@ -266,7 +341,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "encode", "csa", "hca", "sparse"], default="all")
+    ap.add_argument("--only", choices=["all", "encode", "csa", "hca", "prefill", "sparse"], default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -296,6 +371,9 @@ def main():
         secondary["csa_decode_cfg3"] = bench_csa(args, dev, 8, 16384, 8, 2, False, "cfg3")
     if args.only in ("all", "hca"):
         secondary["hca_decode_cfg4"] = bench_hca(args, dev)
+    if args.only in ("all", "prefill"):
+        secondary["csa_prefill_chunk"] = bench_prefill(args, dev, "csa")
+        secondary["hca_prefill_chunk"] = bench_prefill(args, dev, "hca")
     if args.only in ("all", "sparse"):
         secondary["sparse_sink_attention_report_shape"] = bench_sparse_report_shape(args, dev)
 
