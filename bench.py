@@ -323,6 +323,56 @@ def bench_prefill(args, dev, kind):
     return res
 
 
+def bench_paging(args, dev):
+    """Code pages vs the reference's bf16 pages for one CSA layer (KV D=128 + index IC=64, 32 blocks per
+    128-token page) and one HCA layer (1 block per page), 4-bit: bytes per page, the per-page flush
+    (pack codes + scales; the bf16 format needs a decode of the page's blocks), and materialising a
+    65536-token prefix (512 pages) back into rings."""
+    from aetherkv import PolarQuant
+    from aetherkv.cache import CodeRing, compressed_to_bf16_for_paging
+    from aetherkv.storage import code_page_shape, materialize_pages, pack_rows
+    from aetherkv.synthetic import normal
+
+    pq = PolarQuant(4)
+    n_pages, per_page = 512, 32
+    shape = {"layer0.hca": (1, 128), "layer1.csa": (per_page, 128), "layer1.csa_index": (per_page, 64)}
+    bf16_bytes = sum(b * d * 2 for b, d in shape.values())
+    code_bytes = sum(b * w for b, w in code_page_shape(shape, 4).values())
+    kv_c, kv_s = pq.encode(normal((1, n_pages * per_page, 128), 11, device=dev))
+    ix_c, ix_s = pq.encode(normal((1, n_pages * per_page, 64), 12, device=dev))
+    hc_c, hc_s = pq.encode(normal((1, n_pages, 128), 13, device=dev))
+
+    def flush_codes():
+        return {"layer0.hca": pack_rows(hc_c[0, :1], hc_s[0, :1]),
+                "layer1.csa": pack_rows(kv_c[0, :per_page], kv_s[0, :per_page]),
+                "layer1.csa_index": pack_rows(ix_c[0, :per_page], ix_s[0, :per_page])}
+
+    def flush_bf16():
+        return {"layer0.hca": compressed_to_bf16_for_paging(pq, hc_c, hc_s, 0, 1, torch.bfloat16)[0],
+                "layer1.csa": compressed_to_bf16_for_paging(pq, kv_c, kv_s, 0, per_page, torch.bfloat16)[0],
+                "layer1.csa_index": compressed_to_bf16_for_paging(pq, ix_c, ix_s, 0, per_page, torch.bfloat16)[0]}
+
+    pages = [{"layer1.csa": pack_rows(kv_c[0, i * per_page:(i + 1) * per_page], kv_s[0, i * per_page:(i + 1) * per_page]),
+              "layer1.csa_index": pack_rows(ix_c[0, i * per_page:(i + 1) * per_page],
+                                            ix_s[0, i * per_page:(i + 1) * per_page])} for i in range(n_pages)]
+
+    def materialize():
+        materialize_pages(pages, "layer1.csa", pq, 128, device=dev)
+        materialize_pages(pages, "layer1.csa_index", pq, 64, device=dev)
+
+    ms_fc = timed(flush_codes, args.steps, args.warmup)
+    ms_fb = timed(flush_bf16, args.steps, args.warmup)
+    ms_mat = timed(materialize, max(3, args.steps // 4), 1)
+    res = {"page_bytes_codes": code_bytes, "page_bytes_bf16": bf16_bytes,
+           "flush_ms_codes": round(ms_fc, 5), "flush_ms_bf16_decode": round(ms_fb, 5),
+           "materialize_512_pages_ms": round(ms_mat, 4),
+           "materialize_GB/s": round(n_pages * per_page * (68 + 36) / ms_mat / 1e6, 2),
+           "layout": "uint8 rows [codes | fp32 scale] per block; 1 HCA + 32 CSA (+32 index) blocks per 128-token page"}
+    log(f"paging: {code_bytes} B per code page vs {bf16_bytes} B bf16; flush {ms_fc * 1e3:.1f} us (codes) vs "
+        f"{ms_fb * 1e3:.1f} us (decode to bf16); materialise 512 pages {ms_mat * 1e3:.0f} us")
+    return res
+
+
 def bench_sparse_report_shape(args, dev):
     from aetherkv import sparse_sink_attention
 
@@ -341,7 +391,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "encode", "csa", "hca", "prefill", "sparse"], default="all")
+    ap.add_argument("--only", choices=["all", "encode", "csa", "hca", "prefill", "paging", "sparse"], default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -374,6 +424,8 @@ def main():
     if args.only in ("all", "prefill"):
         secondary["csa_prefill_chunk"] = bench_prefill(args, dev, "csa")
         secondary["hca_prefill_chunk"] = bench_prefill(args, dev, "hca")
+    if args.only in ("all", "paging"):
+        secondary["code_pages"] = bench_paging(args, dev)
     if args.only in ("all", "sparse"):
         secondary["sparse_sink_attention_report_shape"] = bench_sparse_report_shape(args, dev)
 

@@ -305,6 +305,40 @@ class CodeRing:
         self.n += m
         self._visible = None
 
+    def append_codes(self, codes: torch.Tensor, scale: torch.Tensor) -> None:
+        """Store already-encoded blocks (codes [B, m, ·], scales [B, m(, 1)]) after the valid ones,
+        e.g. blocks paged back in; nothing is re-encoded."""
+        if codes.dim() != 3 or codes.size(0) != self.batch or codes.size(2) != self.row_bytes:
+            raise RuntimeError(f"CodeRing.append_codes expects codes [{self.batch}, m, {self.row_bytes}], "
+                               f"got {tuple(codes.shape)}")
+        m = codes.size(1)
+        if scale.numel() != self.batch * m:
+            raise RuntimeError(f"CodeRing.append_codes: {scale.numel()} scales for {self.batch} x {m} blocks")
+        if m == 0:
+            return
+        self.reserve(self.n + m)
+        self._codes[:, self.n:self.n + m].copy_(codes.view(self.code_dtype))
+        self._scale[:, self.n:self.n + m].copy_(scale.reshape(self.batch, m, 1))
+        self.n += m
+        self._visible = None
+
+    def drop_front(self, m: int) -> None:
+        """Remove the first m valid blocks (flushed to pages), keeping the rest in order from slot 0;
+        the freed slots are zeroed."""
+        m = int(m)
+        if m < 0 or m > self.n:
+            raise ValueError(f"CodeRing.drop_front({m}) with {self.n} valid blocks")
+        if m == 0:
+            return
+        rest = self.n - m
+        if rest:
+            self._codes[:, :rest].copy_(self._codes[:, m:self.n].clone())
+            self._scale[:, :rest].copy_(self._scale[:, m:self.n].clone())
+        self._codes[:, rest:self.n].zero_()
+        self._scale[:, rest:self.n].zero_()
+        self.n = rest
+        self._visible = None
+
     def append_emitted(self, c: torch.Tensor, z: torch.Tensor, **emit_kwargs) -> None:
         """Pool, RoPE, normalise and encode one block per row (emit_block) straight into slot n."""
         if c.dim() != 3 or c.size(0) != self.batch or c.size(2) != self.dim:

@@ -102,3 +102,25 @@ def test_hca_decode_over_ring_matches_compact_tensors(dev):
     out_r = hca_decode_ring(q, ring, win, sink, D ** -0.5)
     out_c = hca_decode(q, ring.data.contiguous(), ring.scale.contiguous(), win, sink, D ** -0.5, kv_quant=pq)
     assert torch.equal(out_r, out_c)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_paged_code_pages_round_trip_through_decode(dev, bits):
+    # flush the leading blocks of single-sequence rings to code pages, materialise them back in front
+    # of the resident blocks, and decode: identical to decoding the rings before paging
+    from aetherkv.storage import flush_page, materialize_pages
+
+    n, per_page = 700, 32
+    pq, kv, ix, q, iq, iw, win, sink = _csa_inputs(dev, 1, n, bits, 31 + bits)
+    out0, idx0 = csa_decode_ring(q, iq, iw, ix, kv, win, sink, 128 ** -0.5, top_k=256)
+    pages = []
+    while kv.n >= per_page:
+        pages.append(flush_page({"layer1.csa": kv, "layer1.csa_index": ix},
+                                {"layer1.csa": per_page, "layer1.csa_index": per_page}))
+    assert len(pages) == n // per_page and kv.n == n % per_page
+    kv2 = materialize_pages(pages, "layer1.csa", pq, 128, resident=kv)
+    ix2 = materialize_pages(pages, "layer1.csa_index", pq, 64, resident=ix)
+    assert kv2.n == n and ix2.n == n
+    out1, idx1 = csa_decode_ring(q, iq, iw, ix2, kv2, win, sink, 128 ** -0.5, top_k=256)
+    assert torch.equal(idx0, idx1)
+    assert torch.equal(out0, out1)
