@@ -373,6 +373,53 @@ def bench_paging(args, dev):
     return res
 
 
+def bench_attention_io(args, dev):
+    """Query prep (q_norm(rope(q))), window entry (kv_norm(rope(kv))) and the output's inverse RoPE for a
+    cfg5 decode step (B=64, H=12, D=128, rope_dim 64): one aekv_rope_rmsnorm launch each vs the
+    reference's bf16 torch op sequence (apply_rope + F.rms_norm) on the same GPU, both replayed from
+    HIP graphs."""
+    import torch.nn.functional as F
+
+    from aetherkv.attention_io import rope_rmsnorm
+    from aetherkv.cache import rope_inv_freq
+    from aetherkv.synthetic import normal
+
+    B, H, D, rope = 64, 12, 128, 64
+    q = normal((B, H, D), 21, device=dev)
+    kv = normal((B, 1, D), 22, device=dev)
+    o = normal((B, H, D), 23, device=dev)
+    w = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    inv = rope_inv_freq(rope, 10000.0).to(dev)
+    pos = torch.full((B,), 65535, dtype=torch.int64, device=dev)
+    outs = [torch.empty_like(q), torch.empty_like(kv), torch.empty_like(o)]
+
+    def fused():
+        rope_rmsnorm(q, pos, rope_dim=rope, inv_freq=inv, norm_weight=w, out=outs[0])
+        rope_rmsnorm(kv, pos, rope_dim=rope, inv_freq=inv, norm_weight=w, out=outs[1])
+        rope_rmsnorm(o, pos, rope_dim=rope, inv_freq=inv, inverse=True, out=outs[2])
+
+    pf = pos.float()
+
+    def torch_rope(x, sign):
+        pp, rp = x[..., :-rope], x[..., -rope:]
+        ang = (sign * pf).unsqueeze(-1) * inv
+        cos = torch.repeat_interleave(ang.cos(), 2, dim=-1).to(x.dtype).view(B, 1, rope)
+        sin = torch.repeat_interleave(ang.sin(), 2, dim=-1).to(x.dtype).view(B, 1, rope)
+        x1, x2 = rp[..., ::2], rp[..., 1::2]
+        return torch.cat([pp, rp * cos + torch.stack((-x2, x1), dim=-1).flatten(-2) * sin], dim=-1)
+
+    def reference_ops():
+        outs[0].copy_(F.rms_norm(torch_rope(q, 1), (D,), w, 1e-6))
+        outs[1].copy_(F.rms_norm(torch_rope(kv, 1), (D,), w, 1e-6))
+        outs[2].copy_(torch_rope(o, -1))
+
+    ms_f = timed_graph(fused, args.steps, args.warmup)
+    ms_r = timed_graph(reference_ops, args.steps, args.warmup)
+    log(f"attention io (cfg5 step): fused {ms_f * 1e3:.1f} us vs torch op sequence {ms_r * 1e3:.1f} us")
+    return {"shape": "B=64 H=12 D=128 rope_dim=64: query prep + window entry + inverse rope",
+            "fused_ms": round(ms_f, 5), "torch_ops_ms": round(ms_r, 5), "timing": "HIP graph replay"}
+
+
 def bench_sparse_report_shape(args, dev):
     from aetherkv import sparse_sink_attention
 
@@ -391,7 +438,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "encode", "csa", "hca", "prefill", "paging", "sparse"], default="all")
+    ap.add_argument("--only", choices=["all", "encode", "csa", "hca", "prefill", "paging", "io", "sparse"],
+                    default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -424,6 +472,8 @@ def main():
     if args.only in ("all", "prefill"):
         secondary["csa_prefill_chunk"] = bench_prefill(args, dev, "csa")
         secondary["hca_prefill_chunk"] = bench_prefill(args, dev, "hca")
+    if args.only in ("all", "io"):
+        secondary["attention_io"] = bench_attention_io(args, dev)
     if args.only in ("all", "paging"):
         secondary["code_pages"] = bench_paging(args, dev)
     if args.only in ("all", "sparse"):

@@ -11,6 +11,8 @@ New fused decode path over quantised KV:
                              preallocated code storage appended in place and read by csa_decode_ring /
                              hca_decode_ring
   aetherkv.storage           paged-allocator pages and prefix-cache files holding codes + scales
+  aetherkv.attention_io      query prep, window entry and the output's inverse RoPE (one launch each)
+                             and the grouped output projection
   aetherkv.prefill           chunked prefill through the quantised reader: every target of a chunk
                              scored and attended in one launch each (csa_prefill, hca_prefill)
 All compute runs in libaetherkv.so (hand-written HIP for gfx950, C ABI in include/aetherkv.h).

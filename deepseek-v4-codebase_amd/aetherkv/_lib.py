@@ -33,7 +33,7 @@ SYMBOLS = (
     "aekv_csa_indexer_topk_quant", "aekv_sparse_sink_attention", "aekv_quant_attention_workspace_size",
     "aekv_quant_sink_attention", "aekv_hca_compress", "aekv_tiled_prefill_attention", "aekv_set_generic_kernels",
     "aekv_emit_block", "aekv_csa_prefill_indexer_topk_quant", "aekv_quant_prefill_workspace_size",
-    "aekv_quant_prefill_attention",
+    "aekv_quant_prefill_attention", "aekv_rope_rmsnorm",
 )
 
 _lib: Optional[ctypes.CDLL] = None
@@ -81,6 +81,7 @@ def lib() -> ctypes.CDLL:
         "aekv_csa_prefill_indexer_topk_quant": (
             [P, P, P, P, P, P, I64_, I64_, I64_, I32_, I32_, I32_, I32_, I32_, P, SZ, P, P, P], ctypes.c_int),
         "aekv_quant_prefill_workspace_size": ([I64_, I64_, I64_, I64_, I64_], SZ),
+        "aekv_rope_rmsnorm": ([P, I64_, I32_, I32_, P, I32_, P, I32_, P, F, P, P], ctypes.c_int),
         "aekv_quant_prefill_attention": (
             [P, P, P, P, P, P, P, P, P, P, I64_, I64_, I64_, I64_, I64_, I64_, I64_, I32_, F, P, SZ, P, P], ctypes.c_int),
         "aekv_tiled_prefill_attention": ([P, P, P, I64_, I32_, I64_, I64_, I64_, I64_, I64_, F, I32_, P, P],

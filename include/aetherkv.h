@@ -208,6 +208,18 @@ int aekv_emit_block(const void* c, const void* z, const void* z_bias, int64_t B,
                     const void* norm_weight, float eps, int32_t bits, const float* diag, void* out_codes,
                     float* out_scale, int64_t out_row_stride, void* out_vec, void* stream);
 
+/* RoPE then RMSNorm of head vectors (the attention step's query and window-entry preparation,
+ * aether_2b/serving.py:437-442 _query, :444-448 _window_entry; with pos_sign = -1 and no norm the
+ * inverse RoPE of _post_attention, :469-472; apply_rope modeling.py:122-155, RMSNorm :32-41):
+ * x [rows, heads, d] bf16; vector (n, h) is rotated on its last rope_dim dims at fp32 position
+ * pos_sign * positions[n] with frequencies inv_freq[rope_dim/2] (rope_dim 0: none), then
+ * normalised with norm_weight[d] bf16 and eps (NULL: none); out [rows, heads, d] bf16 (may alias
+ * x).  Rounding points as the reference's bf16 torch ops (bf16 cos/sin and RoPE terms, fp32
+ * RMSNorm).  d = 128 or 256. */
+int aekv_rope_rmsnorm(const void* x, int64_t rows, int32_t heads, int32_t d, const int64_t* positions,
+                      int32_t pos_sign, const float* inv_freq, int32_t rope_dim, const void* norm_weight,
+                      float eps, void* out, void* stream);
+
 /* tiled_prefill_attention drop-in: sink attention of every target over all S sources,
  * oracle aether_2b/modeling.py:158-178 (sink counted once in the normaliser). */
 int aekv_tiled_prefill_attention(const void* q, const void* kv, const void* sink, int64_t sink_numel,

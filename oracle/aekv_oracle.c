@@ -501,6 +501,48 @@ int aekvo_hca_compress(const float* c, const float* z, int64_t B, int64_t M, int
 /* ------------------------------------------------------------------------------------------ */
 static inline float bf(float v) { return aekvo_bf16_to_f32(aekvo_f32_to_bf16(v)); }
 
+/* apply_rope (modeling.py:122-155) at fp32 position p on the last rope_dim dims, then RMSNorm
+ * (modeling.py:32-41) when norm_w is given, in place on a bf16-valued vector x[D]. */
+static void rope_rmsnorm_vec(float* x, int64_t D, int rope_dim, float p, const float* inv_freq,
+                             const uint16_t* norm_w, float eps) {
+  if (rope_dim > 0) {
+    const int64_t r0 = D - rope_dim;
+    for (int i = 0; i < rope_dim / 2; ++i) {
+      const float ang = p * inv_freq[i];
+      const float cs = bf(cosf(ang)), sn = bf(sinf(ang));
+      const float a = x[r0 + 2 * i], bb = x[r0 + 2 * i + 1];
+      x[r0 + 2 * i] = bf(bf(a * cs) + bf(-bb * sn));
+      x[r0 + 2 * i + 1] = bf(bf(bb * cs) + bf(a * sn));
+    }
+  }
+  if (norm_w) {
+    float ss = 0.0f;
+    for (int64_t d = 0; d < D; ++d) ss += x[d] * x[d];
+    const float r = 1.0f / sqrtf(ss / (float)D + eps);
+    for (int64_t d = 0; d < D; ++d) x[d] = bf((x[d] * r) * aekvo_bf16_to_f32(norm_w[d]));
+  }
+}
+
+/* Query / window-entry preparation and inverse RoPE of the attention output (aether_2b/serving.py:
+ * 437-448, 469-472): x [rows * heads, D] bf16, vector (row n, head h) at fp32 position
+ * sign * pos[n]; rope then (optional) RMSNorm as rope_rmsnorm_vec. */
+int aekvo_rope_rmsnorm(const uint16_t* x, int64_t rows, int64_t heads, int64_t D, const int64_t* pos, int sign,
+                       const float* inv_freq, int rope_dim, const uint16_t* norm_w, float eps, uint16_t* out) {
+  if (rows < 0 || heads < 1 || D < 2 || rope_dim < 0 || rope_dim > D || (rope_dim & 1)) return 1;
+  if (sign != 1 && sign != -1) return 1;
+  float* v = (float*)malloc(sizeof(float) * (size_t)D);
+  if (!v) return 2;
+  for (int64_t n = 0; n < rows; ++n)
+    for (int64_t h = 0; h < heads; ++h) {
+      const uint16_t* xr = x + (n * heads + h) * D;
+      for (int64_t d = 0; d < D; ++d) v[d] = aekvo_bf16_to_f32(xr[d]);
+      rope_rmsnorm_vec(v, D, rope_dim, rope_dim > 0 ? (float)((int64_t)sign * pos[n]) : 0.0f, inv_freq, norm_w, eps);
+      for (int64_t d = 0; d < D; ++d) out[(n * heads + h) * D + d] = aekvo_f32_to_bf16(v[d]);
+    }
+  free(v);
+  return 0;
+}
+
 int aekvo_emit_block(const uint16_t* c, const uint16_t* z, const uint16_t* bias, int64_t B, int64_t L, int64_t D,
                      int rope_dim, const int64_t* pos, const float* inv_freq, const uint16_t* norm_w, float eps,
                      uint16_t* out) {
@@ -527,23 +569,7 @@ int aekvo_emit_block(const uint16_t* c, const uint16_t* z, const uint16_t* bias,
       }
       x[d] = bf(acc);
     }
-    if (rope_dim > 0) {
-      const int64_t r0 = D - rope_dim;
-      const float p = (float)pos[b];
-      for (int i = 0; i < rope_dim / 2; ++i) {
-        const float ang = p * inv_freq[i];
-        const float cs = bf(cosf(ang)), sn = bf(sinf(ang));
-        const float a = x[r0 + 2 * i], bb = x[r0 + 2 * i + 1];
-        x[r0 + 2 * i] = bf(bf(a * cs) + bf(-bb * sn));
-        x[r0 + 2 * i + 1] = bf(bf(bb * cs) + bf(a * sn));
-      }
-    }
-    if (norm_w) {
-      float ss = 0.0f;
-      for (int64_t d = 0; d < D; ++d) ss += x[d] * x[d];
-      const float r = 1.0f / sqrtf(ss / (float)D + eps);
-      for (int64_t d = 0; d < D; ++d) x[d] = bf((x[d] * r) * aekvo_bf16_to_f32(norm_w[d]));
-    }
+    rope_rmsnorm_vec(x, D, rope_dim, rope_dim > 0 ? (float)pos[b] : 0.0f, inv_freq, norm_w, eps);
     for (int64_t d = 0; d < D; ++d) out[b * D + d] = aekvo_f32_to_bf16(x[d]);
   }
   free(x);

@@ -52,6 +52,7 @@ def lib():
                                             F64, P, I32]
         L.aekvo_hca_compress.argtypes = [P, P, I64, I64, I64, P]
         L.aekvo_emit_block.argtypes = [P, P, P, I64, I64, I64, I32, P, P, P, ctypes.c_float, P]
+        L.aekvo_rope_rmsnorm.argtypes = [P, I64, I64, I64, P, I32, P, I32, P, ctypes.c_float, P]
         L.aekvo_wht_scale.argtypes = [I32]
         L.aekvo_wht_scale.restype = ctypes.c_float
         L.aekvo_softplus.argtypes = [F64]
@@ -221,6 +222,24 @@ def emit_block(c: np.ndarray, z: np.ndarray, bias: Optional[np.ndarray] = None, 
                                 ctypes.c_float(eps), _p(out))
     if rc != 0:
         raise ValueError(f"aekvo_emit_block failed ({rc})")
+    return out
+
+
+def rope_rmsnorm(x: np.ndarray, pos: np.ndarray, inv_freq: Optional[np.ndarray], rope_dim: int,
+                 norm_w: Optional[np.ndarray] = None, eps: float = 1e-6, sign: int = 1) -> np.ndarray:
+    """serving.py:437-448 / 469-472 — RoPE at sign * pos[row] then optional RMSNorm (bf16 points).
+
+    x [rows, heads, D] uint16 (bf16 bits), pos [rows] int64 -> uint16 [rows, heads, D]."""
+    x = _c(x, np.uint16)
+    rows, heads, D = x.shape
+    out = np.empty_like(x)
+    p = _c(np.asarray(pos, dtype=np.int64).reshape(rows), np.int64)
+    f = None if inv_freq is None else _c(inv_freq, np.float32)
+    w = None if norm_w is None else _c(norm_w, np.uint16)
+    rc = lib().aekvo_rope_rmsnorm(_p(x), rows, heads, D, _p(p), int(sign), _p(f), int(rope_dim), _p(w),
+                                  ctypes.c_float(eps), _p(out))
+    if rc != 0:
+        raise ValueError("bad rope_rmsnorm arguments")
     return out
 
 
