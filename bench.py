@@ -18,7 +18,9 @@ attention) are captured 8 at a time in a HIP graph and replayed, as a serving lo
 the eager (per-call Python) step time is reported beside it.
 
 cpu_baseline: the CPU oracle (oracle/liboracle.so, a C restatement of turbo_quant.py's encode)
-timed on this host's cores over the cfg2 layer (median of 3 passes).
+timed on this host's cores over the cfg2 layer (median of 3 passes).  The CSA lines carry their own
+cpu_baseline: the oracle's decode step (dequantise every step or memoised, scores, exact top-256,
+attention) on the first 8 rows of the config.
 """
 from __future__ import annotations
 
@@ -156,6 +158,53 @@ def bench_cpu_encode(out):
                       "(oracle/aekv_oracle.c, OpenMP over vectors)"}
 
 
+def bench_cpu_csa(inp, rows, name, bits):
+    """The CPU oracle's restatement of the reference decode step (aether_2b/serving.py:597-625) on the
+    first `rows` rows of a CSA config, timed on this host: dequantise the index and KV caches (every
+    step, as _read_compressed does, or memoised as its cache does), score all blocks (softplus
+    rule), exact top-256, gather + window + sink attention.  Median of 3 after one warm-up."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    cores = cpu_cores()
+    h = {k: v[:rows].cpu() for k, v in inp.items() if isinstance(v, torch.Tensor) and k != "sink"}
+    sink = inp["sink"].cpu().numpy()
+    f32 = lambda t: t.float().numpy()
+    ixc, ixs = h["ix_codes"].numpy(), h["ix_scale"].numpy()
+    kvc, kvs = h["kv_codes"].numpy(), h["kv_scale"].numpy()
+    q, iq, iw, win = f32(h["q"])[:, 0], f32(h["index_q"]), f32(h["index_w"]), f32(h["win"])
+    d64, d128 = O.diag(42, 64), O.diag(42, 128)
+
+    def step(dequant: bool):
+        if dequant:
+            O.decode(ixc.reshape(-1, ixc.shape[-1]), ixs.reshape(-1), bits, d64, "f32", threads=cores)
+            O.decode(kvc.reshape(-1, kvc.shape[-1]), kvs.reshape(-1), bits, d128, "bf16", threads=cores)
+        keys = keys_memo
+        sc = O.index_scores(iq, iw, keys, threads=cores)
+        idx, _ = O.topk(sc, 256)
+        O.quant_attention(q, kvc, kvs, idx, win, sink, d128, bits, 128 ** -0.5, threads=cores)
+
+    keys_memo = O.decode(ixc.reshape(-1, ixc.shape[-1]), ixs.reshape(-1), bits, d64, "f32",
+                         threads=cores).reshape(rows, ixc.shape[1], 64)
+    res = {"rows": rows, "cores": cores, "kind": "port"}
+    for label, dq in (("dequant_every_step", True), ("memoised_dequant", False)):
+        step(dq)
+        times = []
+        for _ in range(3):
+            t = time.perf_counter()
+            step(dq)
+            times.append(time.perf_counter() - t)
+        med = sorted(times)[1]
+        res[label] = {"s_per_step": round(med, 5), "tokens_per_s": round(rows / med, 2)}
+    log(f"cpu oracle {name} ({rows} rows, {cores} threads): {res['dequant_every_step']['tokens_per_s']:.1f} tok/s "
+        f"dequantising every step, {res['memoised_dequant']['tokens_per_s']:.1f} tok/s memoised")
+    res["sample"] = (f"first {rows} rows of {name}: dequant (index f32 + KV bf16), scores, exact top-256, gather + "
+                     f"window + sink attention, C oracle with OpenMP; median of 3")
+    return res
+
+
 def make_csa_inputs(dev, B, S, bits, seed, outliers):
     from aetherkv import PolarQuant
     from aetherkv.synthetic import normal, normal_with_outliers
@@ -177,7 +226,7 @@ def make_csa_inputs(dev, B, S, bits, seed, outliers):
     )
 
 
-def bench_csa(args, dev, B, S, bits, seed, outliers, name):
+def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
     from aetherkv.decode import attention_workspace, csa_indexer_topk_quant, indexer_workspace, quant_sink_attention
 
     log(f"{name}: CSA decode B={B} S={S} {bits}-bit")
@@ -215,6 +264,8 @@ def bench_csa(args, dev, B, S, bits, seed, outliers, name):
            "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
     log(f"{name}: {ms * 1e3:.1f} us/step ({ms_i * 1e3:.1f} indexer + {ms_a * 1e3:.1f} attention; graph replay; "
         f"eager {ms_eager * 1e3:.1f}) -> {res['tokens_per_s']:.0f} tok/s, {res['hbm_frac'] * 100:.1f}% of HBM peak")
+    if cpu_rows:
+        res["cpu_baseline"] = bench_cpu_csa(inp, cpu_rows, name, bits)
     del inp
     torch.cuda.empty_cache()
     return res
@@ -465,8 +516,9 @@ def main():
             cpu = bench_cpu_encode(res)
         torch.cuda.empty_cache()
     if args.only in ("all", "csa"):
-        secondary["csa_decode_cfg5"] = bench_csa(args, dev, 64, 65536, 4, 4, True, "cfg5")
-        secondary["csa_decode_cfg3"] = bench_csa(args, dev, 8, 16384, 8, 2, False, "cfg3")
+        cpu_rows = (0, 0) if args.no_cpu_baseline else (8, 8)
+        secondary["csa_decode_cfg5"] = bench_csa(args, dev, 64, 65536, 4, 4, True, "cfg5", cpu_rows[0])
+        secondary["csa_decode_cfg3"] = bench_csa(args, dev, 8, 16384, 8, 2, False, "cfg3", cpu_rows[1])
     if args.only in ("all", "hca"):
         secondary["hca_decode_cfg4"] = bench_hca(args, dev)
     if args.only in ("all", "prefill"):

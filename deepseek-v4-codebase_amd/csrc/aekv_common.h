@@ -36,6 +36,7 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
 bool use_specialised_codec();
 // Matrix-core decode attention for head_dim 128 (quant_attn_mfma.hip).
 bool quant_attn_mfma_supported(int64_t H, int64_t D);
+bool quant_attn_mfma_fits(int64_t rows, int64_t n_src);  // grid and split-combine limits
 size_t quant_attn_mfma_workspace(int64_t B, int64_t H, int64_t n_src);
 int launch_quant_attn_mfma(const void* q, const void* codes, const float* scale, const int64_t* sel,
                            const void* window, const float* sink, const float* diag, int64_t B, int64_t H, int64_t S,

@@ -33,7 +33,13 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kD = 128;
 constexpr int kGroup = 32;                    // sources per wave step
-constexpr int kSplitSrc = 1024;               // sources per workgroup when a row is split
+constexpr int kSplitSrc = 1024;               // most sources per workgroup (a row is split beyond)
+#ifndef AEKV_ATTN_MIN_SPLIT
+#define AEKV_ATTN_MIN_SPLIT 512
+#endif
+#ifndef AEKV_ATTN_TARGET_WG
+#define AEKV_ATTN_TARGET_WG 512
+#endif
 constexpr float kNegInf = -__builtin_inff();
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
@@ -57,7 +63,7 @@ struct QAttnMfmaArgs {
   const int32_t* wlen;
   int64_t T, Wt;
   int64_t S, K, n_comp, n_src;
-  int H, n_split;
+  int H, n_split, split_src;
   float sm_scale, wscale;
   float* part;            // [B, n_split, H, 2 + 128] (split runs only)
   uint16_t* out;          // [B, H, 128] bf16
@@ -106,8 +112,8 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
   const int64_t w0 = a.wstart ? min<int64_t>(max(a.wstart[b], 0), a.Wt) : 0;
   const int64_t wl = a.wlen ? min<int64_t>(max(a.wlen[b], 0), a.Wt - w0) : a.Wt - w0;
   // this workgroup's sources [src0, src1); the selected block ids go to LDS (-1: skipped)
-  const int64_t src0 = static_cast<int64_t>(split) * kSplitSrc;
-  const int64_t src1 = min<int64_t>(n_comp + wl, src0 + kSplitSrc);
+  const int64_t src0 = static_cast<int64_t>(split) * a.split_src;
+  const int64_t src1 = min<int64_t>(n_comp + wl, src0 + a.split_src);
   if (a.sel) {
     const int64_t nsel = min<int64_t>(src1, n_comp) - src0;
     for (int64_t i = threadIdx.x; i < nsel; i += kThreads) {
@@ -401,36 +407,72 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
 }
 
 // Split combine: M = max(sink, split maxima), L = e^{sink-M} + sum_s e^{m_s-M} l_s,
-// out = sum_s e^{m_s-M} acc_s / L.
+// out = sum_s e^{m_s-M} acc_s / L.  The per-head factors e^{m_s-M} / L go to LDS first (one load
+// round for every split's statistics), then each output sums its splits' partials, all loads of a
+// thread issued together: two dependent memory rounds per row whatever the split count.
+constexpr int kMaxCombineSplits = 256;
 __global__ __launch_bounds__(kThreads) void quant_attn_mfma_combine_kernel(QAttnMfmaArgs a) {
+  __shared__ float st[kMaxCombineSplits * 16 * 2];  // [split][head][m, l]
+  __shared__ float fac[kMaxCombineSplits * 16];     // [split][head] e^{m_s - M} / L
   const int64_t b = blockIdx.x;
   const int H = a.H, ns = a.n_split;
   const float* part = a.part + b * ns * H * (kD + 2);
-  for (int p = threadIdx.x; p < H * kD; p += kThreads) {
-    const int h = p / kD, d = p % kD;
+  for (int i = threadIdx.x; i < ns * H; i += kThreads) {
+    const float* ps = part + static_cast<int64_t>(i) * (kD + 2);
+    st[2 * i] = ps[0];
+    st[2 * i + 1] = ps[1];
+  }
+  __syncthreads();
+  if (threadIdx.x < H) {
+    const int h = threadIdx.x;
     const float sk = a.sink[h];
     float M = sk;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, part[(s * H + h) * (kD + 2)]);
-    float L = __expf(sk - M), acc = 0.0f;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, st[2 * (s * H + h)]);
+    float L = __expf(sk - M);
     for (int s = 0; s < ns; ++s) {
-      const float* ps = part + (s * H + h) * (kD + 2);
-      const float ms = ps[0];
+      const float ms = st[2 * (s * H + h)];
       const float f = ms == kNegInf ? 0.0f : __expf(ms - M);
-      L = fmaf(f, ps[1], L);
-      acc = fmaf(f, ps[2 + d], acc);
+      fac[s * H + h] = f;
+      L = fmaf(f, st[2 * (s * H + h) + 1], L);
     }
-    a.out[(b * H + h) * kD + d] = bf16_bits(acc / L);
+    const float r = 1.0f / L;
+    for (int s = 0; s < ns; ++s) fac[s * H + h] *= r;
+  }
+  __syncthreads();
+  // thread -> (head, 4 consecutive dims); the splits' partials are independent loads
+  for (int p = threadIdx.x; p < H * (kD / 4); p += kThreads) {
+    const int h = p / (kD / 4), d4 = 4 * (p % (kD / 4));
+    f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+    for (int s = 0; s < ns; ++s) {
+      const float* ps = part + static_cast<int64_t>(s * H + h) * (kD + 2) + 2 + d4;
+      const float f = fac[s * H + h];
+      acc = f32x4_t{fmaf(f, ps[0], acc[0]), fmaf(f, ps[1], acc[1]), fmaf(f, ps[2], acc[2]), fmaf(f, ps[3], acc[3])};
+    }
+    const uint2 v = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
+    *reinterpret_cast<uint2*>(a.out + (b * H + h) * kD + d4) = v;
   }
 }
 
 }  // namespace
 
+// Sources per workgroup: kSplitSrc, halved (down to AEKV_ATTN_MIN_SPLIT) while the grid has fewer
+// than AEKV_ATTN_TARGET_WG workgroups, so that few long rows still spread over the chip.  A row
+// with more sources than that takes one workgroup per piece plus the split combine.
+int64_t split_sources(int64_t rows, int64_t n_src) {
+  int64_t s = kSplitSrc;
+  while (s > AEKV_ATTN_MIN_SPLIT && rows * ceil_div(std::max<int64_t>(n_src, 1), s) < AEKV_ATTN_TARGET_WG) s >>= 1;
+  return s;
+}
+
 bool quant_attn_mfma_supported(int64_t H, int64_t D) { return D == kD && H >= 1 && H <= 16; }
 
-// Rows of up to kSplitSrc sources take one workgroup; longer rows one per kSplitSrc sources plus
-// the split combine.
+bool quant_attn_mfma_fits(int64_t rows, int64_t n_src) {
+  return rows <= 65535 && (n_src <= 0 || ceil_div(n_src, split_sources(rows, n_src)) <= kMaxCombineSplits);
+}
+
 size_t quant_attn_mfma_workspace(int64_t B, int64_t H, int64_t n_src) {
-  const int64_t n_split = n_src > 0 ? ceil_div(n_src, kSplitSrc) : 1;
+  const int64_t n_split = n_src > 0 ? ceil_div(n_src, split_sources(B, n_src)) : 1;
   return n_split > 1 ? align_up(static_cast<size_t>(B * n_split * H * (kD + 2)) * 4, 256) : 0;
 }
 
@@ -457,8 +499,9 @@ int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* s
   a.n_comp = all_blocks ? S : K;
   a.n_src = a.n_comp + Wt;  // an upper bound of every row's sources
   a.H = static_cast<int>(H);
-  const int64_t n_split = a.n_src > 0 ? ceil_div(a.n_src, kSplitSrc) : 1;
-  if (n_split > 65535 || rows > 65535)
+  a.split_src = static_cast<int>(split_sources(rows, a.n_src));
+  const int64_t n_split = a.n_src > 0 ? ceil_div(a.n_src, static_cast<int64_t>(a.split_src)) : 1;
+  if (n_split > kMaxCombineSplits || rows > 65535)
     return fail(AEKV_ERR_UNSUPPORTED, "%s: %lld rows x %lld sources exceed the launch grid", who,
                 static_cast<long long>(rows), static_cast<long long>(a.n_src));
   a.n_split = static_cast<int>(n_split);

@@ -445,7 +445,8 @@ extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const
   }
   if (!ws || ws_bytes < l.part_bytes)
     return fail(AEKV_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who, l.part_bytes, ws_bytes);
-  if (quant_attn_mfma_supported(H, D) && use_specialised_codec() && is_aligned(q, 16) && is_aligned(out, 8) &&
+  if (quant_attn_mfma_supported(H, D) && quant_attn_mfma_fits(B, n_comp + W) && use_specialised_codec() &&
+      is_aligned(q, 16) && is_aligned(out, 8) &&
       is_aligned(diag, 16) && (n_comp == 0 || is_aligned(codes, 16)) && (W == 0 || is_aligned(window, 16)))
     return launch_quant_attn_mfma(q, codes, scale, sel, window, sink, diag, B, H, S, K, all_blocks, W, bits,
                                   softmax_scale, ws, out, as_stream(stream), who);
@@ -500,6 +501,9 @@ extern "C" int aekv_quant_prefill_attention(const void* q, const void* codes, co
   if (!quant_attn_mfma_supported(H, D))
     return fail(AEKV_ERR_UNSUPPORTED, "%s: head_dim %lld with %lld heads (128 and at most 16 supported)", who,
                 (long long)D, (long long)H);
+  if (B > 0 && !quant_attn_mfma_fits(B * T, (n_sel < 0 ? S : n_sel) + Wt))
+    return fail(AEKV_ERR_UNSUPPORTED, "%s: %lld targets with %lld sources exceed the launch limits", who,
+                (long long)(B * T), (long long)((n_sel < 0 ? S : n_sel) + Wt));
   if (B < 0 || T < 1 || S < 0 || Wt < 0) return fail(AEKV_ERR_SHAPE, "%s: bad sizes", who);
   if (B > 0 && T > 65535 / B) return fail(AEKV_ERR_UNSUPPORTED, "%s: B*T exceeds 65535", who);
   const bool all_blocks = n_sel < 0;  // HCA: blocks 0 .. visible-1 in order
