@@ -37,6 +37,13 @@ bool use_specialised_codec();
 // Matrix-core decode attention for head_dim 128 (quant_attn_mfma.hip).
 bool quant_attn_mfma_supported(int64_t H, int64_t D);
 bool quant_attn_mfma_fits(int64_t rows, int64_t n_src);  // grid and split-combine limits
+// Chunked-prefill HCA attention over bf16 blocks [B, S, 128] already decoded (prefill_flash.hip).
+bool hca_prefill_flash_supported(int64_t H, int64_t D);
+size_t hca_prefill_flash_workspace(int64_t B, int64_t S);  // the decoded blocks
+int launch_hca_prefill_flash(const void* q, const void* kblk, const void* window, const int32_t* vis,
+                             const int32_t* wstart, const int32_t* wlen, const float* sink, int64_t B, int64_t T,
+                             int64_t H, int64_t S, int64_t Wt, float softmax_scale, void* out, hipStream_t st,
+                             const char* who);
 size_t quant_attn_mfma_workspace(int64_t B, int64_t H, int64_t n_src);
 int launch_quant_attn_mfma(const void* q, const void* codes, const float* scale, const int64_t* sel,
                            const void* window, const float* sink, const float* diag, int64_t B, int64_t H, int64_t S,

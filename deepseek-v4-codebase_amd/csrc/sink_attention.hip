@@ -487,7 +487,11 @@ extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const
 
 extern "C" size_t aekv_quant_prefill_workspace_size(int64_t B, int64_t T, int64_t H, int64_t n_comp, int64_t Wt) {
   if (B <= 0 || T <= 0 || H <= 0) return 256;
-  return std::max<size_t>(256, quant_attn_mfma_workspace(B * T, H, std::max<int64_t>(n_comp, 0) + std::max<int64_t>(Wt, 0)));
+  const int64_t nc = std::max<int64_t>(n_comp, 0);
+  // per-target split partials (CSA) or every block decoded to bf16 (HCA: n_comp = S)
+  const size_t rows = quant_attn_mfma_workspace(B * T, H, nc + std::max<int64_t>(Wt, 0));
+  const size_t blocks = hca_prefill_flash_workspace(B, nc);
+  return std::max<size_t>(256, std::max(rows, blocks));
 }
 
 extern "C" int aekv_quant_prefill_attention(const void* q, const void* codes, const float* scale, const int64_t* sel,
@@ -515,6 +519,19 @@ extern "C" int aekv_quant_prefill_attention(const void* q, const void* codes, co
   if (!is_aligned(q, 16) || !is_aligned(out, 8) || !is_aligned(diag, 16) || (n_comp > 0 && !is_aligned(codes, 16)) ||
       (Wt > 0 && !is_aligned(window, 16)) || !is_aligned(sink, 4) || (scale && !is_aligned(scale, 4)))
     return fail(AEKV_ERR_ALIGN, "%s: misaligned pointer", who);
+  if (all_blocks && hca_prefill_flash_supported(H, D)) {
+    // HCA: decode every block once (exactly PolarQuant.decode's bf16 values) into the workspace,
+    // then the flash kernel over [blocks; window] with per-target masks
+    const size_t need = S > 0 ? hca_prefill_flash_workspace(B, S) : 0;
+    if (need > 0 && (!ws || ws_bytes < need))
+      return fail(AEKV_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who, need, ws_bytes);
+    if (need > 0 && !is_aligned(ws, 256)) return fail(AEKV_ERR_ALIGN, "%s: workspace must be 256-byte aligned", who);
+    if (S > 0) {
+      if (int rc = aekv_tq_decode(codes, scale, B * S, 128, bits, diag, ws, AEKV_BF16, stream)) return rc;
+    }
+    return launch_hca_prefill_flash(q, ws, window, visible, win_start, win_len, sink, B, T, H, S, Wt,
+                                    softmax_scale, out, as_stream(stream), who);
+  }
   const size_t need = quant_attn_mfma_workspace(B * T, H, n_comp + Wt);
   if (need > 0 && (!ws || ws_bytes < need))
     return fail(AEKV_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who, need, ws_bytes);

@@ -1,13 +1,14 @@
 """GPU tests of chunked prefill through the quantised reader (aetherkv.prefill).
 
-Each target of a chunk is checked three ways:
-  * against the oracle's decode-step attention on that target's own sources (its visible blocks or
-    its indexer selection, and its window slice; modeling.py:316-325 / :521-539), within the bf16
-    tolerance of the quantised attention tests;
-  * bit for bit against the decode entry point called once per target on the same sources (the
-    prefill launch must reproduce the per-target launches exactly);
-  * the multi-target indexer bit for bit against the single-target indexer per target, and its
-    selection against the oracle's exact top-k up to fp32 near-ties.
+Each target of a chunk is checked against the oracle's decode-step attention on that target's own
+sources (its visible blocks or its indexer selection, and its window slice; modeling.py:316-325 /
+:521-539), within the bf16 tolerance of the quantised attention tests.  CSA targets are also
+checked bit for bit against the decode entry point called once per target on the same sources
+(the per-target rows reuse the decode kernel), and the multi-target indexer bit for bit against
+the single-target indexer per target and its selection against the oracle's exact top-k up to
+fp32 near-ties.  HCA prefill runs a different kernel (blocks decoded once, then a flash-style
+pass shared by many targets), so its bar is the oracle tolerance and closeness to the decode
+launches within the same tolerance.
 """
 from __future__ import annotations
 
@@ -49,7 +50,9 @@ def _oracle_target(pq, codes, scale, sel_np, q_t, win_t, sink, sm):
 @pytest.mark.parametrize("bits,B,T,H,start,M,W,nb,S", [
     (4, 2, 40, 12, 100, 8, 16, 17, 24),     # capacity past the emitted blocks; targets cross block edges
     (8, 3, 33, 16, 0, 4, 8, 8, 8),          # first chunk: the early targets see no block
-    (4, 2, 6, 12, 9000, 8, 128, 1130, 1200),  # ~1250 sources per target: split rows + combine
+    (4, 2, 6, 12, 9000, 8, 128, 1130, 1200),  # ~1250 sources per target
+    (4, 2, 200, 12, 6300, 128, 128, 60, 64),  # the model's HCA shape: a block edge inside the chunk
+    (8, 1, 70, 5, 37, 4, 20, 30, 40),       # rows per workgroup not a multiple of the head count
 ])
 def test_hca_prefill_matches_oracle_and_decode(dev, bits, B, T, H, start, M, W, nb, S):
     Wt = W - 1 + T
@@ -72,7 +75,8 @@ def test_hca_prefill_matches_oracle_and_decode(dev, bits, B, T, H, start, M, W, 
         # the decode entry point on the same sources (blocks 0..g-1 in order, the same window slice)
         dec = quant_sink_attention(q[:, t], codes[:, :g].contiguous(), scale[:, :g].contiguous(), None, win_t, sink,
                                    sm, quant=pq)
-        assert torch.equal(out[:, t], dec), f"target {t} differs from the decode launch"
+        np.testing.assert_allclose(to_np_f32(out[:, t]), to_np_f32(dec), rtol=QUANT_RTOL, atol=QUANT_ATOL,
+                                   err_msg=f"target {t} vs the decode launch")
 
 
 @pytest.mark.parametrize("bits", [4, 8])
