@@ -9,22 +9,35 @@
 //   row r = t * H + h of sequence b; source j < g_t (block) or window entry e in
 //   [win_start_t, win_start_t + win_len_t).
 //
-// A workgroup (4 waves) owns 64 consecutive rows, each wave 16 (one per lane column c16).  The
-// sources of the workgroup's targets (blocks [0, max g), window [min start, max end)) stream
-// through LDS in tiles of TILE keys, row-major (key, 128 dims), in two alternating buffers: the
-// next tile is loaded into registers while the current one is multiplied, one barrier per tile.
-// The same tile is both operands: S^T = K Q^T reads 16-byte row chunks (v_mfma_f32_16x16x32_bf16,
-// keys x rows), and O^T += V^T P^T reads V^T with the gfx950 transpose load ds_read_b64_tr_b16,
-// which hands lane i of each 16-lane group element j of source lane 4j + i/4's 4 halfwords
-// (element i%4): source lane s of group g points at key 4g + s/4, dims 4(s%4)..+3 of a 16-dim
-// block, so every lane receives 4 keys of one dim.  Row chunks are XOR-swizzled by key
-// (chunk_swizzle) so that both the 16-lane row-chunk reads (16 keys, one chunk) and the transpose
-// reads (8 keys x 32 bytes per 32-lane pass) hit distinct banks, with no padding.
+// Work split.  A workgroup (4 waves) owns 64 consecutive rows.  The sources of its targets
+// (blocks [0, max g), window [min start, max end)) stream through LDS in tiles of TILE keys,
+// row-major (key, 128 dims), in two alternating buffers (one barrier per tile).  Wave w takes row
+// half w % 2 (32 rows, lane l holds row l % 32) and key half w / 2 of every tile, so each wave
+// reads half a tile per step for 32 rows: with v_mfma_f32_32x32x16_bf16 every LDS byte feeds
+// twice the matrix work of a 16-row wave over the whole tile.  The two waves of a row half keep
+// separate online-softmax states, merged once at the end through LDS.
 //
-// Softmax in the exp2 domain with the exact running maximum (so a row's largest weight is exactly
-// 1 in bf16, as in a two-pass softmax); the rescale of O and l is a wave-uniform branch taken only
-// on tiles that raise some row's maximum, which after the first few tiles is rare.  Tiles that
-// every row of the workgroup sees in full skip the masks.
+// Matrix layouts (v_mfma_f32_32x32x16_bf16, measured): A lane l holds A[l%32][8(l/32)+j], B lane l
+// holds B[8(l/32)+j][l%32], D lane l register v holds D[8(v/4) + 4(l/32) + v%4][l%32].
+//   S^T = K Q^T: m = key, n = row, k = dims 16 ks + 8 (l/32) + j.  A = 16-byte row chunks of the
+//     tile, B = the row's query (registers).  Lane l gets the scores of keys
+//     8q + 4(l/32) + r (q, r < 4) of each 32-key block for its row.
+//   O^T += V^T P^T per 16-key chunk c: m = dim, n = row, k = key with lane half h = l/32 holding
+//     keys {16c + 4h + j, 16c + 8 + 4h + j} (j < 4): exactly the lane's own scores, so P^T needs
+//     no data movement.  A = V^T comes from the same row-major tile through the gfx950 transpose
+//     load ds_read_b64_tr_b16 (lane i of a 16-lane group gets element i%4 of source lane
+//     4j + i/4 as element j, measured): source lane s of the group points at key k_(s/4), dims
+//     4(s%4)..+3 of the group's 16 dims, so every lane receives 4 keys of one dim.
+//   Row chunks are stored XOR-swizzled, chunk c of key r at c ^ sigma(r % 16) with
+//   sigma(r) = 4(r%4) + (r/4)%4: the 16 keys of a row-chunk read land on 16 distinct chunks, and
+//   the 4 keys x 4 chunks of a 32-lane transpose pass on 16 distinct chunks (64 banks), no padding.
+//
+// Softmax in the exp2 domain with the exact running maximum, so a row's largest weight is exactly 1
+// in bf16 and every weight ratio carries one bf16 rounding (a maximum raised only past a margin
+// leaves two, which measurably exceeds the attention tolerance).  The rescale of O and l is a
+// wave-uniform branch taken on tiles that raise some row's maximum.  The normaliser is one more
+// product per 16-key chunk with an all-ones A operand: the sum of the very bf16 weights the
+// numerator used.  Tiles that every row of the workgroup sees in full skip the masks.
 #include "tq_device.h"
 
 namespace aekv {
@@ -32,38 +45,33 @@ namespace {
 
 constexpr int kFD = 128;
 constexpr int kFThreads = 256;        // 4 waves
-constexpr int kFRows = 64;            // query rows per workgroup (16 per wave)
+constexpr int kFRows = 64;            // query rows per workgroup (32 per row half)
 constexpr int kRowBytes = kFD * 2;    // one key of the tile in LDS
 #ifndef AEKV_FLASH_TILE
-#define AEKV_FLASH_TILE 64
-#endif
-#ifndef AEKV_FLASH_SWZ
-#define AEKV_FLASH_SWZ 64
+#define AEKV_FLASH_TILE 128
 #endif
 constexpr int kFTile = AEKV_FLASH_TILE;  // sources per tile
-constexpr int kChunks = kFTile / 16;     // 16-byte chunks per thread and tile
+constexpr int kKW = kFTile / 2;          // sources per wave and tile
+constexpr int kKB = kKW / 32;            // 32-key score blocks per wave and tile
+constexpr int kChunks = kFTile / 16;     // 16-byte staging chunks per thread and tile
 constexpr int kTileBytes = kFTile * kRowBytes;
+#ifndef AEKV_FLASH_PF
+#define AEKV_FLASH_PF 1
+#endif
+constexpr int kPrefetch = AEKV_FLASH_PF;  // tiles in flight from memory (2 spills registers at 128-key tiles)
+static_assert(kPrefetch == 1 || kPrefetch == 2, "prefetch distance 1 or 2 (register sets alternate with the buffers)");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kFNegInf = -__builtin_inff();
-static_assert(kFTile % 32 == 0 && kFTile <= 128, "tiles are whole 32-key chunks");
+static_assert(kFTile % 64 == 0 && kFTile <= 128, "tiles are whole 32-key blocks per wave");
 constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: raw 32-bit data, range-checked
 
 typedef __attribute__((ext_vector_type(8))) __bf16 fbf16x8_t;
-typedef __attribute__((ext_vector_type(4))) float ff32x4_t;
+typedef __attribute__((ext_vector_type(16))) float ff32x16_t;
 typedef __attribute__((ext_vector_type(4))) short fi16x4_t;
 typedef __attribute__((address_space(3))) fi16x4_t lds_i16x4_t;
 
-// Position of 16-byte chunk c of key r in its 256-byte LDS row: c ^ chunk_swizzle(r % 16).  A
-// bijection on the 16 keys of a row-chunk read, and for the 8 keys of a transpose-read pass it
-// sends chunk pairs {2n, 2n+1} to 8 distinct pairs (64 banks of 4 bytes).  AEKV_FLASH_SWZ=32
-// selects the layout that is conflict-free for 32 banks instead.
-__device__ __forceinline__ int chunk_swizzle(int r) {
-#if AEKV_FLASH_SWZ == 32
-  return ((r & 3) << 1) | ((r >> 2) & 1) | (r & 8);
-#else
-  return ((r & 7) << 1) | (r >> 3);
-#endif
-}
+// chunk c of key r sits at c ^ chunk_swizzle(r % 16) of its 256-byte LDS row
+__device__ __forceinline__ int chunk_swizzle(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 template <int N>
 struct IntC {
@@ -95,6 +103,10 @@ __device__ __forceinline__ fi16x4_t lds_read_tr16(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
 }
 
+__device__ __forceinline__ ff32x16_t mfma32(fbf16x8_t a, fbf16x8_t b, ff32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
 struct FlashArgs {
   const uint16_t* q;      // [B, T, H, 128] bf16
   const uint16_t* kblk;   // [B, S, 128] bf16 (dequantised blocks)
@@ -111,14 +123,15 @@ struct FlashArgs {
   uint16_t* out;          // [B, T, H, 128] bf16
 };
 
-// Two waves per SIMD (at most 256 registers per lane): the accumulators then stay in VGPRs across
-// the loop (the matrix instructions take VGPR operands) instead of moving to AGPRs and back, and
-// the scheduler may spend registers on reading LDS operands ahead of the products.  A launch has
-// about 1.5 workgroups per CU at the bench shape, so more resident waves would not exist anyway.
+// Two waves per SIMD (at most 256 registers per lane): the accumulators stay in VGPRs across the
+// loop (the matrix instructions take VGPR operands) instead of moving to AGPRs and back, and the
+// scheduler may spend registers on reading LDS operands ahead of the products.  A launch has about
+// 1.5 workgroups per CU at the bench shape, so more resident waves would not exist anyway.
 __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void hca_prefill_flash_kernel(
     FlashArgs a) {
   __shared__ __align__(16) uint8_t Ls[2][kTileBytes];  // [buffer][key][swizzled 16-byte chunks]
-  __shared__ int s_rng[4][4];  // per wave: max blocks, min blocks, window lo, window hi
+  __shared__ int s_rng[4][4];                          // per wave: max blocks, min blocks, window lo, hi
+  __shared__ float s_ml[2][2][64];                     // key half 1's (m, l) per row half and lane
 
   // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2): renumber them so
   // that XCD x runs the consecutive range [x n/8, (x+1) n/8), i.e. whole sequences, whose blocks
@@ -129,10 +142,12 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   if (n_wg % 8 == 0) wgi = (wgi % 8) * (n_wg / 8) + wgi / 8;
   const int b = static_cast<int>(wgi / a.gx);
   const int wrow = static_cast<int>(wgi % a.gx);
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, c16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int rh = wv & 1, kh = wv >> 1;  // row half, key half
+  const int rl = lane & 31, hh = lane >> 5;
   const int H = a.H;
   const int RT = a.T * H;
-  const int r = wrow * kFRows + wv * 16 + c16;  // this lane's row
+  const int r = wrow * kFRows + 32 * rh + rl;  // this lane's row
   const bool rv = r < RT;
   const int t = rv ? static_cast<int>(static_cast<uint32_t>(r) / static_cast<uint32_t>(H)) : 0;
   const int h = rv ? r - t * H : 0;
@@ -175,28 +190,41 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const int n_wt = whi > wlo ? (whi - wlo + kFTile - 1) / kFTile : 0;
   const int n_tiles = n_bt + n_wt;
 
-  // queries as the B operand of S^T = K Q^T: lane (row c16) holds dims 32 ks + 8 g .. + 7
-  fbf16x8_t qb[4];
+  // the row's query as the B operand of S^T = K Q^T: dims 16 ks + 8 hh .. + 7
+  fbf16x8_t qb[8];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
+  for (int ks = 0; ks < 8; ++ks) {
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (rv) v = *reinterpret_cast<const uint4*>(a.q + (static_cast<int64_t>(b) * RT + r) * kFD + 32 * ks + 8 * g);
+    if (rv) v = *reinterpret_cast<const uint4*>(a.q + (static_cast<int64_t>(b) * RT + r) * kFD + 16 * ks + 8 * hh);
     qb[ks] = __builtin_bit_cast(fbf16x8_t, v);
   }
+  // the queries have landed before any tile load is issued: otherwise the wait for them, merged
+  // over the loop's back edge, becomes a wait for every tile load on every iteration
+  __builtin_amdgcn_s_waitcnt(0);
 
-  // LDS byte offsets, fixed per lane.  Staging: thread tid moves chunk tid % 16 of keys
-  // tid / 16 + 16 c.  Row-chunk reads: key 16 kb + c16, logical chunk 4 ks + g.  Transpose reads:
-  // key 32 kc + 4 g + c16 / 4 (+16), dims 16 n8 + 4 (c16 % 4) .. + 3.
+  // LDS byte offsets, fixed per lane (the tile and block offsets are multiples of 16 keys, which
+  // leave the swizzle unchanged, and become immediates).  Staging: thread tid moves chunk tid % 16
+  // of keys tid / 16 + 16 c.  Row-chunk reads: key kKW kh + 32 kb + rl, chunk 2 ks + hh.
+  // Transpose reads (16-lane group G = lane / 16, s = lane % 16): key kKW kh + 16 c + 4 hh + s / 4
+  // (+ 8 e), dims 32 mb + 16 (G % 2) + 4 (s % 4) .. + 3.
   const int st_key = tid >> 4;
   const int st_off = st_key * kRowBytes + (((tid & 15) ^ chunk_swizzle(st_key)) << 4);
-  int soff[4];
+  const int kbase = kKW * kh * kRowBytes;
+  int soff[8];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) soff[ks] = c16 * kRowBytes + (((4 * ks + g) ^ chunk_swizzle(c16)) << 4);
-  const int tr_key = 4 * g + (c16 >> 2);
-  int toff[8];
+  for (int ks = 0; ks < 8; ++ks) soff[ks] = kbase + rl * kRowBytes + (((2 * ks + hh) ^ chunk_swizzle(rl & 15)) << 4);
+  int toff[2][4];
+  {
+    const int s16 = lane & 15, G = lane >> 4;
 #pragma unroll
-  for (int n8 = 0; n8 < 8; ++n8)
-    toff[n8] = tr_key * kRowBytes + (((2 * n8 + ((c16 >> 1) & 1)) ^ chunk_swizzle(tr_key)) << 4) + 8 * (c16 & 1);
+    for (int e = 0; e < 2; ++e) {
+      const int key = 4 * hh + (s16 >> 2) + 8 * e;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        toff[e][mb] = kbase + key * kRowBytes + (((4 * mb + 2 * (G & 1) + ((s16 & 3) >> 1)) ^ chunk_swizzle(key)) << 4) +
+                      8 * (s16 & 1);
+    }
+  }
 
   const uint8_t* kseq = reinterpret_cast<const uint8_t*>(a.kblk + static_cast<int64_t>(b) * a.S * kFD);
   const uint8_t* wseq = reinterpret_cast<const uint8_t*>(a.win + static_cast<int64_t>(b) * a.Wt * kFD);
@@ -205,13 +233,14 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   for (int c = 0; c < kChunks; ++c) voff[c] = 16 * tid + 16 * kRowBytes * c;
   // tile it: keys [base, base + TILE) of the blocks (it < n_bt) or of the window, read through a
   // buffer resource whose range ends at the workgroup's last source, so that the rows past it
-  // read as zero (never attended) without a branch or an access
+  // read as zero (never attended) without a branch or an access.  A tile past the last has an
+  // empty range: its loads are issued (no branch, so the wait counts stay exact) but touch nothing.
   auto load_tile = [&](int it, uint4 (&v)[kChunks]) {
     const bool blk = it < n_bt;
     const int base = blk ? it * kFTile : wlo + (it - n_bt) * kFTile;
     const int lim = blk ? gmax : whi;
-    const uint8_t* src = (blk ? kseq : wseq) + static_cast<int64_t>(base) * kRowBytes;
-    const int n_bytes = min(lim - base, kFTile) * kRowBytes;
+    const uint8_t* src = (blk ? kseq : wseq) + static_cast<int64_t>(it < n_tiles ? base : 0) * kRowBytes;
+    const int n_bytes = it < n_tiles ? min(lim - base, kFTile) * kRowBytes : 0;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), 0, n_bytes, kBufWord3);
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[c], 0, 0));
@@ -221,42 +250,43 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     for (int c = 0; c < kChunks; ++c) *reinterpret_cast<uint4*>(Ls[buf] + st_off + 16 * kRowBytes * c) = v[c];
   };
 
-  // m_run: the row's running maximum in scaled log2 units.  lsum: the row's sum of the bf16 weights
-  // fed to the products, as a product with an all-ones operand (every element holds the sum), so
-  // the normaliser matches the numerator's weights and needs no lane reduction.
+  // m_run: the row's running maximum over this wave's keys, in scaled log2 units (the same in both
+  // lane halves).  lsum: the row's sum of the bf16 weights (every element holds it).
   float m_run = kFNegInf;
-  ff32x4_t O[8], lsum = ff32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  ff32x16_t O[4], lsum = {};
 #pragma unroll
-  for (int n8 = 0; n8 < 8; ++n8) O[n8] = ff32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int mb = 0; mb < 4; ++mb) O[mb] = ff32x16_t{};
   const fbf16x8_t ones = __builtin_bit_cast(fbf16x8_t, make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u));
 
-  uint4 nv[kChunks];
-  if (n_tiles > 0) {
-    load_tile(0, nv);
-    store_tile(0, nv);
-  }
-  // every load issued so far (queries, first tile) has landed: without this wait the loop's first
-  // matrix instruction would wait for the next tile's loads on every iteration
-  __builtin_amdgcn_s_waitcnt(0);
+  // Tiles are loaded kPrefetch tiles ahead into a ring of register sets (tile j in set j % kPrefetch)
+  // and stored to LDS one tile ahead.
+  uint4 nv[kPrefetch][kChunks];
+#pragma unroll
+  for (int j = 0; j < kPrefetch; ++j) load_tile(j, nv[j]);
+  if (n_tiles > 0) store_tile(0, nv[0]);
   __syncthreads();
-  // one tile; the buffer index is a compile-time constant so that LDS offsets are immediates
-  auto step = [&](int it, auto buf_c) {
-    constexpr int buf = decltype(buf_c)::value;
-    if (it + 1 < n_tiles) load_tile(it + 1, nv);  // in flight during this tile's matrix work
+  // one tile; buffer and register-set indices are compile-time constants (LDS offsets are
+  // immediates, registers stay registers)
+  auto step = [&](int it, auto buf_c, auto set_c) {
+    constexpr int buf = decltype(buf_c)::value;  // LDS buffer of tile it
+    constexpr int set = decltype(set_c)::value;  // register set of tile it (free: it is in LDS)
+    constexpr int nset = (set + 1) % kPrefetch;  // register set of tile it + 1
+    load_tile(it + kPrefetch, nv[set]);
     const uint8_t* lt = Ls[buf];
 
-    // S^T for keys 16 kb + 4 g + i of this tile, rows c16
-    constexpr int KB = kFTile / 16;
-    ff32x4_t s[KB];
+    // S^T for keys 32 kb + 8 q + 4 hh + r of this wave's half tile, row rl (s[kb][4 q + r])
+    ff32x16_t s[kKB];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      uint4 kv[4];  // the 16 keys' row chunks, all read before the first product
+    for (int kb = 0; kb < kKB; ++kb) {
+      s[kb] = ff32x16_t{};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kv[ks] = *reinterpret_cast<const uint4*>(lt + 16 * kRowBytes * kb + soff[ks]);
-      s[kb] = ff32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int k4 = 0; k4 < 2; ++k4) {
+        uint4 kv[4];  // four row chunks read before their products
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(fbf16x8_t, kv[ks]), qb[ks], s[kb], 0, 0, 0);
+        for (int u = 0; u < 4; ++u) kv[u] = *reinterpret_cast<const uint4*>(lt + 32 * kRowBytes * kb + soff[4 * k4 + u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s[kb] = mfma32(__builtin_bit_cast(fbf16x8_t, kv[u]), qb[4 * k4 + u], s[kb]);
+      }
     }
     // masks (only where some row of the workgroup does not see the whole tile)
     const bool blk_tile = it < n_bt;
@@ -264,21 +294,22 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     float tmax = kFNegInf;
     if (blk_tile && base + kFTile <= nbmin) {
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+      for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[kb][i]);
+        for (int v = 0; v < 16; ++v) tmax = fmaxf(tmax, s[kb][v]);
     } else {
-      const int lo = (blk_tile ? 0 : w0) - base, hi = (blk_tile ? nb : w1) - base;  // this row's keys of the tile
+      // this row's keys of the wave's half tile: [lo, hi) relative to its first key
+      const int k0 = base + kKW * kh;
+      const int lo = (blk_tile ? 0 : w0) - k0, hi = (blk_tile ? nb : w1) - k0;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+      for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int k = 16 * kb + 4 * g + i;
-          s[kb][i] = (k >= lo && k < hi) ? s[kb][i] : kFNegInf;
-          tmax = fmaxf(tmax, s[kb][i]);
+        for (int v = 0; v < 16; ++v) {
+          const int k = 32 * kb + 8 * (v >> 2) + 4 * hh + (v & 3);
+          s[kb][v] = (k >= lo && k < hi) ? s[kb][v] : kFNegInf;
+          tmax = fmaxf(tmax, s[kb][v]);
         }
     }
-    tmax = fmaxf(tmax, xor_lane<16>(tmax));
     tmax = fmaxf(tmax, xor_lane<32>(tmax));
     const float mt = tmax * a.scale2;
     if (__builtin_amdgcn_ballot_w64(mt > m_run)) {  // some row's maximum moved up
@@ -286,58 +317,82 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       const float alpha = m_new == kFNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       lsum *= alpha;
 #pragma unroll
-      for (int n8 = 0; n8 < 8; ++n8) O[n8] *= alpha;
+      for (int mb = 0; mb < 4; ++mb) O[mb] *= alpha;
       m_run = m_new;
     }
     const float nm = m_run == kFNegInf ? 0.0f : -m_run;
-    float sv[4 * KB];
+    // O^T[dims 32 mb + ..][row rl] += V^T P^T per 16-key chunk c of each block
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
+    for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sv[4 * kb + i] = __builtin_amdgcn_exp2f(fmaf(s[kb][i], a.scale2, nm));
-    // O^T[dims 16 n8 + 4 g + i][row c16] += V^T P^T per 32-key chunk; the reduction index runs over
-    // keys {4g..4g+3, 16+4g..16+4g+3} of the chunk for lane group g, in both operands
+      for (int c = 0; c < 2; ++c) {
+        float p[8];
 #pragma unroll
-    for (int kc = 0; kc < kFTile / 32; ++kc) {
-      const fbf16x8_t pb = __builtin_bit_cast(
-          fbf16x8_t, make_uint4(pack_bf16x2(sv[8 * kc + 0], sv[8 * kc + 1]), pack_bf16x2(sv[8 * kc + 2], sv[8 * kc + 3]),
-                                pack_bf16x2(sv[8 * kc + 4], sv[8 * kc + 5]), pack_bf16x2(sv[8 * kc + 6], sv[8 * kc + 7])));
-      lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb, lsum, 0, 0, 0);
-      fbf16x8_t va[8];  // the chunk's V^T operands, all read before the first product
+        for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * c + j], a.scale2, nm));
+        const fbf16x8_t pb = __builtin_bit_cast(
+            fbf16x8_t, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                                  pack_bf16x2(p[6], p[7])));
+        lsum = mfma32(ones, pb, lsum);
+        fbf16x8_t va[4];  // the chunk's V^T operands, read before their products
 #pragma unroll
-      for (int n8 = 0; n8 < 8; ++n8) {
-        const uint8_t* p = lt + 32 * kRowBytes * kc + toff[n8];
-        const fi16x4_t lo = lds_read_tr16(p);
-        const fi16x4_t hi = lds_read_tr16(p + 16 * kRowBytes);
-        va[n8] = __builtin_bit_cast(fbf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        for (int mb = 0; mb < 4; ++mb) {
+          const uint8_t* q0 = lt + (32 * kb + 16 * c) * kRowBytes;
+          const fi16x4_t lo4 = lds_read_tr16(q0 + toff[0][mb]);
+          const fi16x4_t hi4 = lds_read_tr16(q0 + toff[1][mb]);
+          va[mb] = __builtin_bit_cast(fbf16x8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) O[mb] = mfma32(va[mb], pb, O[mb]);
       }
-#pragma unroll
-      for (int n8 = 0; n8 < 8; ++n8) O[n8] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[n8], pb, O[n8], 0, 0, 0);
-    }
     // the other buffer was last read before the previous barrier
-    if (it + 1 < n_tiles) store_tile(buf ^ 1, nv);
+    if (it + 1 < n_tiles) store_tile(buf ^ 1, nv[nset]);
     __syncthreads();
   };
+  // unrolled over the two buffers so that both indices are constants (a skipped second step
+  // leaves the loop, so it does not blur the wait counts on the back edge)
 #pragma unroll 1
   for (int it = 0; it < n_tiles; it += 2) {
-    step(it, IntC<0>{});
-    if (it + 1 < n_tiles) step(it + 1, IntC<1>{});
+    step(it, IntC<0>{}, IntC<0>{});
+    if (it + 1 < n_tiles) step(it + 1, IntC<1>{}, IntC<1 % kPrefetch>{});
   }
 
-  // the sink, counted once: out = O / (l + e^{sink - m}) with m = max(m_run, sink)
-  const float l_run = lsum[0];
-  if (!rv) return;
+  // merge the two key halves of each row half (through the tile buffers, free after the last
+  // barrier): key half 1 writes its state, key half 0 combines and stores
+  float* ob = reinterpret_cast<float*>(&Ls[0][0]) + rh * (4 * 16 * 64);  // [mb][v][lane]
+  if (kh == 1) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) ob[(mb * 16 + v) * 64 + lane] = O[mb][v];
+    s_ml[rh][0][lane] = m_run;
+    s_ml[rh][1][lane] = lsum[0];
+  }
+  __syncthreads();
+  if (kh == 1 || !rv) return;
+  const float m1 = s_ml[rh][0][lane], l1 = s_ml[rh][1][lane];
+  const float mm = fmaxf(m_run, m1);
+  const float f0 = m_run == kFNegInf ? 0.0f : exp2f(m_run - mm);
+  const float f1 = m1 == kFNegInf ? 0.0f : exp2f(m1 - mm);
+  const float l_run = lsum[0] * f0 + l1 * f1;
+  // the sink, counted once: out = O / (l + e^{sink - m}) with m = max(mm, sink)
   const float sk = a.sink[h] * kLog2e;
-  const float mf = fmaxf(m_run, sk);
-  const float fo = m_run == kFNegInf ? 0.0f : exp2f(m_run - mf);
+  const float mf = fmaxf(mm, sk);
+  const float fo = mm == kFNegInf ? 0.0f : exp2f(mm - mf);
   const float L = fmaf(l_run, fo, exp2f(sk - mf));
-  const float rs = fo / L;
+  const float rs0 = f0 * fo / L, rs1 = f1 * fo / L;
   uint16_t* orow = a.out + (static_cast<int64_t>(b) * RT + r) * kFD;  // r < RT here
 #pragma unroll
-  for (int n8 = 0; n8 < 8; ++n8) {
-    const uint2 v = make_uint2(pack_bf16x2(O[n8][0] * rs, O[n8][1] * rs), pack_bf16x2(O[n8][2] * rs, O[n8][3] * rs));
-    *reinterpret_cast<uint2*>(orow + 16 * n8 + 4 * g) = v;
-  }
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int v = 4 * q + i;
+        o[i] = O[mb][v] * rs0 + ob[(mb * 16 + v) * 64 + lane] * rs1;
+      }
+      *reinterpret_cast<uint2*>(orow + 32 * mb + 8 * q + 4 * hh) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+    }
 }
 
 }  // namespace
