@@ -42,6 +42,7 @@ constexpr int kSortCap = 1024;       // at most this many candidates are sorted 
 constexpr int kMaxMfmaK = 1024;
 constexpr int kMaxNrb = 4;           // row blocks of 4 heads (IH <= 16)
 constexpr int64_t kMaxKeys = int64_t(1) << 30;
+constexpr int kScoreTT = 4;          // prefill rows sharing each key group in the score kernel
 
 typedef __attribute__((ext_vector_type(4))) int i32x4_t;
 
@@ -119,6 +120,28 @@ __device__ __forceinline__ int cmap(int ks, int g, int p) {
     const int q4 = p >> 2, r = p & 3;
     return 64 * ks + 16 * g + 8 * (q4 >> 1) + 2 * r + (q4 & 1);
   }
+}
+
+// Sum over the four 16-lane groups ("rows") of t[q], delivered to row q: a reduce-scatter with
+// three permlane swaps.  permlane16_swap(a, b) exchanges the odd rows of a with the even rows of b,
+// so a' + b' holds a's pair sums (rows 0+1, 2+3) in rows 0 and 2 and b's in rows 1 and 3;
+// permlane32_swap(u, w) exchanges u's upper half with w's lower half, so u' + w' holds u's half
+// sums in rows 0-1 and w's in rows 2-3.  Every row ends with (t[q]_0 + t[q]_1) + (t[q]_2 + t[q]_3)
+// for q = its row: the pairing of a butterfly sum, so the same fp32 value.  (The swap results are
+// copied to scalars before the bit casts: hipcc lowers __builtin_bit_cast of element 1 of the
+// builtin's result vector as element 0.)
+__device__ __forceinline__ float row_sums_scatter(const float (&t)[4]) {
+  auto sw16 = [](float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                    false, false);
+    const uint32_t x0 = r[0], x1 = r[1];
+    return __builtin_bit_cast(float, x0) + __builtin_bit_cast(float, x1);
+  };
+  const float u = sw16(t[0], t[1]), w = sw16(t[2], t[3]);
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, u), __builtin_bit_cast(uint32_t, w),
+                                                  false, false);
+  const uint32_t x0 = r[0], x1 = r[1];
+  return __builtin_bit_cast(float, x0) + __builtin_bit_cast(float, x1);
 }
 
 // 64-bit lane exchange with partner lane ^ j (j a power of two below 64, constant after unrolling).
@@ -344,36 +367,67 @@ __device__ __forceinline__ void query_fragments(const MfmaIdxArgs& a, int b, int
 
 // ---- score: keys -> order keys + the max of every 16-key slot ----------------------------------
 // A wave scores groups of SPW slots of 64 keys; lane l keeps key base + 64s + l of slot s.  All
-// loads of a group are issued before its matrix work.
-template <int BITS, int IC, int NRB>
-__global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a) {
+// loads of a group are issued before its matrix work.  With TT > 1 a workgroup scores TT rows
+// of the same key row (prefill targets of one sequence) against every key group it loads: the
+// codes and scales are read, and the integer B operand built, once for the TT rows.  Row
+// (sequence bs, target t) is bs * T + t; workgroup row y takes targets TT (y % ceil(T / TT)) + tt.
+// The register bound (at least 2 waves per SIMD, so at most 256 registers per lane) keeps the
+// matrix results in VGPRs: with the default 512 the compiler uses the AGPR form and moves every
+// result out with v_accvgpr_read.
+template <int BITS, int IC, int NRB, int TT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void
+idx_mfma_score_kernel(MfmaIdxArgs a) {
   constexpr int KS = IC / 64;
   constexpr int RB = BITS == 8 ? IC : IC / 2;        // code bytes per key
   constexpr int SPW = RB <= 32 ? 4 : (RB <= 64 ? 2 : 1);
   constexpr int LW = BITS == 8 ? 4 : 2;               // dwords per lane per k-step
-  const int b = blockIdx.y;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
   const int64_t S = a.S;
-  const int64_t nv = visible(a, b);
+
+  // this workgroup's rows: TT targets of key row kr (rows past the sequence's T are not scored)
+  int64_t row[TT];
+  bool rok[TT];
+  int64_t kr;
+  if constexpr (TT == 1) {
+    row[0] = blockIdx.y;
+    rok[0] = true;
+    kr = row[0] / a.T;
+  } else {
+    const int64_t ngt = (a.T + TT - 1) / TT;
+    kr = blockIdx.y / ngt;
+    const int64_t t0 = (blockIdx.y % ngt) * TT;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      rok[tt] = t0 + tt < a.T;
+      row[tt] = kr * a.T + (rok[tt] ? t0 + tt : t0);
+    }
+  }
+  int64_t nv[TT], nv_max = 0;
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    nv[tt] = rok[tt] ? visible(a, static_cast<int>(row[tt])) : 0;
+    nv_max = max(nv_max, nv[tt]);
+  }
 
   __shared__ int8_t dig[4][16][IC];
   __shared__ float hf[16][4];  // per head: digit factors S * 2^-7d (/16 for 4-bit) * weight
   __shared__ float hb[16][2];  // per head: clamp bounds
-  i32x4_t A[NRB][KS];
-  float f[NRB][4], lo[NRB], hi[NRB];
-  query_fragments<BITS, IC, NRB>(a, b, dig, hf, hb, A, f, lo, hi);
+  i32x4_t A[TT][NRB][KS];
+  float f[TT][NRB][4], lo[TT][NRB], hi[TT][NRB];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    if (tt > 0) __syncthreads();  // the previous row's fragments have been read out of LDS
+    query_fragments<BITS, IC, NRB>(a, static_cast<int>(row[tt]), dig, hf, hb, A[tt], f[tt], lo[tt], hi[tt]);
+  }
 
-  const int64_t kr = static_cast<int64_t>(b) / a.T;
   const uint8_t* crow = a.codes + kr * S * RB;
   const float* srow = a.kscale + kr * S;
-  uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.ks;
-  uint32_t* mrow = a.smax + static_cast<int64_t>(b) * a.ms;
   constexpr int64_t kGroupKeys = SPW * 64;
   const int64_t wave_base = (static_cast<int64_t>(blockIdx.x) * 4 + wv) * a.gpw * kGroupKeys;
 #pragma unroll 1
   for (int gi = 0; gi < a.gpw; ++gi) {
     const int64_t kb = wave_base + gi * kGroupKeys;
-    if (kb >= nv) break;  // wave-uniform
+    if (kb >= nv_max) break;  // wave-uniform
     uint32_t raw[SPW][4][KS][LW];
     float scl[SPW];
 #pragma unroll
@@ -381,7 +435,7 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a)
 #pragma unroll
       for (int tq = 0; tq < 4; ++tq) {
         const int64_t j = kb + 64 * s + 16 * tq + (lane & 15);
-        const int64_t jr = j < nv ? j : 0;  // nv >= 1 here; rows past nv are scored and dropped
+        const int64_t jr = j < nv_max ? j : 0;  // nv_max >= 1 here; keys past a row's count are dropped
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           if constexpr (BITS == 8) {
@@ -398,55 +452,65 @@ __global__ __launch_bounds__(kThreads) void idx_mfma_score_kernel(MfmaIdxArgs a)
         }
       }
       const int64_t jo = kb + 64 * s + lane;
-      scl[s] = srow[jo < nv ? jo : 0];
+      scl[s] = srow[jo < nv_max ? jo : 0];
     }
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
-      float tq_t[4];
+      i32x4_t Bop[4][KS];
 #pragma unroll
-      for (int tq = 0; tq < 4; ++tq) {
-        i32x4_t acc[NRB];
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) acc[rb] = i32x4_t{0, 0, 0, 0};
+      for (int tq = 0; tq < 4; ++tq)
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          i32x4_t Bop;
           if constexpr (BITS == 8) {
-            Bop = i32x4_t{static_cast<int>(raw[s][tq][ks][0]), static_cast<int>(raw[s][tq][ks][1]),
-                          static_cast<int>(raw[s][tq][ks][2]), static_cast<int>(raw[s][tq][ks][3])};
+            Bop[tq][ks] = i32x4_t{static_cast<int>(raw[s][tq][ks][0]), static_cast<int>(raw[s][tq][ks][1]),
+                                  static_cast<int>(raw[s][tq][ks][2]), static_cast<int>(raw[s][tq][ks][3])};
           } else {
             const uint32_t x = raw[s][tq][ks][0], y = raw[s][tq][ks][1];
-            Bop = i32x4_t{static_cast<int>((x << 4) & 0xF0F0F0F0u), static_cast<int>(x & 0xF0F0F0F0u),
-                          static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
+            Bop[tq][ks] = i32x4_t{static_cast<int>((x << 4) & 0xF0F0F0F0u), static_cast<int>(x & 0xF0F0F0F0u),
+                                  static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
           }
-#pragma unroll
-          for (int rb = 0; rb < NRB; ++rb) acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb][ks], Bop, acc[rb], 0, 0, 0);
         }
-        float t = 0.0f;
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) {
-          float v = static_cast<float>(acc[rb][0]) * f[rb][0];
-          v = fmaf(static_cast<float>(acc[rb][1]), f[rb][1], v);
-          v = fmaf(static_cast<float>(acc[rb][2]), f[rb][2], v);
-          v = fmaf(static_cast<float>(acc[rb][3]), f[rb][3], v);
-          t += __builtin_amdgcn_fmed3f(v, lo[rb], hi[rb]);
-        }
-        t += xor_lane<16>(t);  // sum over the four head groups
-        t += xor_lane<32>(t);
-        tq_t[tq] = t;
-      }
-      // lane l keeps key kb + 64s + l, i.e. tq = l / 16
-      const float mine = g == 0 ? tq_t[0] : (g == 1 ? tq_t[1] : (g == 2 ? tq_t[2] : tq_t[3]));
       const int64_t jo = kb + 64 * s + lane;
-      const uint32_t key = jo < nv ? order_key(mine * scl[s]) : 0u;
-      if (jo < nv) krow[jo] = key;
-      // max of the 16-key slot of lanes 16u .. 16u+15, stored by its first lane
-      uint32_t mx = key;
-      mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<1>(__builtin_bit_cast(float, mx))));
-      mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<2>(__builtin_bit_cast(float, mx))));
-      mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<4>(__builtin_bit_cast(float, mx))));
-      mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<8>(__builtin_bit_cast(float, mx))));
-      if ((lane & 15) == 0 && jo < nv) mrow[jo >> 4] = mx;
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        if (TT > 1 && kb + 64 * s >= nv[tt]) continue;  // wave-uniform: this row has no key in the slot group
+        float tq_t[4];
+#pragma unroll
+        for (int tq = 0; tq < 4; ++tq) {
+          i32x4_t acc[NRB];
+#pragma unroll
+          for (int rb = 0; rb < NRB; ++rb) acc[rb] = i32x4_t{0, 0, 0, 0};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+              acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tt][rb][ks], Bop[tq][ks], acc[rb], 0, 0, 0);
+          float t = 0.0f;
+#pragma unroll
+          for (int rb = 0; rb < NRB; ++rb) {
+            float v = static_cast<float>(acc[rb][0]) * f[tt][rb][0];
+            v = fmaf(static_cast<float>(acc[rb][1]), f[tt][rb][1], v);
+            v = fmaf(static_cast<float>(acc[rb][2]), f[tt][rb][2], v);
+            v = fmaf(static_cast<float>(acc[rb][3]), f[tt][rb][3], v);
+            t += __builtin_amdgcn_fmed3f(v, lo[tt][rb], hi[tt][rb]);
+          }
+          tq_t[tq] = t;
+        }
+        // sum over the four head groups; lane l keeps key kb + 64s + l, i.e. tq = l / 16
+        const float mine = row_sums_scatter(tq_t);
+        const bool ok = jo < nv[tt];
+        const uint32_t key = ok ? order_key(mine * scl[s]) : 0u;
+        uint32_t* krow = a.keys + row[tt] * a.ks;
+        uint32_t* mrow = a.smax + row[tt] * a.ms;
+        if (ok) krow[jo] = key;
+        // max of the 16-key slot of lanes 16u .. 16u+15, stored by its first lane
+        uint32_t mx = key;
+        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<1>(__builtin_bit_cast(float, mx))));
+        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<2>(__builtin_bit_cast(float, mx))));
+        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<4>(__builtin_bit_cast(float, mx))));
+        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<8>(__builtin_bit_cast(float, mx))));
+        if ((lane & 15) == 0 && ok) mrow[jo >> 4] = mx;
+      }
     }
   }
 }
@@ -770,12 +834,19 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
 typedef void (*kern_fn)(MfmaIdxArgs);
 
 template <int BITS, int IC>
-kern_fn pick_score(int nrb) {
+kern_fn pick_score(int nrb, int tt) {
+  if (tt == kScoreTT) {
+    switch (nrb) {
+      case 1: return idx_mfma_score_kernel<BITS, IC, 1, kScoreTT>;
+      case 2: return idx_mfma_score_kernel<BITS, IC, 2, kScoreTT>;
+      default: return nullptr;
+    }
+  }
   switch (nrb) {
-    case 1: return idx_mfma_score_kernel<BITS, IC, 1>;
-    case 2: return idx_mfma_score_kernel<BITS, IC, 2>;
-    case 3: return idx_mfma_score_kernel<BITS, IC, 3>;
-    case 4: return idx_mfma_score_kernel<BITS, IC, 4>;
+    case 1: return idx_mfma_score_kernel<BITS, IC, 1, 1>;
+    case 2: return idx_mfma_score_kernel<BITS, IC, 2, 1>;
+    case 3: return idx_mfma_score_kernel<BITS, IC, 3, 1>;
+    case 4: return idx_mfma_score_kernel<BITS, IC, 4, 1>;
     default: return nullptr;
   }
 }
@@ -817,16 +888,20 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
   a.ks = static_cast<int64_t>(align_up(static_cast<size_t>(S), 16));
 
   const int nrb = (IH + 3) / 4;
+  // prefill rows (T > 1 targets per key row) share each key group kScoreTT rows at a time
+  const int tt = (T >= kScoreTT && nrb <= 2) ? kScoreTT : 1;
   kern_fn score = nullptr;
-  if (bits == 8) score = IC == 64 ? pick_score<8, 64>(nrb) : pick_score<8, 128>(nrb);
-  else score = IC == 64 ? pick_score<4, 64>(nrb) : pick_score<4, 128>(nrb);
+  if (bits == 8) score = IC == 64 ? pick_score<8, 64>(nrb, tt) : pick_score<8, 128>(nrb, tt);
+  else score = IC == 64 ? pick_score<4, 64>(nrb, tt) : pick_score<4, 128>(nrb, tt);
   if (!score) return fail(AEKV_ERR_UNSUPPORTED, "%s: no matrix-core indexer for IH=%d IC=%d", who, IH, IC);
+  // workgroup rows: one per row, or one per kScoreTT targets of a key row
+  const int64_t n_y = tt == 1 ? B : (B / T) * ceil_div(T, static_cast<int64_t>(tt));
   // slot-group size of the score kernel (must match SPW there) and groups per wave: enough
   // workgroups to fill the chip (~2048), at most 16 groups per wave
   const int rb_bytes = bits == 8 ? IC : IC / 2;
   const int64_t group_keys = 64 * (rb_bytes <= 32 ? 4 : (rb_bytes <= 64 ? 2 : 1));
   const int64_t groups_per_row = ceil_div(S, group_keys);
-  int64_t gpw = (B * groups_per_row) / (4 * 2048);
+  int64_t gpw = (n_y * groups_per_row) / (4 * 2048);
   gpw = std::min<int64_t>(16, std::max<int64_t>(1, gpw));
   a.gpw = static_cast<int>(gpw);
   const int64_t n_score = ceil_div(groups_per_row, 4 * gpw);
@@ -834,7 +909,8 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
     return fail(AEKV_ERR_UNSUPPORTED, "%s: B=%lld S=%lld exceed the launch grid", who, static_cast<long long>(B),
                 static_cast<long long>(S));
   const uint32_t by = static_cast<uint32_t>(B);
-  hipLaunchKernelGGL(score, dim3(static_cast<uint32_t>(n_score), by), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL(score, dim3(static_cast<uint32_t>(n_score), static_cast<uint32_t>(n_y)), dim3(kThreads), 0, st,
+                     a);
   if (int rc = check_launch(who)) return rc;
   hipLaunchKernelGGL(idx_mfma_final_kernel, dim3(by), dim3(kSelThreads), 0, st, a, out_idx, out_score);
   return check_launch(who);
