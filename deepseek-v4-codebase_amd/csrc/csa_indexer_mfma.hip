@@ -43,6 +43,10 @@ constexpr int kMaxMfmaK = 1024;
 constexpr int kMaxNrb = 4;           // row blocks of 4 heads (IH <= 16)
 constexpr int64_t kMaxKeys = int64_t(1) << 30;
 constexpr int kScoreTT = 4;          // prefill rows sharing each key group in the score kernel
+#ifndef AEKV_IDX_TARGET_WG
+#define AEKV_IDX_TARGET_WG 2048
+#endif
+constexpr int64_t kScoreTargetWG = AEKV_IDX_TARGET_WG;  // score workgroups the launch aims for
 
 typedef __attribute__((ext_vector_type(4))) int i32x4_t;
 
@@ -901,7 +905,7 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
   const int rb_bytes = bits == 8 ? IC : IC / 2;
   const int64_t group_keys = 64 * (rb_bytes <= 32 ? 4 : (rb_bytes <= 64 ? 2 : 1));
   const int64_t groups_per_row = ceil_div(S, group_keys);
-  int64_t gpw = (n_y * groups_per_row) / (4 * 2048);
+  int64_t gpw = (n_y * groups_per_row) / (4 * kScoreTargetWG);
   gpw = std::min<int64_t>(16, std::max<int64_t>(1, gpw));
   a.gpw = static_cast<int>(gpw);
   const int64_t n_score = ceil_div(groups_per_row, 4 * gpw);
