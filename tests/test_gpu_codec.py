@@ -195,10 +195,11 @@ def test_specialised_and_generic_encode_agree(dev):
     np.testing.assert_array_equal(cs.cpu().numpy(), want_c)
 
 
-@pytest.mark.parametrize("n", [1, 15, 16, 4097])
+@pytest.mark.parametrize("n", [1, 15, 16, 4097, 262147])
 def test_specialised_and_generic_decode_agree(dev, n):
     """4-bit D=128 bf16 decode: the quad-layout kernel against the generic one and the oracle,
-    including scales of 2^124 and above (the kernel's exact-product fallback) and tiny scales."""
+    including scales of 2^124 and above (the kernel's exact-product fallback) and tiny scales.
+    262147 vectors take the several-passes-per-wave launch (65537 passes, the last one partial)."""
     import aetherkv._lib as L
 
     rng = np.random.default_rng(n)

@@ -119,16 +119,19 @@ def test_csa_prefill_matches_oracle_and_decode(dev, bits):
         assert torch.equal(out[:, t], dec), f"target {t} differs from the decode launch"
 
 
-def test_multi_target_indexer_ragged_valid(dev):
-    # per-(row, target) visible counts, including 0 and counts below k
-    B, T, S, IH, IC, k = 3, 7, 3000, 4, 64, 64
-    pq = PolarQuant(4)
+@pytest.mark.parametrize("bits,IH,IC", [(4, 4, 64), (8, 8, 128), (4, 6, 64)])
+def test_multi_target_indexer_ragged_valid(dev, bits, IH, IC):
+    # per-(row, target) visible counts, including 0 and counts below k; the targets go through the
+    # score kernel 4 per key group (IH 5..8: two 4-head row blocks), the reference through the
+    # single-target kernel
+    B, T, S, k = 3, 7, 3000, 64
+    pq = PolarQuant(bits)
     codes, scale = pq.encode(normal((B, S, IC), 71).to(dev))
     index_q = normal((B, T, IH, IC), 72, dtype=torch.float32).to(dev)
     index_w = normal((B, T, IH), 73, dtype=torch.float32).to(dev)
     valid = torch.tensor([[0, 1, 63, 64, 65, 2999, 3000], [5, 5, 5, 5, 5, 5, 5], [3000, 0, 1000, 17, 64, 1, 2]],
                          dtype=torch.int32)
-    print("multi-target indexer ragged", flush=True)
+    print(f"multi-target indexer ragged bits={bits} IH={IH} IC={IC}", flush=True)
     idx, sc = csa_prefill_indexer_topk_quant(index_q, index_w, codes, scale, k, quant=pq, valid=valid,
                                              return_scores=True)
     torch.cuda.synchronize()
@@ -138,6 +141,15 @@ def test_multi_target_indexer_ragged_valid(dev):
         assert torch.equal(idx[:, t], one), f"target {t}"
         assert torch.equal(sc[:, t], sc1), f"target {t} scores"
     assert bool((idx[0, 0] == -1).all()) and int((idx[1] >= 0).sum(-1).max()) == 5
+    # and against the oracle's exact top-k (up to fp32 near-ties)
+    keys = O.decode(codes.cpu().numpy(), scale.cpu().numpy(), bits, O.diag(42, IC), "f32")
+    for t in range(T):
+        qn, wn = index_q[:, t].cpu().numpy(), index_w[:, t].cpu().numpy()
+        vt = valid[:, t].numpy()
+        scores = O.index_scores(qn, wn, keys, valid=vt)
+        wa = np.log1p(np.exp(wn.astype(np.float64)))
+        tol = score_error_bound(qn, wa, keys, extra_rel=16 * math.log2(IC) * 2.0 ** -24)
+        assert_topk_matches(idx[:, t].cpu().numpy(), scores, k, tol, vt)
 
 
 def test_prefill_attention_defaults_and_empty_targets(dev):
