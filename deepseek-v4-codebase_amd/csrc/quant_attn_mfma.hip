@@ -69,12 +69,16 @@ struct QAttnMfmaArgs {
   uint16_t* out;          // [B, H, 128] bf16
 };
 
-// LDS layout (bytes): wave outputs for the merge | wave stats | per-head factors | block ids
-constexpr size_t kOffOb = 0;
-constexpr size_t kOffSt = kOffOb + sizeof(float) * kWaves * 16 * kD;
-constexpr size_t kOffInv = kOffSt + sizeof(float) * kWaves * 16 * 2;
-constexpr size_t kOffIdx = kOffInv + sizeof(float) * 16;
-constexpr size_t kLds = kOffIdx + sizeof(int32_t) * kSplitSrc;
+// LDS layout (bytes) for NW waves: wave outputs for the merge | wave stats | per-head factors |
+// block ids
+template <int NW>
+struct QLay {
+  static constexpr size_t ob = 0;
+  static constexpr size_t st = ob + sizeof(float) * NW * 16 * kD;
+  static constexpr size_t inv = st + sizeof(float) * NW * 16 * 2;
+  static constexpr size_t idx = inv + sizeof(float) * 16;
+  static constexpr size_t bytes = idx + sizeof(int32_t) * kSplitSrc;
+};
 
 __device__ __forceinline__ uint16_t bf16_bits(float v) { return static_cast<uint16_t>(pack_bf16x2(v, 0.0f) & 0xffffu); }
 
@@ -91,13 +95,17 @@ __device__ __forceinline__ int code_index(int g, int p) {
   }
 }
 
-template <int BITS>
-__global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs a) {
+// NW waves per workgroup: 8 for few rows (more waves share a row's sources), 4 for launches with
+// many rows (prefill), where half the merge work and LDS lets twice the workgroups reside.
+template <int BITS, int NW>
+__global__ __launch_bounds__(64 * NW) void quant_attn_mfma_kernel(QAttnMfmaArgs a) {
+  constexpr int kW = NW, kT = 64 * NW;
+  using L = QLay<NW>;
   extern __shared__ __align__(16) unsigned char lds[];
-  float* Ob = reinterpret_cast<float*>(lds + kOffOb);    // [wave][head][128]
-  float* stat = reinterpret_cast<float*>(lds + kOffSt);  // [wave][head][m, l]
-  float* inv = reinterpret_cast<float*>(lds + kOffInv);  // [head]
-  int32_t* sidx = reinterpret_cast<int32_t*>(lds + kOffIdx);
+  float* Ob = reinterpret_cast<float*>(lds + L::ob);    // [wave][head][128]
+  float* stat = reinterpret_cast<float*>(lds + L::st);  // [wave][head][m, l]
+  float* inv = reinterpret_cast<float*>(lds + L::inv);  // [head]
+  int32_t* sidx = reinterpret_cast<int32_t*>(lds + L::idx);
   constexpr int RB = BITS == 8 ? kD : kD / 2;   // code bytes per row
   constexpr int HB = RB / 2;                    // code bytes per 64-code half
 
@@ -116,7 +124,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
   const int64_t src1 = min<int64_t>(n_comp + wl, src0 + a.split_src);
   if (a.sel) {
     const int64_t nsel = min<int64_t>(src1, n_comp) - src0;
-    for (int64_t i = threadIdx.x; i < nsel; i += kThreads) {
+    for (int64_t i = threadIdx.x; i < nsel; i += kT) {
       const int64_t blk = a.sel[b * a.K + src0 + i];
       sidx[i] = blk >= 0 && blk < a.S ? static_cast<int32_t>(blk) : -1;
     }
@@ -186,7 +194,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
 
   const int n_groups = src1 > src0 ? static_cast<int>((src1 - src0 + kGroup - 1) / kGroup) : 0;
 #pragma unroll 1
-  for (int G = wv; G < n_groups; G += kWaves) {
+  for (int G = wv; G < n_groups; G += kW) {
     // both blocks' rows are requested before either is decoded (two gathers in flight)
     int kind[2];  // 0 empty, 1 code row, 2 window row
     uint32_t cw[2][2][BITS == 8 ? 4 : 2];
@@ -364,10 +372,10 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
     const int h = threadIdx.x;
     float M = a.n_split == 1 ? a.sink[h] : kNegInf;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, stat[(w * 16 + h) * 2]);
+    for (int w = 0; w < kW; ++w) M = fmaxf(M, stat[(w * 16 + h) * 2]);
     float L = a.n_split == 1 ? __expf(a.sink[h] - M) : 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kW; ++w) {
       const float mw = stat[(w * 16 + h) * 2];
       const float f = mw == kNegInf ? 0.0f : __expf(mw - M);
       L = fmaf(f, stat[(w * 16 + h) * 2 + 1], L);
@@ -383,11 +391,11 @@ __global__ __launch_bounds__(kThreads) void quant_attn_mfma_kernel(QAttnMfmaArgs
   }
   __syncthreads();
   // every output: 4 consecutive dims per thread; the diagonal folded into the keys comes off here
-  for (int p = threadIdx.x; p < H * (kD / 4); p += kThreads) {
+  for (int p = threadIdx.x; p < H * (kD / 4); p += kT) {
     const int h = p / (kD / 4), d4 = 4 * (p % (kD / 4));
     f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kW; ++w) {
       const float f = stat[(w * 16 + h) * 2];
       const f32x4_t o = *reinterpret_cast<const f32x4_t*>(Ob + (w * 16 + h) * kD + d4);
       acc = f32x4_t{fmaf(f, o[0], acc[0]), fmaf(f, o[1], acc[1]), fmaf(f, o[2], acc[2]), fmaf(f, o[3], acc[3])};
@@ -509,14 +517,18 @@ int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* s
   a.wscale = wht_scale(kD);
   a.part = static_cast<float*>(ws);
   a.out = static_cast<uint16_t*>(out);
-  auto fn = bits == 8 ? quant_attn_mfma_kernel<8> : quant_attn_mfma_kernel<4>;
-  static std::once_flag once8, once4;
-  std::call_once(bits == 8 ? once8 : once4, [&] {
+  // 4 waves per workgroup once the launch has >= 1024 workgroups (prefill rows), else 8
+  const bool narrow = rows * n_split >= 1024;
+  auto fn = narrow ? (bits == 8 ? quant_attn_mfma_kernel<8, 4> : quant_attn_mfma_kernel<4, 4>)
+                   : (bits == 8 ? quant_attn_mfma_kernel<8, 8> : quant_attn_mfma_kernel<4, 8>);
+  const size_t lds = narrow ? QLay<4>::bytes : QLay<8>::bytes;
+  static std::once_flag once[4];
+  std::call_once(once[(bits == 8 ? 2 : 0) + (narrow ? 1 : 0)], [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(kLds));
+                              static_cast<int>(lds));
   });
-  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(n_split), static_cast<uint32_t>(rows)), dim3(kThreads), kLds, st,
-                     a);
+  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(n_split), static_cast<uint32_t>(rows)), dim3(narrow ? 256 : kThreads),
+                     lds, st, a);
   if (int rc = check_launch(who)) return rc;
   if (n_split > 1) {
     hipLaunchKernelGGL(quant_attn_mfma_combine_kernel, dim3(static_cast<uint32_t>(rows)), dim3(kThreads), 0, st, a);
