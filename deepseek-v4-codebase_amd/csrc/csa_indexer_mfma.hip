@@ -38,7 +38,6 @@ constexpr int kThreads = 256;
 constexpr int kSelThreads = 1024;
 constexpr int kHistBins = 4096;      // slot-max histogram bins (key >> 16 below the row maximum)
 constexpr int kCandCap = 4096;       // candidates a row's workgroup collects in LDS (fast route)
-constexpr int kSortCap = 1024;       // at most this many candidates are sorted outright (one per thread)
 constexpr int kMaxMfmaK = 1024;
 constexpr int kMaxNrb = 4;           // row blocks of 4 heads (IH <= 16)
 constexpr int64_t kMaxKeys = int64_t(1) << 30;
@@ -537,15 +536,19 @@ __device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
 //     the kk-th largest key T; keys > T are taken with the lowest-index keys == T and the kk words
 //     placed by rank.  If the candidates overflow LDS (many equal keys), the levels run over all
 //     of the row's keys, read in index order.
-__global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs a, int64_t* __restrict__ out_idx,
+// NT threads per row; CAP candidates collected in LDS; up to NT candidates sorted outright.
+// 1024 / 4096 for few rows; 512 / 1536 (37 KB of LDS, 80 VGPRs: three rows per CU, where the
+// 1024-thread instance at 73 VGPRs fits one) for launches of many rows with k <= 512.
+template <int NT, int CAP>
+__global__ __launch_bounds__(NT) void idx_mfma_final_kernel(MfmaIdxArgs a, int64_t* __restrict__ out_idx,
                                                                      float* __restrict__ out_score) {
-  constexpr int NW = kSelThreads / 64;
-  __shared__ uint64_t cbuf[kCandCap];  // candidates: keys ck[] then indices ci[], or sort words
+  constexpr int NW = NT / 64;
+  __shared__ uint64_t cbuf[CAP];  // candidates: keys ck[] then indices ci[], or sort words
   __shared__ __align__(16) uint32_t h[kHistBins];
   __shared__ uint64_t sel[kMaxMfmaK];
   __shared__ uint32_t s_tot[NW], s_res[3], s_cnt[2], s_wave_eq[NW];
   uint32_t* ck = reinterpret_cast<uint32_t*>(cbuf);
-  uint32_t* ci = ck + kCandCap;
+  uint32_t* ci = ck + CAP;
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t nv = visible(a, b);
@@ -553,7 +556,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
   const uint32_t kk = static_cast<uint32_t>(min<int64_t>(k, nv));
   int64_t* orow = out_idx + static_cast<int64_t>(b) * k;
   float* srow = out_score ? out_score + static_cast<int64_t>(b) * k : nullptr;
-  for (int i = static_cast<int>(kk) + tid; i < k; i += kSelThreads) {
+  for (int i = static_cast<int>(kk) + tid; i < k; i += NT) {
     orow[i] = -1;
     if (srow) srow[i] = -__builtin_inff();
   }
@@ -564,17 +567,17 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
   const int64_t n_slots = (nv + 15) >> 4;
 
   // ---- 1. slot bound and candidates ----
-  // thread tid owns slots c0 + tid + r * kSelThreads (r < 4) of each pass of 4096 slots; with
+  // thread tid owns slots c0 + tid + r * NT (r < 4) of each pass of 4096 slots; with
   // n_slots <= 4096 (S <= 65536) the maxima loaded for the histogram are reused for the scan
   constexpr int kSlotPer = 4;
-  constexpr int64_t kSlotPass = static_cast<int64_t>(kSlotPer) * kSelThreads;
-  for (int i = tid; i < kHistBins; i += kSelThreads) h[i] = 0u;
+  constexpr int64_t kSlotPass = static_cast<int64_t>(kSlotPer) * NT;
+  for (int i = tid; i < kHistBins; i += NT) h[i] = 0u;
   if (tid == 0) s_cnt[0] = 0u;
   uint32_t mx[kSlotPer];
   auto load_max = [&](int64_t c0) {
 #pragma unroll
     for (int r = 0; r < kSlotPer; ++r) {
-      const int64_t sl = c0 + tid + static_cast<int64_t>(r) * kSelThreads;
+      const int64_t sl = c0 + tid + static_cast<int64_t>(r) * NT;
       mx[r] = sl < n_slots ? mrow[sl] : 0u;
     }
   };
@@ -598,7 +601,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
 #pragma unroll
     for (int r = 0; r < kSlotPer; ++r) {
       const uint32_t d = top - (mx[r] >> 16);
-      if (c0 + tid + static_cast<int64_t>(r) * kSelThreads < n_slots)
+      if (c0 + tid + static_cast<int64_t>(r) * NT < n_slots)
         atomicAdd(&h[kHistBins - 1 - (d < kHistBins - 1 ? d : kHistBins - 1)], 1u);
     }
   }
@@ -606,7 +609,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
   uint32_t tau = 0u;
   if (static_cast<int64_t>(kk) <= n_slots) {
     uint32_t t, ab, ct;
-    block_threshold<kSelThreads, kHistBins / kSelThreads>(h, kk, s_tot, s_res, t, ab, ct);
+    block_threshold<NT, kHistBins / NT>(h, kk, s_tot, s_res, t, ab, ct);
     (void)ab;
     (void)ct;
     tau = t > 0u ? (top - (kHistBins - 1 - t)) << 16 : 0u;
@@ -624,7 +627,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
       uint32_t tot = 0u;
 #pragma unroll
       for (int r = 0; r < kSlotPer; ++r) {
-        const int64_t sl = c0 + tid + static_cast<int64_t>(r) * kSelThreads;
+        const int64_t sl = c0 + tid + static_cast<int64_t>(r) * NT;
         q[r] = sl < n_slots && mx[r] >= tau;
         m[r] = __builtin_amdgcn_ballot_w64(q[r]);
         tot += static_cast<uint32_t>(__builtin_popcountll(m[r]));
@@ -634,13 +637,13 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
       base = __builtin_amdgcn_readfirstlane(base);
 #pragma unroll
       for (int r = 0; r < kSlotPer; ++r) {
-        if (q[r]) h[base + static_cast<uint32_t>(mbcnt64(m[r]))] = static_cast<uint32_t>(tid + r * kSelThreads);
+        if (q[r]) h[base + static_cast<uint32_t>(mbcnt64(m[r]))] = static_cast<uint32_t>(tid + r * NT);
         base += static_cast<uint32_t>(__builtin_popcountll(m[r]));
       }
     }
     __syncthreads();
     const int n_list = static_cast<int>(s_cnt[1]);
-    for (int li = tid; li < n_list; li += kSelThreads) {
+    for (int li = tid; li < n_list; li += NT) {
       const int64_t sl = c0 + h[li];
       uint32_t kw[16];
 #pragma unroll
@@ -658,7 +661,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         if (16 * sl + e < nv && kw[e] >= tau) {
-          if (p < static_cast<uint32_t>(kCandCap)) {
+          if (p < static_cast<uint32_t>(CAP)) {
             ck[p] = kw[e];
             ci[p] = static_cast<uint32_t>(16 * sl + e);
           }
@@ -669,14 +672,14 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
   }
   __syncthreads();
   const uint32_t n_cand = s_cnt[0];
-  const bool fast = n_cand <= static_cast<uint32_t>(kCandCap);
+  const bool fast = n_cand <= static_cast<uint32_t>(CAP);
   const int n = fast ? static_cast<int>(n_cand) : 0;
 
-  // ---- 2a. up to kSortCap candidates (the usual case): sort them all, emit the first kk ----
+  // ---- 2a. up to NT candidates (the usual case): sort them all, emit the first kk ----
   // Wave w sorts candidates 64w .. 64w+63 in registers (bitonic network over lane exchanges);
   // the runs go to LDS and every candidate's final position is its index in its run plus, for
   // each other run, the number of smaller words there (binary search).  Words are distinct.
-  if (fast && n <= kSortCap) {
+  if (fast && n <= NT) {
     uint64_t w = tid < n ? sort_word(ck[tid], ci[tid]) : ~0ull;
     if (64 * wv < n) {  // wave-uniform: waves past the candidates only pad
 #pragma unroll
@@ -732,16 +735,16 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
     const int nshift = shift - wbits;
     const uint32_t mask = static_cast<uint32_t>(nb - 1);
     __syncthreads();  // the previous level's readers of h are done
-    for (int i = tid; i < nb; i += kSelThreads) h[i] = 0u;
+    for (int i = tid; i < nb; i += NT) h[i] = 0u;
     __syncthreads();
     // (key >> 32) is undefined: level 0 has no prefix to match
     if (fast) {
-      for (int i = tid; i < n; i += kSelThreads) {
+      for (int i = tid; i < n; i += NT) {
         const uint32_t key = ck[i];
         if (lvl == 0 || (key >> shift) == prefix) atomicAdd(&h[(key >> nshift) & mask], 1u);
       }
     } else {
-      for (int64_t j = tid; j < nv; j += kSelThreads) {
+      for (int64_t j = tid; j < nv; j += NT) {
         const uint32_t key = krow[j];
         if (lvl == 0 || (key >> shift) == prefix) atomicAdd(&h[(key >> nshift) & mask], 1u);
       }
@@ -749,7 +752,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
     __syncthreads();
     uint32_t t, ab, ct;
     if (lvl < 2) {
-      block_threshold<kSelThreads, kHistBins / kSelThreads>(h, need, s_tot, s_res, t, ab, ct);
+      block_threshold<NT, kHistBins / NT>(h, need, s_tot, s_res, t, ab, ct);
     } else {
       if (wv == 0) wave_threshold<4>(h, need, s_res);  // 256 bins
       __syncthreads();
@@ -772,7 +775,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
   __syncthreads();
   if (fast) {
     const bool all_eq = n_eq == need;
-    for (int i = tid; i < n; i += kSelThreads) {
+    for (int i = tid; i < n; i += NT) {
       const uint32_t key = ck[i], idx = ci[i];
       const uint32_t pg = wave_reserve<1>(&s_cnt[0], key > T ? 1u : 0u);
       const uint32_t pe = wave_reserve<1>(&s_cnt[1], key == T && all_eq ? 1u : 0u);
@@ -790,7 +793,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
     }
   } else {
     uint32_t eq_run = 0;
-    for (int64_t base = 0; base < nv; base += kSelThreads) {
+    for (int64_t base = 0; base < nv; base += NT) {
       const int64_t j = base + tid;
       const uint32_t key = j < nv ? krow[j] : 0u;
       const bool gt = j < nv && key > T;
@@ -819,7 +822,7 @@ __global__ __launch_bounds__(kSelThreads) void idx_mfma_final_kernel(MfmaIdxArgs
   // the kk words are distinct: each one's output position is its rank.  Four adjacent lanes
   // share an element, each counting over a quarter of the words.
   const int q4 = (static_cast<int>(kk) + 3) / 4;
-  for (int base = 0; base < static_cast<int>(kk); base += kSelThreads / 4) {
+  for (int base = 0; base < static_cast<int>(kk); base += NT / 4) {
     const int i = base + (tid >> 2), part = tid & 3;
     const uint64_t w = i < static_cast<int>(kk) ? sel[i] : 0ull;
     const int j0 = part * q4, j1 = min(static_cast<int>(kk), j0 + q4);
@@ -916,7 +919,11 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
   hipLaunchKernelGGL(score, dim3(static_cast<uint32_t>(n_score), static_cast<uint32_t>(n_y)), dim3(kThreads), 0, st,
                      a);
   if (int rc = check_launch(who)) return rc;
-  hipLaunchKernelGGL(idx_mfma_final_kernel, dim3(by), dim3(kSelThreads), 0, st, a, out_idx, out_score);
+  if (B >= 1024 && k <= 512)
+    hipLaunchKernelGGL((idx_mfma_final_kernel<512, 1536>), dim3(by), dim3(512), 0, st, a, out_idx, out_score);
+  else
+    hipLaunchKernelGGL((idx_mfma_final_kernel<kSelThreads, kCandCap>), dim3(by), dim3(kSelThreads), 0, st, a, out_idx,
+                       out_score);
   return check_launch(who);
 }
 

@@ -152,6 +152,32 @@ def test_multi_target_indexer_ragged_valid(dev, bits, IH, IC):
         assert_topk_matches(idx[:, t].cpu().numpy(), scores, k, tol, vt)
 
 
+def test_multi_target_indexer_many_rows(dev):
+    # >= 1024 rows with k <= 512 select through the 512-thread kernel: sampled targets against the
+    # single-target indexer (1024-thread kernel) bit for bit and against the oracle's exact top-k
+    B, T, S, IH, IC, k = 2, 512, 2500, 4, 64, 256
+    pq = PolarQuant(8)
+    codes, scale = pq.encode(normal((B, S, IC), 81).to(dev))
+    index_q = normal((B, T, IH, IC), 82, dtype=torch.float32).to(dev)
+    index_w = normal((B, T, IH), 83, dtype=torch.float32).to(dev)
+    valid = torch.randint(0, S + 1, (B, T), generator=torch.Generator().manual_seed(84), dtype=torch.int32)
+    valid[0, :8] = torch.tensor([0, 1, 255, 256, 257, S, S - 1, 511], dtype=torch.int32)
+    print("multi-target indexer, 1024 rows", flush=True)
+    idx = csa_prefill_indexer_topk_quant(index_q, index_w, codes, scale, k, quant=pq, valid=valid)
+    torch.cuda.synchronize()
+    keys = O.decode(codes.cpu().numpy(), scale.cpu().numpy(), 8, O.diag(42, IC), "f32")
+    for t in list(range(8)) + list(range(9, T, 37)):
+        one = csa_indexer_topk_quant(index_q[:, t], index_w[:, t], codes, scale, k, quant=pq,
+                                     valid=valid[:, t].to(dev))
+        assert torch.equal(idx[:, t], one), f"target {t}"
+        qn, wn = index_q[:, t].cpu().numpy(), index_w[:, t].cpu().numpy()
+        vt = valid[:, t].numpy()
+        scores = O.index_scores(qn, wn, keys, valid=vt)
+        tol = score_error_bound(qn, np.log1p(np.exp(wn.astype(np.float64))), keys,
+                                extra_rel=16 * math.log2(IC) * 2.0 ** -24)
+        assert_topk_matches(idx[:, t].cpu().numpy(), scores, k, tol, vt)
+
+
 def test_prefill_attention_defaults_and_empty_targets(dev):
     # visible / window slices omitted: every target sees all n_sel blocks and the whole window; a
     # target with no source at all gets zeros (serving.py:451-452)
