@@ -12,7 +12,7 @@ load to the same bf16 values PolarQuant.decode produces, and attends them togeth
 and the per-head sink (split over source tiles, merged with the sink counted once).
 
 Score rule: ``mode="softplus"`` (aether_2b/modeling.py:609-611, default), ``"raw"`` (the serving
-engine's sum_h w_h relu(q_h.k), serving.py:618-619) or ``"relu_w"`` (csa_indexer_cuda.cu:222-231).
+engine's sum_h w_h relu(q_h.k), serving.py:618-619) or ``"relu_w"`` (csa_indexer_cuda.cu:44-55).
 """
 from __future__ import annotations
 

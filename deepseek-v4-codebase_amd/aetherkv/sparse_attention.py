@@ -5,7 +5,7 @@ Reference: aether_kernels/sparse_attention.py:8-83 (wrappers) and aether_kernels
 
 * ``sparse_sink_attention(q, kv, topk_indices, sink, softmax_scale)``
 * ``tiled_prefill_attention(q, kv, sink, softmax_scale, tile_size=256)``
-* ``csa_indexer_topk(index_q, index_kv, index_weight, k, *, mode="softplus")``
+* ``csa_indexer_topk(index_q, index_kv, index_weight, k, *, mode="relu_w")``
 * ``hca_compress(buffer_c, buffer_z)``
 
 Outputs are freshly allocated tensors on the inputs' device; kernels run on the current stream.
@@ -92,8 +92,8 @@ def _ext_tiled_prefill_attention(q, kv, sink, softmax_scale, tile_size):
     return out
 
 
-def _ext_csa_indexer_topk(index_q, index_kv, index_weight, k, mode="softplus"):
-    """bindings.cpp:88-101 and csa_indexer_cuda.cu:258-272 checks, then aekv_csa_indexer_topk."""
+def _ext_csa_indexer_topk(index_q, index_kv, index_weight, k, mode="relu_w"):
+    """bindings.cpp:88-101 and csa_indexer_cuda.cu:88-95 checks, then aekv_csa_indexer_topk."""
     for n, t in (("index_q", index_q), ("index_kv", index_kv), ("index_weight", index_weight)):
         _check_input(n, t)
     if index_q.dim() != 3:
@@ -161,12 +161,16 @@ def tiled_prefill_attention(q: torch.Tensor, kv: torch.Tensor, sink: torch.Tenso
 
 
 def csa_indexer_topk(index_q: torch.Tensor, index_kv: torch.Tensor, index_weight: torch.Tensor, k: int, *,
-                     mode: str = "softplus") -> torch.Tensor:
+                     mode: str = "relu_w") -> torch.Tensor:
     """Fused indexer score + top-k -> [B, k] int64, sorted by (score desc, index asc).
 
-    mode "softplus": sum_h softplus(w_h) relu(q_h.k)  (aether_2b/modeling.py:609-611, default)
+    The default is the rule of the reference function this replaces, so an unchanged caller gets
+    the same selection (up to fp32 near-ties; torch.topk's order among equal scores is unspecified):
+    mode "relu_w":   sum_h max(w_h,0) (q_h.k)         (aether_kernels/csrc/csa_indexer_cuda.cu:44-55,
+                                                       docstring aether_kernels/sparse_attention.py:57)
+    The model's and the serving engine's rules are selectable:
+    mode "softplus": sum_h softplus(w_h) relu(q_h.k)  (aether_2b/modeling.py:609-611)
     mode "raw":      sum_h w_h relu(q_h.k)            (aether_2b/serving.py:618-619)
-    mode "relu_w":   sum_h max(w_h,0) (q_h.k)         (aether_kernels/csrc/csa_indexer_cuda.cu:222-231)
     """
     return _ext_csa_indexer_topk(index_q.float().contiguous(), index_kv.float().contiguous(),
                                  index_weight.float().contiguous(), int(k), mode)

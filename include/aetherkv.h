@@ -61,7 +61,7 @@ typedef enum {
 /* Indexer score rules.  The reference has three (file:line of each):
  *   AEKV_IDX_SOFTPLUS : sum_h softplus(w_h) * relu(q_h . k_j)   aether_2b/modeling.py:609-611, :521-523
  *   AEKV_IDX_RAW      : sum_h w_h * relu(q_h . k_j)             aether_2b/serving.py:618-619
- *   AEKV_IDX_RELU_W   : sum_h max(w_h, 0) * (q_h . k_j)         aether_kernels/csrc/csa_indexer_cuda.cu:222-231 */
+ *   AEKV_IDX_RELU_W   : sum_h max(w_h, 0) * (q_h . k_j)         aether_kernels/csrc/csa_indexer_cuda.cu:44-55 */
 typedef enum {
   AEKV_IDX_SOFTPLUS = 0,
   AEKV_IDX_RAW = 1,

@@ -276,7 +276,7 @@ int aekvo_decode(const uint8_t* codes, const float* scale, int64_t n, int d, int
 /*   mode 0 softplus : aether_2b/modeling.py:609-611 (and :521-523)                             */
 /*                     score = sum_h softplus(w_h) * relu(q_h . k)                               */
 /*   mode 1 raw      : aether_2b/serving.py:618-619  score = sum_h w_h * relu(q_h . k)           */
-/*   mode 2 relu_w   : aether_kernels/csrc/csa_indexer_cuda.cu:222-231                           */
+/*   mode 2 relu_w   : aether_kernels/csrc/csa_indexer_cuda.cu:44-55                           */
 /*                     score = sum_{h: w_h > 0} w_h * (q_h . k)                                  */
 /* softplus = torch.nn.functional.softplus(beta=1, threshold=20): x > 20 ? x : log1p(exp(x)).   */
 /* keys: fp32 [B,S,IC]; scores double [B,S]; j >= valid[b] -> -inf (modeling.py:612-614).       */

@@ -138,7 +138,7 @@ def decode(codes: np.ndarray, scale: np.ndarray, bits: int, diag_vec: np.ndarray
 # ---- CSA indexer -----------------------------------------------------------------------------
 def index_scores(q: np.ndarray, w: np.ndarray, keys: np.ndarray, valid: Optional[np.ndarray] = None,
                  mode: str = "softplus", threads: int = 0) -> np.ndarray:
-    """Indexer scores in double (modeling.py:609-611 / serving.py:618-619 / csa_indexer_cuda.cu:222-231).
+    """Indexer scores in double (modeling.py:609-611 / serving.py:618-619 / csa_indexer_cuda.cu:44-55).
 
     q [B,IH,IC] f32, w [B,IH] f32, keys [B,S,IC] f32 -> [B,S] float64 (-inf beyond valid[b])."""
     q, w, keys = _c(q, np.float32), _c(w, np.float32), _c(keys, np.float32)

@@ -178,6 +178,32 @@ def test_config3_csa_decode_end_to_end(dev):
     _close(out.view(B, H, D), _oracle_quant(pq, kv_codes, kv_scale, idx, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
 
 
+def test_config5_csa_decode_end_to_end(dev):
+    # benchmark configuration cfg5: B=64, 65536 blocks (compression 4), 4-bit codes, N(0,1) with 2% outlier
+    # channels x8, seed 4; indexer 4x64 softplus over all blocks, top-256 + window 128 + per-head sink
+    # (serving.py:597-625).  Inputs as bench.py generates them.  Every row's selection against the
+    # oracle's exact top-k (up to fp32 near-ties), attention against the oracle on that selection.
+    from test_gpu_indexer import _oracle_rows_check
+
+    B, H, D, S, W, IH, IC, seed = 64, 12, 128, 65536, 128, 4, 64, 4
+    pq = PolarQuant(4)
+    kv_codes, kv_scale = pq.encode(normal_with_outliers((B, S, D), seed, device=dev, trailing_dims=1))
+    ix_codes, ix_scale = pq.encode(normal_with_outliers((B, S, IC), seed + 1000, device=dev, trailing_dims=1))
+    q = normal((B, 1, H, D), seed + 1).to(dev)
+    index_q = normal((B, IH, IC), seed + 2, dtype=torch.float32).to(dev)
+    index_w = normal((B, IH), seed + 3, dtype=torch.float32).to(dev)
+    win = normal((B, W, D), seed + 4).to(dev)
+    sink = normal((H,), seed + 5, dtype=torch.float32).to(dev)
+    sm = D ** -0.5
+    print("cfg5 CSA decode, 64 rows", flush=True)
+    out, idx = csa_decode(q, index_q, index_w, ix_codes, ix_scale, kv_codes, kv_scale, win, sink, sm, kv_quant=pq,
+                          top_k=256)
+    torch.cuda.synchronize()
+    assert idx.shape == (B, 256) and out.shape == q.shape
+    _oracle_rows_check(pq, ix_codes, ix_scale, index_q, index_w, idx.cpu().numpy(), 256, range(B))
+    _close(out.view(B, H, D), _oracle_quant(pq, kv_codes, kv_scale, idx, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
+
+
 @pytest.fixture(params=["matrix", "generic"])
 def attn_path(request):
     """Run a case on the matrix-core attention (default for head_dim 128) and on the generic one."""

@@ -124,3 +124,56 @@ def test_paged_code_pages_round_trip_through_decode(dev, bits):
     out1, idx1 = csa_decode_ring(q, iq, iw, ix2, kv2, win, sink, 128 ** -0.5, top_k=256)
     assert torch.equal(idx0, idx1)
     assert torch.equal(out0, out1)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_code_pages_match_oracle(dev, bits):
+    # The reference's paged allocator stores each flushed block as PolarQuant.decode of its code, in bf16
+    # (serving.py:378-398, :857-905).  A code page stores the code itself: its rows must equal the
+    # oracle's encode of the original blocks, their decode must equal the oracle's decode (the values the
+    # reference's bf16 page holds), and a decode step over materialised pages must match the oracle's
+    # exact top-k and its attention over that selection.
+    from aetherkv.storage import flush_page, materialize_pages, unpack_rows
+    from test_gpu_indexer import w_act
+    from topk_check import assert_topk_matches, score_error_bound
+
+    n, per_page, H, D, W, IH, IC = 700, 32, 12, 128, 32, 4, 64
+    pq = PolarQuant(bits)
+    g = torch.Generator().manual_seed(61 + bits)
+    xk = torch.randn(1, n, D, generator=g).to(torch.bfloat16)
+    xi = torch.randn(1, n, IC, generator=g).to(torch.bfloat16)
+    kv, ix = CodeRing(pq, 1, D, capacity=64, device=dev), CodeRing(pq, 1, IC, capacity=64, device=dev)
+    kv.append(xk.to(dev))
+    ix.append(xi.to(dev))
+    pages = []
+    while kv.n >= per_page:
+        pages.append(flush_page({"kv": kv, "ix": ix}, {"kv": per_page, "ix": per_page}))
+    dg, dgi = O.diag(42, D), O.diag(42, IC)
+    want_c, want_s = O.encode(bf16_bits(xk).reshape(n, D), "bf16", bits, dg)
+    for i, p in enumerate(pages):
+        c, s = unpack_rows(p["kv"], bits)
+        rows = slice(i * per_page, (i + 1) * per_page)
+        np.testing.assert_array_equal(c.cpu().numpy(), want_c[rows], err_msg=f"page {i} codes")
+        np.testing.assert_array_equal(s.cpu().numpy(), want_s[rows], err_msg=f"page {i} scales")
+        np.testing.assert_array_equal(bf16_bits(pq.decode(c, s)), O.decode(want_c[rows], want_s[rows], bits, dg, "bf16"),
+                                      err_msg=f"page {i} decoded values")
+    kv2 = materialize_pages(pages, "kv", pq, D, resident=kv)
+    ix2 = materialize_pages(pages, "ix", pq, IC, resident=ix)
+    gq = torch.Generator().manual_seed(71 + bits)
+    q = torch.randn(1, 1, H, D, generator=gq).to(torch.bfloat16).to(dev)
+    iq = torch.randn(1, IH, IC, generator=gq).to(dev)
+    iw = torch.randn(1, IH, generator=gq).to(dev)
+    win = torch.randn(1, W, D, generator=gq).to(torch.bfloat16).to(dev)
+    sink = torch.randn(H, generator=gq).to(dev)
+    out, idx = csa_decode_ring(q, iq, iw, ix2, kv2, win, sink, D ** -0.5, top_k=256)
+    # oracle: keys from the ORIGINAL blocks' codes
+    ic, is_ = O.encode(bf16_bits(xi).reshape(n, IC), "bf16", bits, dgi)
+    keys = O.decode(ic, is_, bits, dgi, "f32").reshape(1, n, IC)
+    qn, wn = iq.cpu().numpy(), iw.cpu().numpy()
+    scores = O.index_scores(qn, wn, keys)
+    tol = score_error_bound(qn, w_act(wn, "softplus"), keys, extra_rel=96 * 2.0 ** -24)
+    assert_topk_matches(idx.cpu().numpy(), scores, 256, tol)
+    want = O.quant_attention(q.float().cpu().numpy().reshape(1, H, D), want_c.reshape(1, n, -1),
+                             want_s.reshape(1, n), idx.cpu().numpy(), win.float().cpu().numpy(),
+                             sink.cpu().numpy(), dg, bits, D ** -0.5)
+    np.testing.assert_allclose(out.float().cpu().numpy().reshape(1, H, D), want, rtol=1e-2, atol=2e-3)

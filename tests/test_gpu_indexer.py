@@ -44,7 +44,7 @@ def test_fp32_indexer_matches_oracle(dev, mode, S, k):
 
 
 def test_fp32_indexer_reference_contract(dev):
-    # k must be in [1, S] (csa_indexer_cuda.cu:272); output int64 [B, k]
+    # k must be in [1, S] (csa_indexer_cuda.cu:95); output int64 [B, k]
     q = torch.randn(1, 2, 8, device=dev)
     kv = torch.randn(1, 5, 8, device=dev)
     w = torch.randn(1, 2, device=dev)
@@ -163,3 +163,103 @@ def test_quant_indexer_exact_ties_take_lowest_indices(dev, indexer_path, bits, n
     s = sc.cpu()
     top = min(n_special, k)
     assert torch.all(s[:, :top] == s[:, :1]) and torch.all(s[:, top:] * 2 == s[:, :1])
+
+
+def test_fp32_indexer_default_rule_is_the_reference_functions(dev):
+    # an unchanged caller of csa_indexer_topk (no mode) gets the rule of the function it replaces:
+    # sum over heads with w_h > 0 of w_h * (q_h . k), no relu on the dot
+    # (aether_kernels/csrc/csa_indexer_cuda.cu:44-55; "relu applied internally", sparse_attention.py:57)
+    B, S, IH, IC, k = 3, 3000, 4, 64, 256
+    g = torch.Generator().manual_seed(91)
+    q = torch.randn(B, IH, IC, generator=g)
+    kv = torch.randn(B, S, IC, generator=g)
+    w = torch.randn(B, IH, generator=g) * 2
+    w[0] = torch.tensor([1.5, -0.5, 0.25, -2.0])   # mixed signs: relu on the weight matters
+    idx = csa_indexer_topk(q.to(dev), kv.to(dev), w.to(dev), k).cpu().numpy()
+    scores = O.index_scores(q.numpy(), w.numpy(), kv.numpy(), mode="relu_w")
+    tol = score_error_bound(q.numpy(), w_act(w.numpy(), "relu_w"), kv.numpy())
+    assert_topk_matches(idx, scores, k, tol)
+    # the softplus rule selects a different set on these rows, so the default is not it
+    soft = O.topk(O.index_scores(q.numpy(), w.numpy(), kv.numpy(), mode="softplus"), k)[0]
+    assert any(set(idx[b]) != set(soft[b]) for b in range(B))
+
+
+def _cfg5_index_inputs(dev, B=64, S=65536, IH=4, IC=64, seed=4):
+    """cfg5's index cache and query: 4-bit keys, N(0,1) with 2% outlier channels x8 (seed 4)."""
+    pq = PolarQuant(4)
+    codes, scale = pq.encode(normal_with_outliers((B, S, IC), seed + 1000, device=dev, trailing_dims=1))
+    q = normal((B, IH, IC), seed + 2, dtype=torch.float32).to(dev)
+    w = normal((B, IH), seed + 3, dtype=torch.float32).to(dev)
+    return pq, codes, scale, q, w
+
+
+def _oracle_rows_check(pq, codes, scale, q, w, idx, k, rows, valid=None, mode="softplus"):
+    """Oracle top-k check of the given rows, 8 rows at a time (keys dequantised in fp32)."""
+    IC = q.shape[-1]
+    dg = O.diag(42, IC)
+    rows = list(rows)
+    for i in range(0, len(rows), 8):
+        r = rows[i:i + 8]
+        keys = O.decode(codes[r].cpu().numpy(), scale[r].cpu().numpy(), pq.bits, dg, "f32")
+        qn, wn = q[r].cpu().numpy(), w[r].cpu().numpy()
+        vr = None if valid is None else np.asarray(valid)[r].astype(np.int32)
+        scores = O.index_scores(qn, wn, keys, valid=vr, mode=mode)
+        tol = score_error_bound(qn, w_act(wn, mode), keys, extra_rel=16 * math.log2(IC) * 2.0 ** -24)
+        assert_topk_matches(idx[r], scores, k, tol, vr)
+
+
+@pytest.mark.parametrize("ragged", [False, True])
+def test_config5_indexer_all_rows_multi_group_waves(dev, ragged):
+    # cfg5's whole launch: 64 rows x 65536 4-bit keys.  The score kernel gives each wave two slot groups
+    # here (64 rows x 256 groups / 8192); 2-row launches give one.  Both must agree bit for bit, and every
+    # row must match the oracle's exact top-k.  Ragged visible counts end a wave's keys part-way through
+    # its groups.
+    B, S, k = 64, 65536, 256
+    pq, codes, scale, q, w = _cfg5_index_inputs(dev)
+    valid = None
+    if ragged:
+        g = torch.Generator().manual_seed(45)
+        valid = torch.randint(0, S + 1, (B,), generator=g, dtype=torch.int32)
+        valid[:6] = torch.tensor([0, 1, 255, 256, 257, 65535], dtype=torch.int32)
+        valid[6:12] = torch.tensor([300, 511, 513, 767, 1025, 33000], dtype=torch.int32)
+    vd = None if valid is None else valid.to(dev)
+    print(f"cfg5 indexer, all 64 rows, ragged={ragged}", flush=True)
+    idx, sc = csa_indexer_topk_quant(q, w, codes, scale, k, quant=pq, valid=vd, return_scores=True)
+    torch.cuda.synchronize()
+    for b in range(0, B, 2):
+        one, sc1 = csa_indexer_topk_quant(q[b:b + 2], w[b:b + 2], codes[b:b + 2], scale[b:b + 2], k, quant=pq,
+                                          valid=None if vd is None else vd[b:b + 2], return_scores=True)
+        assert torch.equal(idx[b:b + 2], one), f"rows {b}, {b + 1}: 64-row launch differs from a 2-row launch"
+        assert torch.equal(sc[b:b + 2], sc1), f"rows {b}, {b + 1}: scores differ"
+    rows = range(B) if not ragged else list(range(12)) + list(range(12, B, 7))
+    _oracle_rows_check(pq, codes, scale, q, w, idx.cpu().numpy(), k, rows,
+                       None if valid is None else valid.numpy())
+
+
+def test_prefill_chunk_indexer_bench_shape(dev):
+    # the CSA prefill chunk of the benchmark: 8 sequences x 256 targets at positions 65280..65535 over
+    # 16384 8-bit blocks (top-256).  The score kernel shares each key group among 4 targets and gives
+    # each wave 8 slot groups (512 row groups x 128 groups / 8192).  Sampled targets against the
+    # single-target indexer bit for bit and against the oracle.
+    from aetherkv.prefill import csa_prefill_indexer_topk_quant
+
+    B, T, S, IH, IC, k = 8, 256, 16384, 4, 64, 256
+    pq = PolarQuant(8)
+    codes, scale = pq.encode(normal((B, S, IC), 12).to(dev))
+    index_q = normal((B, T, IH, IC), 13, dtype=torch.float32).to(dev)
+    index_w = normal((B, T, IH), 14, dtype=torch.float32).to(dev)
+    pos = torch.arange(65280, 65536)
+    valid = torch.clamp(torch.div(pos + 1, 4, rounding_mode="floor"), max=S).to(torch.int32)   # visible blocks
+    print("prefill chunk indexer, 2048 rows", flush=True)
+    idx = csa_prefill_indexer_topk_quant(index_q, index_w, codes, scale, k, quant=pq, valid=valid)
+    torch.cuda.synchronize()
+    dg = O.diag(42, IC)
+    keys = O.decode(codes.cpu().numpy(), scale.cpu().numpy(), 8, dg, "f32")
+    for t in (0, 1, 2, 3, 4, 127, 128, 200, 254, 255):
+        vt = torch.full((B,), int(valid[t]), dtype=torch.int32)
+        one = csa_indexer_topk_quant(index_q[:, t], index_w[:, t], codes, scale, k, quant=pq, valid=vt.to(dev))
+        assert torch.equal(idx[:, t], one), f"target {t}"
+        qn, wn = index_q[:, t].cpu().numpy(), index_w[:, t].cpu().numpy()
+        scores = O.index_scores(qn, wn, keys, valid=vt.numpy())
+        tol = score_error_bound(qn, w_act(wn, "softplus"), keys, extra_rel=16 * math.log2(IC) * 2.0 ** -24)
+        assert_topk_matches(idx[:, t].cpu().numpy(), scores, k, tol, vt.numpy())

@@ -204,3 +204,37 @@ def test_prefill_rejects_unsupported_shapes(dev):
     with pytest.raises(RuntimeError, match="16 supported"):
         quant_prefill_attention(q, codes, torch.ones(1, 3, device=dev), None, None, torch.zeros(17, device=dev),
                                 0.1, quant=pq)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_prefill_attention_many_rows(dev, bits):
+    # >= 1024 rows: the attention runs its 4-wave workgroup instance.  Ragged per-target selections
+    # (some entries out of range) and window slices; sampled targets against the oracle and against
+    # the decode entry point on the same sources (the 8-wave instance), both within the tolerance.
+    B, T, H, S, K, Wt = 2, 512, 12, 3000, 256, 160
+    pq, codes, scale, q, win, sink = _inputs(dev, B, T, H, S, Wt, bits, 120 + bits)
+    g = torch.Generator().manual_seed(121 + bits)
+    sel = torch.randint(-3, S + 3, (B, T, K), generator=g)
+    visible = torch.randint(0, K + 1, (B, T), generator=g, dtype=torch.int32)
+    visible[0, :4] = torch.tensor([0, 1, K, K - 1], dtype=torch.int32)
+    win_start = torch.randint(0, Wt, (B, T), generator=g, dtype=torch.int32)
+    win_len = torch.randint(0, 129, (B, T), generator=g, dtype=torch.int32)
+    win_len = torch.minimum(win_len, Wt - win_start)
+    win_len[1, :3] = 0
+    sm = 128 ** -0.5
+    print(f"prefill attention 1024 rows bits={bits}", flush=True)
+    out = quant_prefill_attention(q, codes, scale, sel.to(dev), win, sink, sm, quant=pq, visible=visible.to(dev),
+                                  win_start=win_start.to(dev), win_len=win_len.to(dev))
+    torch.cuda.synchronize()
+    for t in list(range(6)) + list(range(7, T, 41)):
+        for b in range(B):
+            g_, s0, n = int(visible[b, t]), int(win_start[b, t]), int(win_len[b, t])
+            st = sel[b:b + 1, t, :g_].contiguous()
+            win_t = win[b:b + 1, s0:s0 + n].contiguous()
+            want = _oracle_target(pq, codes[b:b + 1], scale[b:b + 1], st.numpy(), q[b:b + 1, t], win_t, sink, sm)
+            np.testing.assert_allclose(to_np_f32(out[b, t])[None], want, rtol=QUANT_RTOL, atol=QUANT_ATOL,
+                                       err_msg=f"target {t} row {b}")
+            dec = quant_sink_attention(q[b:b + 1, t], codes[b:b + 1].contiguous(), scale[b:b + 1].contiguous(),
+                                       st.to(dev), win_t if n else None, sink, sm, quant=pq)
+            np.testing.assert_allclose(to_np_f32(out[b, t]), to_np_f32(dec[0]), rtol=QUANT_RTOL, atol=QUANT_ATOL,
+                                       err_msg=f"target {t} row {b} vs the decode launch")

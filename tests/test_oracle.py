@@ -247,7 +247,7 @@ def test_encode_decode_deterministic_and_threads_agree():
     np.testing.assert_array_equal(a[1], b[1])
 
 
-# ---- indexer (modeling.py:609-616, serving.py:618-621, csa_indexer_cuda.cu:222-231) ----------------
+# ---- indexer (modeling.py:609-616, serving.py:618-621, csa_indexer_cuda.cu:44-55) ----------------
 def _brute_scores(q, w, keys, mode):
     dots = np.einsum("bhc,bsc->bhs", q.astype(np.float64), keys.astype(np.float64))
     w = w.astype(np.float64)
