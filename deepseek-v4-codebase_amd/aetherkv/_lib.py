@@ -33,8 +33,11 @@ SYMBOLS = (
     "aekv_csa_indexer_topk_quant", "aekv_sparse_sink_attention", "aekv_quant_attention_workspace_size",
     "aekv_quant_sink_attention", "aekv_hca_compress", "aekv_tiled_prefill_attention", "aekv_set_generic_kernels",
     "aekv_emit_block", "aekv_csa_prefill_indexer_topk_quant", "aekv_quant_prefill_workspace_size",
-    "aekv_quant_prefill_attention", "aekv_rope_rmsnorm",
+    "aekv_quant_prefill_attention", "aekv_rope_rmsnorm", "aekv_csa_indexer_topk_quant_noalloc",
 )
+
+# size of the static device scratch behind aekv_csa_indexer_topk_quant_noalloc (AEKV_STATIC_SCRATCH_BYTES)
+STATIC_SCRATCH_BYTES = 32 << 20
 
 _lib: Optional[ctypes.CDLL] = None
 
@@ -78,6 +81,8 @@ def lib() -> ctypes.CDLL:
                                       ctypes.c_int),
         "aekv_hca_compress": ([P, P, I32_, I64_, I64_, I64_, P, P], ctypes.c_int),
         "aekv_emit_block": ([P, P, P, I64_, I64_, I32_, I32_, P, P, P, F, I32_, P, P, P, I64_, P, P], ctypes.c_int),
+        "aekv_csa_indexer_topk_quant_noalloc": ([P, P, P, P, P, P, I64_, I64_, I32_, I32_, I32_, I32_, I32_, P, P, P],
+                                                ctypes.c_int),
         "aekv_csa_prefill_indexer_topk_quant": (
             [P, P, P, P, P, P, I64_, I64_, I64_, I32_, I32_, I32_, I32_, I32_, P, SZ, P, P, P], ctypes.c_int),
         "aekv_quant_prefill_workspace_size": ([I64_, I64_, I64_, I64_, I64_], SZ),

@@ -18,6 +18,7 @@
 // (the WHT is orthogonal and symmetric; turbo_quant.py:208-209), and since scale_j > 0,
 // relu(scale_j * x) = scale_j * relu(x).
 #include <algorithm>
+#include <mutex>
 
 #include "aekv_common.h"
 
@@ -404,10 +405,11 @@ extern "C" int aekv_csa_indexer_topk(const float* index_q, const float* index_kv
 namespace {
 
 // rows = B * T query rows; row r scores the codes of key row r / T
-int topk_quant_rows(const float* index_q, const float* index_weight, const void* key_codes, const float* key_scale,
-                    const float* diag, const int32_t* valid, int64_t B, int64_t T, int64_t S, int32_t IH, int32_t IC,
-                    int32_t bits, int32_t k, int32_t mode, void* ws, size_t ws_bytes, int64_t* out_idx,
-                    float* out_score, void* stream, const char* who) {
+// host-side checks of a quantised-key launch (no HIP call)
+int validate_quant_rows(const float* index_q, const float* index_weight, const void* key_codes,
+                        const float* key_scale, const float* diag, int64_t B, int64_t T, int64_t S, int32_t IH,
+                        int32_t IC, int32_t bits, int32_t k, int32_t mode, void* ws, size_t ws_bytes,
+                        int64_t* out_idx, const char* who) {
   if (bits != 4 && bits != 8) return fail(AEKV_ERR_VALUE, "bits must be 4 or 8, got %d", bits);
   if (!is_pow2(IC)) return fail(AEKV_ERR_VALUE, "WHT requires last dim to be a power of 2, got %d", IC);
   if (bits == 4 && IC < 2) return fail(AEKV_ERR_VALUE, "4-bit packing needs an even last dim, got %d", IC);
@@ -415,8 +417,19 @@ int topk_quant_rows(const float* index_q, const float* index_weight, const void*
   if (B > 0 && T > 65535 / B) return fail(AEKV_ERR_UNSUPPORTED, "%s: B*T exceeds 65535", who);
   const int64_t rows = B * T;
   if (int rc = validate_common(index_q, index_weight, rows, S, IH, IC, k, mode, ws, ws_bytes, out_idx, who)) return rc;
+  if (rows > 0 && S > 0 && (!key_codes || !key_scale || !diag)) return fail(AEKV_ERR_VALUE, "%s: null key pointer", who);
+  return AEKV_OK;
+}
+
+int topk_quant_rows(const float* index_q, const float* index_weight, const void* key_codes, const float* key_scale,
+                    const float* diag, const int32_t* valid, int64_t B, int64_t T, int64_t S, int32_t IH, int32_t IC,
+                    int32_t bits, int32_t k, int32_t mode, void* ws, size_t ws_bytes, int64_t* out_idx,
+                    float* out_score, void* stream, const char* who) {
+  if (int rc = validate_quant_rows(index_q, index_weight, key_codes, key_scale, diag, B, T, S, IH, IC, bits, k, mode,
+                                   ws, ws_bytes, out_idx, who))
+    return rc;
+  const int64_t rows = B * T;
   if (rows == 0) return AEKV_OK;
-  if (S > 0 && (!key_codes || !key_scale || !diag)) return fail(AEKV_ERR_VALUE, "%s: null key pointer", who);
   if (use_specialised_codec() && mfma_indexer_supported(IH, IC, k, S))
     return launch_mfma_indexer(index_q, index_weight, key_codes, key_scale, diag, valid, rows, T, S, IH, IC, bits, k,
                                mode, ws, out_idx, out_score, as_stream(stream), who);
@@ -444,6 +457,72 @@ extern "C" int aekv_csa_indexer_topk_quant(const float* index_q, const float* in
                                            void* stream) {
   return topk_quant_rows(index_q, index_weight, key_codes, key_scale, diag, valid, B, 1, S, IH, IC, bits, k, mode, ws,
                          ws_bytes, out_idx, out_score, stream, "aekv_csa_indexer_topk_quant");
+}
+
+// ---- allocation-free variant --------------------------------------------------------------
+// The workspace lives in a file-scope device array, one copy per GPU the library runs on, held
+// until the process ends.  In host code `scratch` names a host-side stand-in, so its device address
+// is looked up once per device (hipGetSymbolAddress with that device current) and only that
+// address is ever handed to kernels.  The kernels write every workspace word they later read
+// within the same call (order keys, slot maxima, per-chunk candidate counts), so nothing has to
+// be cleared between calls; calls that overlap on one GPU share the array and race.
+static __device__ __align__(256) unsigned char scratch[AEKV_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxScratchDevices] = {};
+
+int static_scratch(hipStream_t st, void** addr, const char* who) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(AEKV_ERR_HIP, "%s: hipGetDevice failed", who);
+  if (st) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(st, &sdev) != hipSuccess) return fail(AEKV_ERR_HIP, "%s: hipStreamGetDevice failed", who);
+    if (sdev != dev)
+      return fail(AEKV_ERR_VALUE, "%s: the stream belongs to device %d, the current device is %d", who,
+                  static_cast<int>(sdev), dev);
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) return fail(AEKV_ERR_UNSUPPORTED, "%s: device %d out of range", who, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(AEKV_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: HIP error %d (%s)", who, dev,
+                  static_cast<int>(e), hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return AEKV_OK;
+}
+
+}  // namespace
+
+extern "C" int aekv_csa_indexer_topk_quant_noalloc(const float* index_q, const float* index_weight,
+                                                   const void* key_codes, const float* key_scale, const float* diag,
+                                                   const int32_t* valid, int64_t B, int64_t S, int32_t IH, int32_t IC,
+                                                   int32_t bits, int32_t k, int32_t mode, int64_t* out_idx,
+                                                   float* out_score, void* stream) {
+  const char* who = "aekv_csa_indexer_topk_quant_noalloc";
+  // the workspace entry point's argument checks first, with the workspace check deferred (no HIP call)
+  void* const placeholder = reinterpret_cast<void*>(static_cast<uintptr_t>(256));
+  if (int rc = validate_quant_rows(index_q, index_weight, key_codes, key_scale, diag, B, 1, S, IH, IC, bits, k, mode,
+                                   placeholder, SIZE_MAX, out_idx, who))
+    return rc;
+  if (B == 0) return AEKV_OK;
+  const size_t need = aekv_csa_indexer_workspace_size(B, S, k);
+  if (need > AEKV_STATIC_SCRATCH_BYTES)
+    return fail(AEKV_ERR_UNSUPPORTED,
+                "%s: B=%lld S=%lld k=%d needs %zu bytes of scratch, more than the static %zu bytes; use "
+                "aekv_csa_indexer_topk_quant with a caller workspace",
+                who, static_cast<long long>(B), static_cast<long long>(S), k, need,
+                static_cast<size_t>(AEKV_STATIC_SCRATCH_BYTES));
+  void* ws = nullptr;
+  if (int rc = static_scratch(as_stream(stream), &ws, who)) return rc;
+  return topk_quant_rows(index_q, index_weight, key_codes, key_scale, diag, valid, B, 1, S, IH, IC, bits, k, mode, ws,
+                         AEKV_STATIC_SCRATCH_BYTES, out_idx, out_score, stream, who);
 }
 
 extern "C" int aekv_csa_prefill_indexer_topk_quant(const float* index_q, const float* index_weight,

@@ -125,6 +125,22 @@ int aekv_csa_indexer_topk_quant(const float* index_q, const float* index_weight,
                                 int32_t bits, int32_t k, int32_t mode, void* ws, size_t ws_bytes,
                                 int64_t* out_idx, float* out_score, void* stream);
 
+/* Allocation-free variant of aekv_csa_indexer_topk_quant (same arguments and results, no ws/ws_bytes).
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its scratch is a static
+ * device array of AEKV_STATIC_SCRATCH_BYTES in the library, one per GPU, held until the process ends;
+ * the first call on a device looks up its address (the current device must be the stream's).
+ * Launches whose workspace, aekv_csa_indexer_workspace_size(B, S, k), exceeds it return
+ * AEKV_ERR_UNSUPPORTED (cfg5, B = 64 x S = 65536, needs 17.8 MB).  It calls no allocating routine.
+ * Every call on one GPU shares the array: calls that overlap on that GPU (other streams, other
+ * threads) race and must be serialised by the caller. */
+#define AEKV_STATIC_SCRATCH_BYTES ((size_t)32 << 20)
+int aekv_csa_indexer_topk_quant_noalloc(const float* index_q, const float* index_weight,
+                                        const void* key_codes, const float* key_scale, const float* diag,
+                                        const int32_t* valid, int64_t B, int64_t S, int32_t IH, int32_t IC,
+                                        int32_t bits, int32_t k, int32_t mode, int64_t* out_idx,
+                                        float* out_score, void* stream);
+
 /* Chunked-prefill variant: T targets per sequence (modeling.py:496-534, the per-target indexer of
  * _forward_tiled_prefill).  index_q [B,T,IH,IC], index_weight [B,T,IH], valid [B,T] (target t of
  * row b scores blocks j < valid[b,t] of key row b: its causally visible blocks), out_idx
