@@ -227,14 +227,16 @@ def make_csa_inputs(dev, B, S, bits, seed, outliers):
 
 
 def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
-    from aetherkv.decode import attention_workspace, csa_indexer_topk_quant, indexer_workspace, quant_sink_attention
+    from aetherkv.decode import (attention_workspace, csa_decode_step, csa_indexer_topk_quant, decode_workspace,
+                                 indexer_workspace, quant_sink_attention)
 
     log(f"{name}: CSA decode B={B} S={S} {bits}-bit")
     inp = make_csa_inputs(dev, B, S, bits, seed, outliers)
     k = 256
-    H, D = 12, 128
+    H, D, W = 12, 128, 128
     ws_i = indexer_workspace(B, S, k, dev)
-    ws_a = attention_workspace(B, H, D, k, 128, dev)
+    ws_a = attention_workspace(B, H, D, k, W, dev)
+    ws_s = decode_workspace(B, S, k, H, D, W, dev)
     idx = torch.empty((B, k), dtype=torch.int64, device=dev)
     out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
     pq = inp["pq"]
@@ -247,12 +249,19 @@ def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
         quant_sink_attention(inp["q"], inp["kv_codes"], inp["kv_scale"], idx, inp["win"], inp["sink"], D ** -0.5,
                              quant=pq, workspace=ws_a, out=out)
 
-    def step():
+    def step_separate():
         index_only()
         attn_only()
 
+    def step():
+        # the decode step as one call: score kernel, then selection + attention fused per row
+        csa_decode_step(inp["q"], inp["index_q"], inp["index_w"], inp["ix_codes"], inp["ix_scale"], inp["kv_codes"],
+                        inp["kv_scale"], inp["win"], inp["sink"], D ** -0.5, k, kv_quant=pq, index_quant=pq,
+                        workspace=ws_s, out_idx=idx, out=out)
+
     ms_eager = timed(step, args.steps, args.warmup)
     ms = timed_graph(step, args.steps, args.warmup)
+    ms_sep = timed_graph(step_separate, args.steps, args.warmup)
     ms_i = timed_graph(index_only, args.steps, args.warmup)
     ms_a = timed_graph(attn_only, args.steps, args.warmup)
     row_bytes = (D if bits == 8 else D // 2) + 4
@@ -260,10 +269,13 @@ def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
     step_bytes = B * (S * ix_bytes + k * row_bytes + 128 * D * 2 + H * D * 2 * 2)
     res = {"B": B, "S": S, "bits": bits, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / ms * 1e3, 1),
            "ms_per_step_eager": round(ms_eager, 5), "timing": f"HIP graph of {GRAPH_STEPS} steps, replayed",
-           "indexer_ms": round(ms_i, 5), "attention_ms": round(ms_a, 5), "bytes_per_step": step_bytes,
-           "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    log(f"{name}: {ms * 1e3:.1f} us/step ({ms_i * 1e3:.1f} indexer + {ms_a * 1e3:.1f} attention; graph replay; "
-        f"eager {ms_eager * 1e3:.1f}) -> {res['tokens_per_s']:.0f} tok/s, {res['hbm_frac'] * 100:.1f}% of HBM peak")
+           "step": "aekv_csa_decode_quant: score kernel + fused select/attention kernel",
+           "ms_per_step_separate_kernels": round(ms_sep, 5),
+           "separate_indexer_ms": round(ms_i, 5), "separate_attention_ms": round(ms_a, 5),
+           "bytes_per_step": step_bytes, "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    log(f"{name}: {ms * 1e3:.1f} us/step fused (graph replay; eager {ms_eager * 1e3:.1f}); separate kernels "
+        f"{ms_sep * 1e3:.1f} ({ms_i * 1e3:.1f} indexer + {ms_a * 1e3:.1f} attention) -> {res['tokens_per_s']:.0f} "
+        f"tok/s, {res['hbm_frac'] * 100:.1f}% of HBM peak")
     if cpu_rows:
         res["cpu_baseline"] = bench_cpu_csa(inp, cpu_rows, name, bits)
     del inp

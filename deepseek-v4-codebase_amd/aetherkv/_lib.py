@@ -34,6 +34,7 @@ SYMBOLS = (
     "aekv_quant_sink_attention", "aekv_hca_compress", "aekv_tiled_prefill_attention", "aekv_set_generic_kernels",
     "aekv_emit_block", "aekv_csa_prefill_indexer_topk_quant", "aekv_quant_prefill_workspace_size",
     "aekv_quant_prefill_attention", "aekv_rope_rmsnorm", "aekv_csa_indexer_topk_quant_noalloc",
+    "aekv_csa_decode_workspace_size", "aekv_csa_decode_quant",
 )
 
 # size of the static device scratch behind aekv_csa_indexer_topk_quant_noalloc (AEKV_STATIC_SCRATCH_BYTES)
@@ -83,6 +84,9 @@ def lib() -> ctypes.CDLL:
         "aekv_emit_block": ([P, P, P, I64_, I64_, I32_, I32_, P, P, P, F, I32_, P, P, P, I64_, P, P], ctypes.c_int),
         "aekv_csa_indexer_topk_quant_noalloc": ([P, P, P, P, P, P, I64_, I64_, I32_, I32_, I32_, I32_, I32_, P, P, P],
                                                 ctypes.c_int),
+        "aekv_csa_decode_workspace_size": ([I64_, I64_, I32_, I64_, I64_, I64_], SZ),
+        "aekv_csa_decode_quant": ([P, P, P, P, P, P, I64_, I64_, I32_, I32_, I32_, I32_, I32_, P, P, P, P, P, P, I64_,
+                                   I64_, I64_, I32_, F, P, SZ, P, P, P, P], ctypes.c_int),
         "aekv_csa_prefill_indexer_topk_quant": (
             [P, P, P, P, P, P, I64_, I64_, I64_, I32_, I32_, I32_, I32_, I32_, P, SZ, P, P, P], ctypes.c_int),
         "aekv_quant_prefill_workspace_size": ([I64_, I64_, I64_, I64_, I64_], SZ),

@@ -26,7 +26,7 @@ from typing import Dict, Optional, Tuple
 import torch
 
 from . import _lib
-from .decode import csa_indexer_topk_quant, quant_sink_attention
+from .decode import csa_decode_step, csa_indexer_topk_quant, quant_sink_attention
 from .turbo_quant import PolarQuant
 
 _COUNTERS = ("token_count", "loaded_prefix_tokens")
@@ -384,13 +384,18 @@ def csa_decode_ring(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.
     if index_ring.n != kv_ring.n:
         raise RuntimeError(f"index ring holds {index_ring.n} blocks, kv ring {kv_ring.n}")
     k = min(int(top_k), kv_ring.n)
+    icodes, iscale = index_ring.storage
+    codes, scale = kv_ring.storage
+    if k > 0 and index_workspace is None and attention_workspace is None and icodes.size(1) == codes.size(1):
+        # both rings hold the same capacity: one call, selection and attention fused per row
+        return csa_decode_step(q, index_q, index_weight, icodes, iscale, codes, scale, window, sink, softmax_scale, k,
+                               kv_quant=kv_ring.quant, index_quant=index_ring.quant, valid=index_ring.visible(),
+                               mode=mode, out_idx=out_idx, out=out)
     if k == 0:
         idx = torch.empty((q.size(0), 0), dtype=torch.int64, device=q.device)
     else:
-        icodes, iscale = index_ring.storage
         idx = csa_indexer_topk_quant(index_q, index_weight, icodes, iscale, k, quant=index_ring.quant,
                                      valid=index_ring.visible(), mode=mode, workspace=index_workspace, out=out_idx)
-    codes, scale = kv_ring.storage
     o = quant_sink_attention(q, codes, scale, idx, window, sink, softmax_scale, quant=kv_ring.quant,
                              workspace=attention_workspace, out=out)
     return o, idx

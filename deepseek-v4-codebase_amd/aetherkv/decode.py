@@ -139,6 +139,86 @@ def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tens
     return out.view(B, 1, H, D) if squeeze else out
 
 
+def decode_workspace(B: int, S: int, k: int, H: int, D: int, W: int, device) -> torch.Tensor:
+    """Workspace of csa_decode_step (the indexer's and the attention's)."""
+    return torch.empty(_lib.lib().aekv_csa_decode_workspace_size(B, S, k, H, D, W), dtype=torch.uint8, device=device)
+
+
+def csa_decode_step(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.Tensor, index_codes: torch.Tensor,
+                    index_scale: torch.Tensor, kv_codes: torch.Tensor, kv_scale: torch.Tensor,
+                    window: Optional[torch.Tensor], sink: torch.Tensor, softmax_scale: float, k: int, *,
+                    kv_quant: PolarQuant, index_quant: PolarQuant, valid: Optional[torch.Tensor] = None,
+                    mode: str = "softplus", return_scores: bool = False, workspace: Optional[torch.Tensor] = None,
+                    out_idx: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+    """The CSA decode step in one call (aekv_csa_decode_quant): the indexer's top-k of the visible
+    index keys, then the sink attention over those blocks and the window.  Same results as
+    csa_indexer_topk_quant followed by quant_sink_attention; the per-row selection and attention run
+    in one kernel where the matrix-core kernels apply.  Index codes [B, S, IC(/2)] and KV codes
+    [B, S, D(/2)] cover the same S blocks.  Returns (out like q, idx [B, k]) or, with return_scores,
+    (out, idx, scores [B, k])."""
+    _lib.require_device("q", q, index_q, index_weight, index_codes, index_scale, kv_codes, kv_scale, window, sink,
+                        valid)
+    if mode not in _lib.INDEX_MODES:
+        raise ValueError(f"mode must be one of {sorted(_lib.INDEX_MODES)}, got {mode!r}")
+    if q.dtype != torch.bfloat16:
+        raise RuntimeError(f"q must be bfloat16, got {q.dtype}")
+    squeeze = q.dim() == 4
+    if squeeze and q.size(1) != 1:
+        raise RuntimeError("csa_decode_step expects one target token per row")
+    q3 = (q.reshape(q.size(0), q.size(-2), q.size(-1)) if squeeze else q).contiguous()
+    B, H, D = q3.shape
+    IB, IH, IC = index_q.shape
+    S = kv_codes.size(1)
+    if index_codes.size(1) != S or IB != B:
+        raise RuntimeError(f"index codes {tuple(index_codes.shape)} and KV codes {tuple(kv_codes.shape)} must cover "
+                           f"the same B rows and S blocks")
+    for name, quant, codes, dim in (("index", index_quant, index_codes, IC), ("KV", kv_quant, kv_codes, D)):
+        want = torch.int8 if quant.bits == 8 else torch.uint8
+        if codes.dtype != want:
+            raise RuntimeError(f"{quant.bits}-bit {name} codes must be {want}, got {codes.dtype}")
+        if codes.size(-1) * (1 if quant.bits == 8 else 2) != dim or codes.size(0) != B:
+            raise RuntimeError(f"{name} codes shape {tuple(codes.shape)} does not match head dim {dim} and batch {B}")
+    if window is not None and window.numel() > 0:
+        if window.dtype != torch.bfloat16 or window.dim() != 3 or window.size(0) != B or window.size(2) != D:
+            raise RuntimeError(f"window must be bf16 [B, W, D], got {window.dtype} {tuple(window.shape)}")
+        win = _lib.aligned(window, 16)
+        W = win.size(1)
+    else:
+        win, W = None, 0
+    sk = sink.to(torch.float32).reshape(-1).contiguous()
+    if sk.numel() == 1:
+        sk = sk.expand(H).contiguous()
+    if sk.numel() != H:
+        raise RuntimeError("sink must be a scalar or a [num_heads] tensor")
+    iq = index_q.to(torch.float32).contiguous()
+    iw = index_weight.to(torch.float32).contiguous()
+    ic = index_codes.contiguous()
+    isc = _scale_2d(index_scale, B, S)
+    kc = _lib.aligned(kv_codes, 16)
+    ksc = _scale_2d(kv_scale, B, S)
+    v = None if valid is None else valid.to(torch.int32).contiguous()
+    dev = q.device
+    idiag = index_quant._diag(IC, dev)
+    kdiag = kv_quant._diag(D, dev)
+    L = _lib.lib()
+    if out_idx is None:
+        out_idx = torch.empty((B, k), dtype=torch.int64, device=dev)
+    scores = torch.empty((B, k), dtype=torch.float32, device=dev) if return_scores else None
+    if out is None:
+        out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
+    if workspace is None:
+        workspace = decode_workspace(B, S, k, H, D, W, dev)
+    with torch.cuda.device(dev):
+        _lib.check(L.aekv_csa_decode_quant(
+            _lib.ptr(iq), _lib.ptr(iw), _lib.ptr(ic), _lib.ptr(isc), _lib.ptr(idiag), _lib.ptr(v), B, S, IH, IC,
+            index_quant.bits, int(k), _lib.INDEX_MODES[mode], _lib.ptr(q3), _lib.ptr(kc), _lib.ptr(ksc), _lib.ptr(win),
+            _lib.ptr(sk), _lib.ptr(kdiag), H, D, W, kv_quant.bits, float(softmax_scale), _lib.ptr(workspace),
+            workspace.numel(), _lib.ptr(out_idx), _lib.ptr(scores), _lib.ptr(out), _lib.stream_of(q)),
+            "aekv_csa_decode_quant")
+    o = out.view(B, 1, H, D) if squeeze else out
+    return (o, out_idx, scores) if return_scores else (o, out_idx)
+
+
 def csa_decode(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.Tensor, index_codes: torch.Tensor,
                index_scale: torch.Tensor, kv_codes: torch.Tensor, kv_scale: torch.Tensor,
                window: Optional[torch.Tensor], sink: torch.Tensor, softmax_scale: float, *, kv_quant: PolarQuant,
@@ -151,10 +231,8 @@ def csa_decode(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.Tenso
     if k == 0:
         return quant_sink_attention(q, kv_codes, kv_scale, kv_codes.new_zeros((q.size(0), 0), dtype=torch.int64),
                                     window, sink, softmax_scale, quant=kv_quant), None
-    idx = csa_indexer_topk_quant(index_q, index_weight, index_codes, index_scale, k, quant=index_quant, valid=valid,
-                                 mode=mode)
-    out = quant_sink_attention(q, kv_codes, kv_scale, idx, window, sink, softmax_scale, quant=kv_quant)
-    return out, idx
+    return csa_decode_step(q, index_q, index_weight, index_codes, index_scale, kv_codes, kv_scale, window, sink,
+                           softmax_scale, k, kv_quant=kv_quant, index_quant=index_quant, valid=valid, mode=mode)
 
 
 def hca_decode(q: torch.Tensor, kv_codes: torch.Tensor, kv_scale: torch.Tensor, window: Optional[torch.Tensor],

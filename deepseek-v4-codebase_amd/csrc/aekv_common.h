@@ -34,6 +34,11 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
                         const int32_t* valid, int64_t B, int64_t T, int64_t S, int IH, int IC, int bits, int k,
                         int mode, void* ws, int64_t* out_idx, float* out_score, hipStream_t st, const char* who);
 bool use_specialised_codec();
+// Host-side argument checks of the quantised-key indexer for B * T rows (csa_indexer.hip).
+int validate_quant_rows(const float* index_q, const float* index_weight, const void* key_codes,
+                        const float* key_scale, const float* diag, int64_t B, int64_t T, int64_t S, int32_t IH,
+                        int32_t IC, int32_t bits, int32_t k, int32_t mode, void* ws, size_t ws_bytes,
+                        int64_t* out_idx, const char* who);
 // Matrix-core decode attention for head_dim 128 (quant_attn_mfma.hip).
 bool quant_attn_mfma_supported(int64_t H, int64_t D);
 bool quant_attn_mfma_fits(int64_t rows, int64_t n_src);  // grid and split-combine limits

@@ -402,11 +402,8 @@ extern "C" int aekv_csa_indexer_topk(const float* index_q, const float* index_kv
   return launch_indexer(kKeyF32, a, B, S, ws, out_idx, out_score, as_stream(stream), who);
 }
 
-namespace {
-
-// rows = B * T query rows; row r scores the codes of key row r / T
-// host-side checks of a quantised-key launch (no HIP call)
-int validate_quant_rows(const float* index_q, const float* index_weight, const void* key_codes,
+// host-side checks of a quantised-key launch of B * T rows (no HIP call)
+int aekv::validate_quant_rows(const float* index_q, const float* index_weight, const void* key_codes,
                         const float* key_scale, const float* diag, int64_t B, int64_t T, int64_t S, int32_t IH,
                         int32_t IC, int32_t bits, int32_t k, int32_t mode, void* ws, size_t ws_bytes,
                         int64_t* out_idx, const char* who) {
@@ -421,6 +418,9 @@ int validate_quant_rows(const float* index_q, const float* index_weight, const v
   return AEKV_OK;
 }
 
+namespace {
+
+// rows = B * T query rows; row r scores the codes of key row r / T
 int topk_quant_rows(const float* index_q, const float* index_weight, const void* key_codes, const float* key_scale,
                     const float* diag, const int32_t* valid, int64_t B, int64_t T, int64_t S, int32_t IH, int32_t IC,
                     int32_t bits, int32_t k, int32_t mode, void* ws, size_t ws_bytes, int64_t* out_idx,

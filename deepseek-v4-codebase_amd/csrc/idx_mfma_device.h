@@ -1,0 +1,860 @@
+// CSA lightning indexer over TurboQuant-coded index keys on the gfx950 matrix cores, with an
+// exact radix top-k.
+//
+// Reference: aether_2b/modeling.py:604-616 and aether_2b/serving.py:606-621 (score rules, top-k);
+// the keys are PolarQuant codes (turbo_quant.py:127-211).
+//
+// Scoring.  q.k_j = scale_j * (q~ . codes_j) with q~ = WHT(diag * q) (the WHT is orthogonal and
+// symmetric).  Per head, q~ is split into four int8 digits with a common power-of-two step S_h:
+//   q~ = S_h * (d0 + 2^-7 d1 + 2^-14 d2 + 2^-21 d3) + r,   |d_i| <= 64,   |r| <= S_h * 2^-22,
+// and v_mfma_i32_16x16x64_i8 computes the exact integer dots I_i = d_i . codes_j for 16 keys at a
+// time (A rows = 4 heads x 4 digits; B columns = keys; 4-bit codes enter as 16*code, the nibble
+// shifted to the top of its byte).  The 16x16 result leaves each lane with the four digit dots of
+// one (head, key); they are combined in fp32 with the head weight folded in, clamped (relu), summed
+// over heads across lane groups and multiplied by scale_j.  The only approximation is r (relative
+// ~2^-27 of max|q~_h|) and three fp32 roundings, i.e. fp32-level scores.
+//
+// Kernels (one stream, in order):
+//   score  (wide grid)  rotates the row's query and splits the digits in LDS (per workgroup),
+//          scores every visible key, stores its order-preserving uint32 key and the max of every
+//          16-key slot.
+//   final  (one workgroup per row)  bounds the k-th largest key from below by the k-th largest
+//          slot max (a histogram of the slot maxima in 1/128-binade bins below the row's largest),
+//          reads only the slots that can hold a top-k key and keeps their keys above the bound.
+//          Up to 1024 candidates (the usual case: a few hundred) are sorted outright, 64 per wave
+//          in registers, the runs placed by binary search; more go through three LDS radix levels
+//          (keys > T and the lowest-index keys == T, placed by rank under (key desc, index asc)).
+//          If the candidates overflow LDS (many equal keys), the levels run over all of the row's
+//          stored keys, read in index order.
+// Both routes return the top-k under the total order (score desc, index asc).
+//
+// The select body (select_row) is shared by the select kernel and the fused CSA decode kernel,
+// which continues with the row's attention in the same workgroup.
+#pragma once
+
+#include <algorithm>
+
+#include "aekv_common.h"
+
+namespace aekv {
+namespace idx {
+
+constexpr int kThreads = 256;
+constexpr int kSelThreads = 1024;
+constexpr int kHistBins = 4096;      // slot-max histogram bins (key >> 16 below the row maximum)
+constexpr int kCandCap = 4096;       // candidates a row's workgroup collects in LDS (fast route)
+constexpr int kMaxMfmaK = 1024;
+constexpr int kMaxNrb = 4;           // row blocks of 4 heads (IH <= 16)
+constexpr int64_t kMaxKeys = int64_t(1) << 30;
+constexpr int kScoreTT = 4;          // prefill rows sharing each key group in the score kernel
+constexpr int64_t kScoreTargetWG = 2048;  // score workgroups the launch aims for
+
+typedef __attribute__((ext_vector_type(4))) int i32x4_t;
+
+__device__ __forceinline__ float softplus_f32(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+__device__ __forceinline__ int mbcnt64(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+}
+
+// Reserves v (< 2^NB) slots per active lane from the LDS counter *cnt with one atomic per wave
+// (per-lane atomics on one LDS address serialise) and returns the lane's first slot.  The
+// exclusive prefix sum over the active lanes comes from NB ballots.
+template <int NB>
+__device__ __forceinline__ uint32_t wave_reserve(uint32_t* cnt, uint32_t v) {
+  uint32_t pre = 0u, tot = 0u;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const uint64_t m = __builtin_amdgcn_ballot_w64(((v >> b) & 1u) != 0u);
+    pre += static_cast<uint32_t>(mbcnt64(m)) << b;
+    tot += static_cast<uint32_t>(__builtin_popcountll(m)) << b;
+  }
+  uint32_t base = 0u;
+  if (mbcnt64(__builtin_amdgcn_ballot_w64(true)) == 0 && tot != 0u) base = atomicAdd(cnt, tot);
+  return __builtin_amdgcn_readfirstlane(base) + pre;
+}
+
+struct MfmaIdxArgs {
+  const float* q;        // [B, IH, IC]
+  const float* w;        // [B, IH]
+  const uint8_t* codes;  // [B, S, IC or IC/2]
+  const float* kscale;   // [B, S]
+  const float* diag;     // [IC]
+  const int32_t* valid;  // [B] or null
+  int64_t S;
+  int64_t T;             // rows per key row: row b scores the keys of key row b / T
+  int IH, k, mode;
+  int gpw;               // slot groups per wave in the score kernel
+  float wscale;
+  uint32_t* keys;        // [B][ks]                   order keys of visible keys
+  int64_t ks;            // key row stride: S rounded up to a multiple of 16 (whole slots)
+  uint32_t* smax;        // [B][ms]                   max order key of each 16-key slot
+  int64_t ms;            // slot-max row stride: ceil(S / 16) rounded up to a multiple of 4
+};
+
+struct WsLayout {
+  size_t keys, smax, total;
+};
+
+inline WsLayout layout(int64_t B, int64_t S) {
+  WsLayout l{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += align_up(bytes, 256);
+    return at;
+  };
+  l.keys = take(static_cast<size_t>(B) * static_cast<size_t>(align_up(static_cast<size_t>(S), 16)) * 4);
+  l.smax = take(static_cast<size_t>(B) * align_up((static_cast<size_t>(S) + 15) / 16, 4) * 4);
+  l.total = o;
+  return l;
+}
+
+__device__ __forceinline__ int64_t visible(const MfmaIdxArgs& a, int b) {
+  return a.valid ? min<int64_t>(a.S, max(0, a.valid[b])) : a.S;
+}
+
+// digit position -> index c of the key element for lane group g, byte position p of k-step ks
+template <int BITS>
+__device__ __forceinline__ int cmap(int ks, int g, int p) {
+  if constexpr (BITS == 8) {
+    return 64 * ks + 16 * g + p;
+  } else {
+    // the lane loads bytes 8g..8g+7 of the 32-byte k-step: dwords (lo nibbles of bytes 0-3,
+    // hi nibbles of bytes 0-3, lo of 4-7, hi of 4-7)
+    const int q4 = p >> 2, r = p & 3;
+    return 64 * ks + 16 * g + 8 * (q4 >> 1) + 2 * r + (q4 & 1);
+  }
+}
+
+// Sum over the four 16-lane groups ("rows") of t[q], delivered to row q: a reduce-scatter with
+// three permlane swaps.  permlane16_swap(a, b) exchanges the odd rows of a with the even rows of b,
+// so a' + b' holds a's pair sums (rows 0+1, 2+3) in rows 0 and 2 and b's in rows 1 and 3;
+// permlane32_swap(u, w) exchanges u's upper half with w's lower half, so u' + w' holds u's half
+// sums in rows 0-1 and w's in rows 2-3.  Every row ends with (t[q]_0 + t[q]_1) + (t[q]_2 + t[q]_3)
+// for q = its row: the pairing of a butterfly sum, so the same fp32 value.  (The swap results are
+// copied to scalars before the bit casts: hipcc lowers __builtin_bit_cast of element 1 of the
+// builtin's result vector as element 0.)
+__device__ __forceinline__ float row_sums_scatter(const float (&t)[4]) {
+  auto sw16 = [](float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                    false, false);
+    const uint32_t x0 = r[0], x1 = r[1];
+    return __builtin_bit_cast(float, x0) + __builtin_bit_cast(float, x1);
+  };
+  const float u = sw16(t[0], t[1]), w = sw16(t[2], t[3]);
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, u), __builtin_bit_cast(uint32_t, w),
+                                                  false, false);
+  const uint32_t x0 = r[0], x1 = r[1];
+  return __builtin_bit_cast(float, x0) + __builtin_bit_cast(float, x1);
+}
+
+// 64-bit lane exchange with partner lane ^ j (j a power of two below 64, constant after unrolling).
+template <int HL>
+__device__ __forceinline__ uint32_t max_xor_u32(uint32_t v) {
+  const uint32_t o = __builtin_bit_cast(uint32_t, xor_lane<HL>(__builtin_bit_cast(float, v)));
+  return v > o ? v : o;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max_xor_u32<1>(v);
+  v = max_xor_u32<2>(v);
+  v = max_xor_u32<4>(v);
+  v = max_xor_u32<8>(v);
+  v = max_xor_u32<16>(v);
+  return max_xor_u32<32>(v);
+}
+
+__device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v, int j) {
+  float lo = __builtin_bit_cast(float, static_cast<uint32_t>(v));
+  float hi = __builtin_bit_cast(float, static_cast<uint32_t>(v >> 32));
+  switch (j) {
+    case 1: lo = xor_lane<1>(lo); hi = xor_lane<1>(hi); break;
+    case 2: lo = xor_lane<2>(lo); hi = xor_lane<2>(hi); break;
+    case 4: lo = xor_lane<4>(lo); hi = xor_lane<4>(hi); break;
+    case 8: lo = xor_lane<8>(lo); hi = xor_lane<8>(hi); break;
+    case 16: lo = xor_lane<16>(lo); hi = xor_lane<16>(hi); break;
+    default: lo = xor_lane<32>(lo); hi = xor_lane<32>(hi); break;
+  }
+  return (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, hi)) << 32) | __builtin_bit_cast(uint32_t, lo);
+}
+
+// Threshold search over a histogram: the largest bin t with sum_{u >= t} h[u] >= need, and
+// above = sum_{u > t} h[u] (1 <= need <= sum of all bins).  Thread `tid` of NT owns the PER
+// contiguous bins [PER*tid, PER*tid + PER), loaded as 16-byte vectors (global or LDS).
+template <int PER>
+__device__ __forceinline__ void load_bins(const uint32_t* h, int tid, uint32_t (&v)[PER]) {
+  static_assert(PER % 4 == 0, "bins are loaded 4 at a time");
+  const uint4* p = reinterpret_cast<const uint4*>(h + PER * tid);
+#pragma unroll
+  for (int i = 0; i < PER / 4; ++i) {
+    const uint4 x = p[i];
+    v[4 * i] = x.x;
+    v[4 * i + 1] = x.y;
+    v[4 * i + 2] = x.z;
+    v[4 * i + 3] = x.w;
+  }
+}
+
+// Inclusive suffix sum over the lanes of a wave (lane 63 holds the highest bins).
+__device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_down(x, off, 64);
+    if (lane + off < 64) x += y;
+  }
+  return x;
+}
+
+// The lane whose bins hold the crossing walks them from the top.
+template <int PER>
+__device__ __forceinline__ void walk_bins(const uint32_t (&v)[PER], int tid, uint32_t excl, uint32_t need,
+                                          uint32_t* s_res) {
+  uint32_t c = excl;
+  bool done = false;
+#pragma unroll
+  for (int i = PER - 1; i >= 0; --i) {
+    if (!done && c + v[i] >= need) {
+      s_res[0] = static_cast<uint32_t>(PER * tid + i);
+      s_res[1] = c;
+      s_res[2] = v[i];
+      done = true;
+    }
+    c += v[i];
+  }
+}
+
+// Block-wide (NT threads, NT * PER bins).  Every thread returns the result (and the count of
+// bin t).  s_tot holds NT/64 words, s_res 3; both may be reused after the call.
+template <int NT, int PER>
+__device__ void block_threshold(const uint32_t* h, uint32_t need, uint32_t* s_tot, uint32_t* s_res, uint32_t& t_out,
+                                uint32_t& above_out, uint32_t& count_out) {
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t v[PER];
+  load_bins<PER>(h, tid, v);
+  uint32_t sum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) sum += v[i];
+  const uint32_t suf = wave_suffix_sum(sum);
+  if (lane == 0) s_tot[wv] = suf;
+  __syncthreads();
+  uint32_t higher = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < NW; ++w2) higher += w2 > wv ? s_tot[w2] : 0u;
+  const uint32_t incl = higher + suf, excl = incl - sum;
+  if (excl < need && incl >= need) walk_bins<PER>(v, tid, excl, need, s_res);  // exactly one thread
+  __syncthreads();
+  t_out = s_res[0];
+  above_out = s_res[1];
+  count_out = s_res[2];
+  __syncthreads();
+}
+
+// Wave-only variant over 64 * PER bins (called by one whole wave); the result lands in s_res[0..2].
+template <int PER>
+__device__ void wave_threshold(const uint32_t* h, uint32_t need, uint32_t* s_res) {
+  const int lane = threadIdx.x & 63;
+  uint32_t v[PER];
+  load_bins<PER>(h, lane, v);
+  uint32_t sum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) sum += v[i];
+  const uint32_t incl = wave_suffix_sum(sum), excl = incl - sum;
+  if (excl < need && incl >= need) walk_bins<PER>(v, lane, excl, need, s_res);
+}
+
+// ---- query side: rotation, digits, A fragments (once per workgroup, in LDS) --------------------
+// Wave wv rotates heads wv, wv+4, .. (< 4*NRB); lane l holds elements l + 64e of the head.
+// q~ = _wht(diag * q): stages h = 1..32 pair lanes (xor_lane), stage 64 pairs e = 0 and 1.  Then
+// every lane assembles its A fragments (4 heads x 4 digits per row block) and combine constants.
+template <int BITS, int IC, int NRB>
+__device__ __forceinline__ void query_fragments(const MfmaIdxArgs& a, int b, int8_t (*dig)[16][IC], float (*hf)[4],
+                                                float (*hb)[2], i32x4_t (&A)[NRB][IC / 64], float (&f)[NRB][4],
+                                                float (&lo)[NRB], float (&hi)[NRB]) {
+  constexpr int KS = IC / 64;
+  constexpr int EPL = IC / 64;
+  const int IH = a.IH;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
+  for (int h = wv; h < 4 * NRB; h += 4) {
+    float v[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const int c = lane + 64 * e;
+      v[e] = h < IH ? a.q[(static_cast<int64_t>(b) * IH + h) * IC + c] * a.diag[c] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float x = v[e];
+      x = fmaf(x, (lane & 1) ? -1.0f : 1.0f, xor_lane<1>(x));    // lower lane: x + p, upper: p - x
+      x = fmaf(x, (lane & 2) ? -1.0f : 1.0f, xor_lane<2>(x));
+      x = fmaf(x, (lane & 4) ? -1.0f : 1.0f, xor_lane<4>(x));
+      x = fmaf(x, (lane & 8) ? -1.0f : 1.0f, xor_lane<8>(x));
+      x = fmaf(x, (lane & 16) ? -1.0f : 1.0f, xor_lane<16>(x));
+      x = fmaf(x, (lane & 32) ? -1.0f : 1.0f, xor_lane<32>(x));
+      v[e] = x;
+    }
+    if constexpr (EPL == 2) {
+      const float x = v[0], y = v[1];
+      v[0] = x + y;
+      v[1] = x - y;
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      v[e] = v[e] * a.wscale;
+      mx = fmaxf(mx, fabsf(v[e]));
+    }
+    mx = wave_max(mx);
+    // step S_h = 2^(e-6) from max|q~_h| = m * 2^e (m in [0.5, 1)); e >= -90 keeps every digit
+    // step and its reciprocal normal
+    int ex = 0;
+    (void)frexpf(mx, &ex);
+    ex = ex < -90 ? -90 : ex;
+    const float step = mx > 0.0f ? ldexpf(1.0f, ex - 6) : 1.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float r = v[e];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const float sd = ldexpf(step, -7 * d);
+        const float di = rintf(r * (1.0f / sd));  // exact: 1/sd is a power of two
+        r = fmaf(-di, sd, r);                      // exact residual
+        dig[d][h][lane + 64 * e] = static_cast<int8_t>(di);
+      }
+    }
+    if (lane == 0) {
+      float wa = 0.0f, lw = -__builtin_inff(), hw = __builtin_inff();
+      if (h < IH) {
+        const float wr = a.w[static_cast<int64_t>(b) * IH + h];
+        if (a.mode == AEKV_IDX_SOFTPLUS) {
+          wa = softplus_f32(wr);
+          lw = 0.0f;
+        } else if (a.mode == AEKV_IDX_RAW) {
+          wa = wr;
+          if (wr >= 0.0f) lw = 0.0f; else hw = 0.0f;  // relu(dot)*w = clamp(dot*w) toward 0
+        } else {
+          wa = fmaxf(wr, 0.0f);                       // relu on the weight only
+        }
+      }
+      const float unit = BITS == 4 ? 1.0f / 16.0f : 1.0f;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) hf[h][d] = ldexpf(step, -7 * d) * unit * wa;
+      hb[h][0] = lw;
+      hb[h][1] = hw;
+    }
+  }
+  __syncthreads();
+  const int row = lane & 15;
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb) {
+    const int h = 4 * rb + (row >> 2), d = row & 3;  // A rows = 4 heads x 4 digits
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int dw = 0; dw < 4; ++dw) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int by = 0; by < 4; ++by) {
+          const int c = cmap<BITS>(ks, g, 4 * dw + by);
+          word |= (static_cast<uint32_t>(static_cast<uint8_t>(dig[d][h][c])) << (8 * by));
+        }
+        A[rb][ks][dw] = static_cast<int>(word);
+      }
+    }
+    const int ho = 4 * rb + g;  // output rows 4g..4g+3 = head 4rb+g, digits 0..3
+#pragma unroll
+    for (int d2 = 0; d2 < 4; ++d2) f[rb][d2] = hf[ho][d2];
+    lo[rb] = hb[ho][0];
+    hi[rb] = hb[ho][1];
+  }
+}
+
+// ---- score: keys -> order keys + the max of every 16-key slot ----------------------------------
+// A wave scores groups of SPW slots of 64 keys; lane l keeps key base + 64s + l of slot s.  All
+// loads of a group are issued before its matrix work.  With TT > 1 a workgroup scores TT rows
+// of the same key row (prefill targets of one sequence) against every key group it loads: the
+// codes and scales are read, and the integer B operand built, once for the TT rows.  Row
+// (sequence bs, target t) is bs * T + t; workgroup row y takes targets TT (y % ceil(T / TT)) + tt.
+// The register bound (at least 2 waves per SIMD, so at most 256 registers per lane) keeps the
+// matrix results in VGPRs: with the default 512 the compiler uses the AGPR form and moves every
+// result out with v_accvgpr_read.
+template <int BITS, int IC, int NRB, int TT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void
+idx_mfma_score_kernel(MfmaIdxArgs a) {
+  constexpr int KS = IC / 64;
+  constexpr int RB = BITS == 8 ? IC : IC / 2;        // code bytes per key
+  constexpr int SPW = RB <= 32 ? 4 : (RB <= 64 ? 2 : 1);
+  constexpr int LW = BITS == 8 ? 4 : 2;               // dwords per lane per k-step
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
+  const int64_t S = a.S;
+
+  // this workgroup's rows: TT targets of key row kr (rows past the sequence's T are not scored)
+  int64_t row[TT];
+  bool rok[TT];
+  int64_t kr;
+  if constexpr (TT == 1) {
+    row[0] = blockIdx.y;
+    rok[0] = true;
+    kr = row[0] / a.T;
+  } else {
+    const int64_t ngt = (a.T + TT - 1) / TT;
+    kr = blockIdx.y / ngt;
+    const int64_t t0 = (blockIdx.y % ngt) * TT;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      rok[tt] = t0 + tt < a.T;
+      row[tt] = kr * a.T + (rok[tt] ? t0 + tt : t0);
+    }
+  }
+  int64_t nv[TT], nv_max = 0;
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    nv[tt] = rok[tt] ? visible(a, static_cast<int>(row[tt])) : 0;
+    nv_max = max(nv_max, nv[tt]);
+  }
+
+  __shared__ int8_t dig[4][16][IC];
+  __shared__ float hf[16][4];  // per head: digit factors S * 2^-7d (/16 for 4-bit) * weight
+  __shared__ float hb[16][2];  // per head: clamp bounds
+  i32x4_t A[TT][NRB][KS];
+  float f[TT][NRB][4], lo[TT][NRB], hi[TT][NRB];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    if (tt > 0) __syncthreads();  // the previous row's fragments have been read out of LDS
+    query_fragments<BITS, IC, NRB>(a, static_cast<int>(row[tt]), dig, hf, hb, A[tt], f[tt], lo[tt], hi[tt]);
+  }
+
+  const uint8_t* crow = a.codes + kr * S * RB;
+  const float* srow = a.kscale + kr * S;
+  constexpr int64_t kGroupKeys = SPW * 64;
+  const int64_t wave_base = (static_cast<int64_t>(blockIdx.x) * 4 + wv) * a.gpw * kGroupKeys;
+#pragma unroll 1
+  for (int gi = 0; gi < a.gpw; ++gi) {
+    const int64_t kb = wave_base + gi * kGroupKeys;
+    if (kb >= nv_max) break;  // wave-uniform
+    uint32_t raw[SPW][4][KS][LW];
+    float scl[SPW];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+#pragma unroll
+      for (int tq = 0; tq < 4; ++tq) {
+        const int64_t j = kb + 64 * s + 16 * tq + (lane & 15);
+        const int64_t jr = j < nv_max ? j : 0;  // nv_max >= 1 here; keys past a row's count are dropped
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          if constexpr (BITS == 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(crow + jr * RB + 64 * ks + 16 * g);
+            raw[s][tq][ks][0] = v.x;
+            raw[s][tq][ks][1] = v.y;
+            raw[s][tq][ks][2] = v.z;
+            raw[s][tq][ks][3] = v.w;
+          } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(crow + jr * RB + 32 * ks + 8 * g);
+            raw[s][tq][ks][0] = v.x;
+            raw[s][tq][ks][1] = v.y;
+          }
+        }
+      }
+      const int64_t jo = kb + 64 * s + lane;
+      scl[s] = srow[jo < nv_max ? jo : 0];
+    }
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      i32x4_t Bop[4][KS];
+#pragma unroll
+      for (int tq = 0; tq < 4; ++tq)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          if constexpr (BITS == 8) {
+            Bop[tq][ks] = i32x4_t{static_cast<int>(raw[s][tq][ks][0]), static_cast<int>(raw[s][tq][ks][1]),
+                                  static_cast<int>(raw[s][tq][ks][2]), static_cast<int>(raw[s][tq][ks][3])};
+          } else {
+            const uint32_t x = raw[s][tq][ks][0], y = raw[s][tq][ks][1];
+            Bop[tq][ks] = i32x4_t{static_cast<int>((x << 4) & 0xF0F0F0F0u), static_cast<int>(x & 0xF0F0F0F0u),
+                                  static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
+          }
+        }
+      const int64_t jo = kb + 64 * s + lane;
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        if (TT > 1 && kb + 64 * s >= nv[tt]) continue;  // wave-uniform: this row has no key in the slot group
+        float tq_t[4];
+#pragma unroll
+        for (int tq = 0; tq < 4; ++tq) {
+          i32x4_t acc[NRB];
+#pragma unroll
+          for (int rb = 0; rb < NRB; ++rb) acc[rb] = i32x4_t{0, 0, 0, 0};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+              acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tt][rb][ks], Bop[tq][ks], acc[rb], 0, 0, 0);
+          float t = 0.0f;
+#pragma unroll
+          for (int rb = 0; rb < NRB; ++rb) {
+            float v = static_cast<float>(acc[rb][0]) * f[tt][rb][0];
+            v = fmaf(static_cast<float>(acc[rb][1]), f[tt][rb][1], v);
+            v = fmaf(static_cast<float>(acc[rb][2]), f[tt][rb][2], v);
+            v = fmaf(static_cast<float>(acc[rb][3]), f[tt][rb][3], v);
+            t += __builtin_amdgcn_fmed3f(v, lo[tt][rb], hi[tt][rb]);
+          }
+          tq_t[tq] = t;
+        }
+        // sum over the four head groups; lane l keeps key kb + 64s + l, i.e. tq = l / 16
+        const float mine = row_sums_scatter(tq_t);
+        const bool ok = jo < nv[tt];
+        const uint32_t key = ok ? order_key(mine * scl[s]) : 0u;
+        uint32_t* krow = a.keys + row[tt] * a.ks;
+        uint32_t* mrow = a.smax + row[tt] * a.ms;
+        if (ok) krow[jo] = key;
+        // max of the 16-key slot of lanes 16u .. 16u+15, stored by its first lane
+        uint32_t mx = key;
+        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<1>(__builtin_bit_cast(float, mx))));
+        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<2>(__builtin_bit_cast(float, mx))));
+        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<4>(__builtin_bit_cast(float, mx))));
+        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<8>(__builtin_bit_cast(float, mx))));
+        if ((lane & 15) == 0 && ok) mrow[jo >> 4] = mx;
+      }
+    }
+  }
+}
+
+// ---- final: exact top-k of a row, sorted ------------------------------------------------------
+__device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
+  // ascending order of (~key, idx) == key descending, index ascending
+  return (static_cast<uint64_t>(~key) << 32) | idx;
+}
+
+// One workgroup per row.
+//  1. Slot bound: every 16-key slot's max is one of its keys, so if kk slot maxima are >= tau
+//     then the kk-th largest key is >= tau, and every top-kk key lies in a slot whose max is >=
+//     tau.  tau is the floor of the bin holding the kk-th largest slot max in an LDS histogram of
+//     the maxima whose 4096 bins are the values of key >> 16 just below the row's largest slot
+//     max (1/128 of a binade each; the lowest bin also takes everything further down, and tau is
+//     0 if it holds the kk-th).  Only the slots with max >= tau are read, and their keys >= tau
+//     collected.
+//  2. Three radix levels over the candidates (bits 31..20, 19..8, 7..0; LDS histograms) give
+//     the kk-th largest key T; keys > T are taken with the lowest-index keys == T and the kk words
+//     placed by rank.  If the candidates overflow LDS (many equal keys), the levels run over all
+//     of the row's keys, read in index order.
+// NT threads per row; CAP candidates collected in LDS; up to NT candidates sorted outright.
+// 1024 / 4096 for few rows; 512 / 1536 (37 KB of LDS, 80 VGPRs: three rows per CU, where the
+// 1024-thread instance at 73 VGPRs fits one) for launches of many rows with k <= 512.
+// sel_lds (nullable): the row's output indices also go there as int32 (-1 padding), for a caller
+// that continues with them in the same workgroup.
+template <int NT, int CAP>
+__device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, int64_t* __restrict__ out_idx,
+                                           float* __restrict__ out_score, int32_t* __restrict__ sel_lds) {
+  constexpr int NW = NT / 64;
+  __shared__ uint64_t cbuf[CAP];  // candidates: keys ck[] then indices ci[], or sort words
+  __shared__ __align__(16) uint32_t h[kHistBins];
+  __shared__ uint64_t sel[kMaxMfmaK];
+  __shared__ uint32_t s_tot[NW], s_res[3], s_cnt[2], s_wave_eq[NW];
+  uint32_t* ck = reinterpret_cast<uint32_t*>(cbuf);
+  uint32_t* ci = ck + CAP;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t nv = visible(a, b);
+  const int k = a.k;
+  const uint32_t kk = static_cast<uint32_t>(min<int64_t>(k, nv));
+  int64_t* orow = out_idx + static_cast<int64_t>(b) * k;
+  float* srow = out_score ? out_score + static_cast<int64_t>(b) * k : nullptr;
+  for (int i = static_cast<int>(kk) + tid; i < k; i += NT) {
+    orow[i] = -1;
+    if (srow) srow[i] = -__builtin_inff();
+    if (sel_lds) sel_lds[i] = -1;
+  }
+  if (kk == 0) return;
+  const uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.ks;
+  const uint4* krow4 = reinterpret_cast<const uint4*>(krow);
+  const uint32_t* mrow = a.smax + static_cast<int64_t>(b) * a.ms;
+  const int64_t n_slots = (nv + 15) >> 4;
+
+  // ---- 1. slot bound and candidates ----
+  // thread tid owns slots c0 + tid + r * NT (r < kSlotPer) of each pass of 4096 slots; with
+  // n_slots <= 4096 (S <= 65536) the maxima loaded for the histogram are reused for the scan
+  constexpr int kSlotPer = kHistBins / NT;  // one pass over the slot maxima for S <= 65536
+  constexpr int64_t kSlotPass = static_cast<int64_t>(kSlotPer) * NT;
+  for (int i = tid; i < kHistBins; i += NT) h[i] = 0u;
+  if (tid == 0) s_cnt[0] = 0u;
+  uint32_t mx[kSlotPer];
+  auto load_max = [&](int64_t c0) {
+#pragma unroll
+    for (int r = 0; r < kSlotPer; ++r) {
+      const int64_t sl = c0 + tid + static_cast<int64_t>(r) * NT;
+      mx[r] = sl < n_slots ? mrow[sl] : 0u;
+    }
+  };
+  // the row's largest slot max anchors the histogram
+  uint32_t mloc = 0u;
+  for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
+    load_max(c0);
+#pragma unroll
+    for (int r = 0; r < kSlotPer; ++r) mloc = mloc > mx[r] ? mloc : mx[r];  // mx is 0 past the end
+  }
+  mloc = wave_max_u32(mloc);
+  if (lane == 0) s_tot[wv] = mloc;
+  __syncthreads();  // also orders the zeroing of h before the histogram
+  uint32_t top = 0u;
+#pragma unroll
+  for (int w2 = 0; w2 < NW; ++w2) top = top > s_tot[w2] ? top : s_tot[w2];
+  top >>= 16;
+  // bin 4095 - d holds the maxima with key >> 16 == top - d (d < 4095); bin 0 everything lower
+  for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
+    if (n_slots > kSlotPass) load_max(c0);  // otherwise mx still holds the only pass
+#pragma unroll
+    for (int r = 0; r < kSlotPer; ++r) {
+      const uint32_t d = top - (mx[r] >> 16);
+      if (c0 + tid + static_cast<int64_t>(r) * NT < n_slots)
+        atomicAdd(&h[kHistBins - 1 - (d < kHistBins - 1 ? d : kHistBins - 1)], 1u);
+    }
+  }
+  __syncthreads();
+  uint32_t tau = 0u;
+  if (static_cast<int64_t>(kk) <= n_slots) {
+    uint32_t t, ab, ct;
+    block_threshold<NT, kHistBins / NT>(h, kk, s_tot, s_res, t, ab, ct);
+    (void)ab;
+    (void)ct;
+    tau = t > 0u ? (top - (kHistBins - 1 - t)) << 16 : 0u;
+  }
+  // qualifying slots (max >= tau) are compacted into a list (in h, free until the radix levels),
+  // then one thread per listed slot reads its 16 keys and appends those >= tau
+  for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
+    if (n_slots > kSlotPass) load_max(c0);  // otherwise mx still holds the only pass
+    __syncthreads();  // h and s_cnt[1] are free
+    if (tid == 0) s_cnt[1] = 0u;
+    __syncthreads();
+    {  // one reservation per wave for all of its slot columns
+      bool q[kSlotPer];
+      uint64_t m[kSlotPer];
+      uint32_t tot = 0u;
+#pragma unroll
+      for (int r = 0; r < kSlotPer; ++r) {
+        const int64_t sl = c0 + tid + static_cast<int64_t>(r) * NT;
+        q[r] = sl < n_slots && mx[r] >= tau;
+        m[r] = __builtin_amdgcn_ballot_w64(q[r]);
+        tot += static_cast<uint32_t>(__builtin_popcountll(m[r]));
+      }
+      uint32_t base = 0u;
+      if (lane == 0 && tot != 0u) base = atomicAdd(&s_cnt[1], tot);
+      base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+      for (int r = 0; r < kSlotPer; ++r) {
+        if (q[r]) h[base + static_cast<uint32_t>(mbcnt64(m[r]))] = static_cast<uint32_t>(tid + r * NT);
+        base += static_cast<uint32_t>(__builtin_popcountll(m[r]));
+      }
+    }
+    __syncthreads();
+    const int n_list = static_cast<int>(s_cnt[1]);
+    for (int li = tid; li < n_list; li += NT) {
+      const int64_t sl = c0 + h[li];
+      uint32_t kw[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 v = krow4[sl * 4 + q];
+        kw[4 * q] = v.x;
+        kw[4 * q + 1] = v.y;
+        kw[4 * q + 2] = v.z;
+        kw[4 * q + 3] = v.w;
+      }
+      uint32_t c = 0;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) c += (16 * sl + e < nv && kw[e] >= tau) ? 1u : 0u;
+      uint32_t p = wave_reserve<5>(&s_cnt[0], c);  // c <= 16
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        if (16 * sl + e < nv && kw[e] >= tau) {
+          if (p < static_cast<uint32_t>(CAP)) {
+            ck[p] = kw[e];
+            ci[p] = static_cast<uint32_t>(16 * sl + e);
+          }
+          ++p;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t n_cand = s_cnt[0];
+  const bool fast = n_cand <= static_cast<uint32_t>(CAP);
+  const int n = fast ? static_cast<int>(n_cand) : 0;
+
+  // ---- 2a. up to NT candidates (the usual case): sort them all, emit the first kk ----
+  // Wave w sorts candidates 64w .. 64w+63 in registers (bitonic network over lane exchanges);
+  // the runs go to LDS and every candidate's final position is its index in its run plus, for
+  // each other run, the number of smaller words there (binary search).  Words are distinct.
+  if (fast && n <= NT) {
+    uint64_t w = tid < n ? sort_word(ck[tid], ci[tid]) : ~0ull;
+    if (64 * wv < n) {  // wave-uniform: waves past the candidates only pad
+#pragma unroll
+      for (int kq = 2; kq <= 64; kq <<= 1) {
+#pragma unroll
+        for (int j = kq >> 1; j > 0; j >>= 1) {
+          const uint64_t o = xor_lane_u64(w, j);
+          const bool keep_min = ((lane & j) == 0) == ((lane & kq) == 0);
+          w = keep_min ? (o < w ? o : w) : (o > w ? o : w);
+        }
+      }
+    }
+    __syncthreads();  // ck/ci are read
+    cbuf[tid] = w;    // run wv at cbuf[64 wv .. 64 wv + 63], ascending; runs past n_runs all ~0
+    __syncthreads();
+    const int n_runs = (n + 63) >> 6;
+    if (tid < n) {
+      // position = number of smaller words over all runs (the own run gives the lane); the binary
+      // searches of 8 runs are interleaved so that their LDS reads overlap
+      uint32_t pos = 0u;
+      for (int r0 = 0; r0 < n_runs; r0 += 8) {
+        int lo[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) lo[q] = 0;
+#pragma unroll
+        for (int step = 32; step > 0; step >>= 1) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            if (cbuf[64 * (r0 + q) + lo[q] + step - 1] < w) lo[q] += step;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {  // the steps reach 63; the last compare 64
+          if (cbuf[64 * (r0 + q) + lo[q]] < w) ++lo[q];
+          pos += static_cast<uint32_t>(lo[q]);
+        }
+      }
+      if (pos < kk) {
+        orow[pos] = static_cast<int64_t>(static_cast<uint32_t>(w & 0xffffffffu));
+        if (srow) srow[pos] = order_key_inv(~static_cast<uint32_t>(w >> 32));
+        if (sel_lds) sel_lds[pos] = static_cast<int32_t>(w & 0xffffffffu);
+      }
+    }
+    return;
+  }
+
+  // ---- 2. three radix levels down to the kk-th largest key T ----
+  uint32_t need = kk;  // keys still to take at or below the current prefix
+  uint32_t prefix = 0u;
+  int shift = 32;
+#pragma unroll 1
+  for (int lvl = 0; lvl < 3; ++lvl) {
+    const int wbits = lvl < 2 ? 12 : 8;
+    const int nb = 1 << wbits;
+    const int nshift = shift - wbits;
+    const uint32_t mask = static_cast<uint32_t>(nb - 1);
+    __syncthreads();  // the previous level's readers of h are done
+    for (int i = tid; i < nb; i += NT) h[i] = 0u;
+    __syncthreads();
+    // (key >> 32) is undefined: level 0 has no prefix to match
+    if (fast) {
+      for (int i = tid; i < n; i += NT) {
+        const uint32_t key = ck[i];
+        if (lvl == 0 || (key >> shift) == prefix) atomicAdd(&h[(key >> nshift) & mask], 1u);
+      }
+    } else {
+      for (int64_t j = tid; j < nv; j += NT) {
+        const uint32_t key = krow[j];
+        if (lvl == 0 || (key >> shift) == prefix) atomicAdd(&h[(key >> nshift) & mask], 1u);
+      }
+    }
+    __syncthreads();
+    uint32_t t, ab, ct;
+    if (lvl < 2) {
+      block_threshold<NT, kHistBins / NT>(h, need, s_tot, s_res, t, ab, ct);
+    } else {
+      if (wv == 0) wave_threshold<4>(h, need, s_res);  // 256 bins
+      __syncthreads();
+      t = s_res[0];
+      ab = s_res[1];
+    }
+    (void)ct;
+    need -= ab;
+    prefix = (prefix << wbits) | t;
+    shift = nshift;
+  }
+  const uint32_t T = prefix;          // the kk-th largest key
+  const uint32_t n_eq = h[T & 0xFFu]; // keys == T
+  const uint32_t n_gt = kk - need;    // keys > T; `need` keys == T are taken, lowest index first
+  __syncthreads();
+  if (tid == 0) {
+    s_cnt[0] = 0u;
+    s_cnt[1] = 0u;
+  }
+  __syncthreads();
+  if (fast) {
+    const bool all_eq = n_eq == need;
+    for (int i = tid; i < n; i += NT) {
+      const uint32_t key = ck[i], idx = ci[i];
+      const uint32_t pg = wave_reserve<1>(&s_cnt[0], key > T ? 1u : 0u);
+      const uint32_t pe = wave_reserve<1>(&s_cnt[1], key == T && all_eq ? 1u : 0u);
+      if (key > T) {
+        if (pg < n_gt) sel[pg] = sort_word(key, idx);
+      } else if (key == T) {
+        if (all_eq) {
+          if (pe < need) sel[n_gt + pe] = sort_word(key, idx);
+        } else {  // ties at T: rank among the equal keys by index
+          uint32_t r = 0;
+          for (int j = 0; j < n; ++j) r += (ck[j] == T && ci[j] < idx) ? 1u : 0u;
+          if (r < need) sel[n_gt + r] = sort_word(key, idx);
+        }
+      }
+    }
+  } else {
+    uint32_t eq_run = 0;
+    for (int64_t base = 0; base < nv; base += NT) {
+      const int64_t j = base + tid;
+      const uint32_t key = j < nv ? krow[j] : 0u;
+      const bool gt = j < nv && key > T;
+      const bool eq = j < nv && key == T;
+      const uint32_t pg = wave_reserve<1>(&s_cnt[0], gt ? 1u : 0u);
+      if (gt && pg < n_gt) sel[pg] = sort_word(key, static_cast<uint32_t>(j));
+      const uint64_t m = __builtin_amdgcn_ballot_w64(eq);
+      if (lane == 0) s_wave_eq[wv] = static_cast<uint32_t>(__builtin_popcountll(m));
+      __syncthreads();
+      uint32_t before = 0, total = 0;
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) {
+        const uint32_t c = s_wave_eq[w2];
+        before += w2 < wv ? c : 0u;
+        total += c;
+      }
+      if (eq) {
+        const uint32_t r = eq_run + before + static_cast<uint32_t>(mbcnt64(m));
+        if (r < need) sel[n_gt + r] = sort_word(key, static_cast<uint32_t>(j));
+      }
+      eq_run += total;
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  // the kk words are distinct: each one's output position is its rank.  Four adjacent lanes
+  // share an element, each counting over a quarter of the words.
+  const int q4 = (static_cast<int>(kk) + 3) / 4;
+  for (int base = 0; base < static_cast<int>(kk); base += NT / 4) {
+    const int i = base + (tid >> 2), part = tid & 3;
+    const uint64_t w = i < static_cast<int>(kk) ? sel[i] : 0ull;
+    const int j0 = part * q4, j1 = min(static_cast<int>(kk), j0 + q4);
+    uint32_t r = 0;
+#pragma unroll 8
+    for (int j = j0; j < j1; ++j) r += sel[j] < w ? 1u : 0u;
+    r += __builtin_bit_cast(uint32_t, xor_lane<1>(__builtin_bit_cast(float, r)));
+    r += __builtin_bit_cast(uint32_t, xor_lane<2>(__builtin_bit_cast(float, r)));
+    if (part == 0 && i < static_cast<int>(kk)) {
+      orow[r] = static_cast<int64_t>(static_cast<uint32_t>(w & 0xffffffffu));
+      if (srow) srow[r] = order_key_inv(~static_cast<uint32_t>(w >> 32));
+      if (sel_lds) sel_lds[r] = static_cast<int32_t>(w & 0xffffffffu);
+    }
+  }
+}
+
+template <int NT, int CAP>
+__global__ __launch_bounds__(NT) void idx_mfma_final_kernel(MfmaIdxArgs a, int64_t* __restrict__ out_idx,
+                                                            float* __restrict__ out_score) {
+  select_row<NT, CAP>(a, blockIdx.x, out_idx, out_score, nullptr);
+}
+
+// Launch set-up shared by the indexer and the fused CSA decode step: fills the kernel arguments
+// for B rows (T per key row), enqueues the score kernel and returns its status.
+int launch_mfma_score(MfmaIdxArgs& a, const float* q, const float* w, const void* codes, const float* kscale,
+                      const float* diag, const int32_t* valid, int64_t B, int64_t T, int64_t S, int IH, int IC,
+                      int bits, int k, int mode, void* ws, hipStream_t st, const char* who);
+
+}  // namespace idx
+}  // namespace aekv

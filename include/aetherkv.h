@@ -26,6 +26,8 @@
  *   aekv_emit_block                  aether_2b/serving.py:495-505 (_hca_emit) and :557-576
  *                                    (_emit_csa_block): pool + RoPE + kv_norm + _quant_append
  *   aekv_tiled_prefill_attention     aether_kernels/sparse_attention.py:19-42   tiled_prefill_attention(...)
+ *   aekv_csa_decode_quant            aether_2b/serving.py:597-625 (the CSA decode step: indexer, topk, gather,
+ *                                    window concat and sink attention)
  */
 #ifndef AETHERKV_H_
 #define AETHERKV_H_
@@ -202,6 +204,23 @@ int aekv_quant_prefill_attention(const void* q, const void* codes, const float* 
                                  int64_t T, int64_t H, int64_t D, int64_t S, int64_t n_sel, int64_t Wt,
                                  int32_t bits, float softmax_scale, void* ws, size_t ws_bytes, void* out,
                                  void* stream);
+
+/* One CSA decode step over TurboQuant-coded caches (aether_2b/serving.py:597-625: score every
+ * visible block of the index cache, topk, gather the selected KV blocks, concat the window, attend
+ * with the per-head sink): aekv_csa_indexer_topk_quant's selection (out_idx [B, k] int64, -1 padded,
+ * out_score nullable) followed by aekv_quant_sink_attention over sel = out_idx, n_sel = k (out
+ * [B, H, D] bf16), with the same results.  Where the matrix-core kernels apply (IH <= 16, IC 64 or
+ * 128, k <= 512, D = 128, H <= 16, k + W <= 1024, 16-byte aligned q, codes, window and diag) the
+ * selection and the attention run in one workgroup per row; otherwise the two entry points run in
+ * turn.  Workspace: aekv_csa_decode_workspace_size(B, S, k, H, D, W). */
+size_t aekv_csa_decode_workspace_size(int64_t B, int64_t S, int32_t k, int64_t H, int64_t D, int64_t W);
+int aekv_csa_decode_quant(const float* index_q, const float* index_weight, const void* index_codes,
+                          const float* index_scale, const float* index_diag, const int32_t* valid, int64_t B,
+                          int64_t S, int32_t IH, int32_t IC, int32_t index_bits, int32_t k, int32_t mode,
+                          const void* q, const void* kv_codes, const float* kv_scale, const void* window,
+                          const float* sink, const float* kv_diag, int64_t H, int64_t D, int64_t W,
+                          int32_t kv_bits, float softmax_scale, void* ws, size_t ws_bytes, int64_t* out_idx,
+                          float* out_score, void* out, void* stream);
 
 /* hca_compress drop-in: out[b,d] = sum_m softmax_m(z[b,:,d]) * c[b,m,d], c/z [B,M,D], dtype
  * F32/F16/BF16, out [B,D] same dtype (hca_compress_cuda.cu:18-68; serving.py:495-497). */
