@@ -20,10 +20,11 @@ tq_encode_cfg2_from_idle).  Decode steps (indexer +
 attention) are captured 8 at a time in a HIP graph and replayed, as a serving loop would run them;
 the eager (per-call Python) step time is reported beside it.
 
-cpu_baseline: the CPU oracle (oracle/liboracle.so, a C restatement of turbo_quant.py's encode)
-timed on this host's cores over the cfg2 layer (median of 3 passes).  The CSA lines carry their own
-cpu_baseline: the oracle's decode step (dequantise every step or memoised, scores, exact top-256,
-attention) on the first 8 rows of the config.
+cpu_baseline: the reference's own encode op sequence in torch eager ops (oracle/torch_ref.py) on
+this host's cores over a quarter of the cfg2 layer, with the C oracle's encode of the whole layer
+beside it (c_port).  The CSA lines carry their own cpu_baseline: the oracle's decode step
+(dequantise every step or memoised, scores, exact top-256, attention) and the reference's torch op
+sequence of the step, on the first 8 rows of the config.
 """
 from __future__ import annotations
 
@@ -178,9 +179,34 @@ def bench_cpu_encode(out):
         times.append(time.perf_counter() - t)
     med = sorted(times)[1]
     log(f"cpu oracle encode (cfg2, {cores} threads): {med:.3f} s, {ENC_BYTES / med / 1e9:.2f} GB/s")
-    return {"value": round(ENC_BYTES / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": "full cfg2 layer (3,145,728 vectors), median of 3 passes of the C oracle encode "
-                      "(oracle/aekv_oracle.c, OpenMP over vectors)"}
+    c_port = {"value": round(ENC_BYTES / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+              "sample": "full cfg2 layer (3,145,728 vectors), median of 3 passes of the C oracle encode "
+                        "(oracle/aekv_oracle.c, OpenMP over vectors)"}
+    # the reference's own op sequence (turbo_quant.py:127-166 in torch eager ops), all host cores, on a
+    # quarter of the layer: 65536 tokens x 12 heads
+    import torch_ref as T
+
+    torch.set_num_threads(cores)
+    n_tok = T2 // 4
+    xs = torch.from_numpy(xb.reshape(T2, H2, D2)[:n_tok].copy()).view(torch.bfloat16)
+    dgt = torch.from_numpy(dg)
+    T.encode(xs, 4, dgt)
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        T.encode(xs, 4, dgt)
+        times.append(time.perf_counter() - t)
+    med_t = sorted(times)[1]
+    bytes_t = ENC_BYTES // 4
+    log(f"cpu torch op sequence encode ({n_tok} tokens, {cores} threads): {med_t:.3f} s, "
+        f"{bytes_t / med_t / 1e9:.2f} GB/s")
+    return {"value": round(bytes_t / med_t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "cpu": cpu_model(),
+            "sample": f"the reference's encode op sequence (turbo_quant.py:127-166: torch.cat butterflies, amax, "
+                      f"divide, multiply, round, clamp, nibble pack; oracle/torch_ref.py) on torch CPU with "
+                      f"{cores} threads, over {n_tok} tokens x 12 heads (a quarter of the cfg2 layer), median of 3 "
+                      f"after one warm-up",
+            "c_port": c_port}
 
 
 def bench_cpu_csa(inp, rows, name, bits):
@@ -227,7 +253,51 @@ def bench_cpu_csa(inp, rows, name, bits):
         f"dequantising every step, {res['memoised_dequant']['tokens_per_s']:.1f} tok/s memoised")
     res["sample"] = (f"first {rows} rows of {name}: dequant (index f32 + KV bf16), scores, exact top-256, gather + "
                      f"window + sink attention, C oracle with OpenMP; median of 3")
+    res["torch_op_sequence"] = bench_torch_csa(inp, rows, name, bits)
     return res
+
+
+def bench_torch_csa(inp, rows, name, bits):
+    """The reference decode step's own torch op sequence (oracle/torch_ref.py: serving.py:597-625 with
+    the PyTorch attention backend, bf16 attention as the engine runs it) on the first `rows` rows,
+    torch on all host cores; dequantising every step and memoised.  Median of 3 after one warm-up."""
+    import torch_ref as T
+
+    cores = cpu_cores()
+    torch.set_num_threads(cores)
+    h = {k: v[:rows].cpu() for k, v in inp.items() if isinstance(v, torch.Tensor) and k != "sink"}
+    h["sink"] = inp["sink"].cpu()
+    d64 = torch.from_numpy(__import__("oracle").diag(42, 64))
+    d128 = torch.from_numpy(__import__("oracle").diag(42, 128))
+    res = {"rows": rows, "cores": cores, "kind": "port", "cpu": cpu_model()}
+    for label, memo in (("dequant_every_step", None), ("memoised_dequant", {})):
+        def step():
+            T.csa_decode_step(h["q"], h["index_q"], h["index_w"], h["ix_codes"], h["ix_scale"], h["kv_codes"],
+                              h["kv_scale"], h["win"], h["sink"], bits, d64, d128, 256, memo=memo)
+        step()
+        times = []
+        for _ in range(3):
+            t = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t)
+        med = sorted(times)[1]
+        res[label] = {"s_per_step": round(med, 5), "tokens_per_s": round(rows / med, 2)}
+    log(f"cpu torch op sequence {name} ({rows} rows, {cores} threads): "
+        f"{res['dequant_every_step']['tokens_per_s']:.1f} tok/s dequantising every step, "
+        f"{res['memoised_dequant']['tokens_per_s']:.1f} tok/s memoised")
+    res["sample"] = (f"first {rows} rows of {name}: the reference's torch ops (decode, einsum, relu, softplus weights, "
+                     f"topk, gather, cat, PyTorch sink attention in bf16); median of 3")
+    return res
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def make_csa_inputs(dev, B, S, bits, seed, outliers):

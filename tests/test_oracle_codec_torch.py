@@ -25,52 +25,16 @@ import scipy.linalg
 import torch
 
 import oracle as O
+import torch_ref as T
 
 N_ROWS = {64: 40000, 128: 75000}   # per (d, bits): 2 * (40000 + 75000) = 230000 rows in all
 
 
-# ---- the reference's op sequence, torch eager (turbo_quant.py:49-76, 127-211) ---------------------
-def _t_wht(x: torch.Tensor) -> torch.Tensor:
-    d = x.shape[-1]
-    lead = x.shape[:-1]
-    out = x.to(torch.float32)
-    h = 1
-    while h < d:
-        blocks = out.view(*lead, d // (2 * h), 2 * h)
-        lo, hi = blocks[..., :h], blocks[..., h:]
-        out = torch.cat([lo + hi, lo - hi], dim=-1).view(*lead, d)
-        h *= 2
-    return out * (d ** -0.5)
-
-
-def _t_encode(x: torch.Tensor, bits: int, diag: torch.Tensor):
-    rot = _t_wht(x.float() * diag)
-    q_max = 127.0 if bits == 8 else 7.0
-    max_abs = rot.abs().amax(dim=-1, keepdim=True).clamp_(min=1e-8)
-    scale = max_abs / q_max
-    q = (rot / max_abs * q_max).round_().clamp_(-q_max, q_max)
-    if bits == 8:
-        return q.to(torch.int8), scale
-    q = q.to(torch.int32)
-    return ((q[..., 0::2] & 0x0F) | ((q[..., 1::2] & 0x0F) << 4)).to(torch.uint8), scale
-
-
-def _t_unpack(data: torch.Tensor, bits: int) -> torch.Tensor:
-    if bits == 8:
-        return data.to(torch.float32)
-    p = data.to(torch.int32)
-    lo, hi = p & 0x0F, (p >> 4) & 0x0F
-    lo = torch.where(lo >= 8, lo - 16, lo)
-    hi = torch.where(hi >= 8, hi - 16, hi)
-    q = torch.empty(*data.shape[:-1], data.shape[-1] * 2, dtype=torch.float32)
-    q[..., 0::2] = lo.float()
-    q[..., 1::2] = hi.float()
-    return q
-
-
-def _t_decode(data: torch.Tensor, scale: torch.Tensor, bits: int, diag: torch.Tensor, out_dtype):
-    rot = _t_unpack(data, bits) * scale.to(torch.float32)
-    return (_t_wht(rot) * diag).to(out_dtype)
+# ---- the reference's op sequence, torch eager (oracle/torch_ref.py) ---------------------------------
+_t_wht = T.wht
+_t_encode = T.encode
+_t_unpack = T.unpack
+_t_decode = T.decode
 
 
 # ---- the two alternative orderings (used only to show the inputs separate them) --------------------
@@ -242,3 +206,31 @@ def test_decode_scale_before_transform_known_answer():
         raise AssertionError("no separating row found")
     got = O.decode(np.array([c], np.int8), np.array([[float(s)]], np.float32), 8, dg, "f32")
     np.testing.assert_array_equal(got[0], np.array([float(v) for v in ref], np.float32))
+
+
+# ---- the torch CSA decode step (the CPU baseline) against the C oracle ---------------------------------
+@pytest.mark.parametrize("bits", [4, 8])
+def test_torch_csa_decode_step_matches_c_oracle(bits):
+    # aether_2b/serving.py:597-625 as torch ops (oracle/torch_ref.py) and the C oracle's pieces must agree:
+    # the selected set up to fp32 near-ties, the attention within the path's tolerance (fp32 compute)
+    from topk_check import assert_topk_matches, score_error_bound
+
+    B, S, H, D, W, IH, IC, k = 3, 700, 12, 128, 32, 4, 64, 64
+    g = torch.Generator().manual_seed(bits)
+    dk, di = torch.from_numpy(O.diag(42, D)), torch.from_numpy(O.diag(42, IC))
+    kv_codes, kv_scale = T.encode(torch.randn(B, S, D, generator=g).to(torch.bfloat16), bits, dk)
+    ix_codes, ix_scale = T.encode(torch.randn(B, S, IC, generator=g).to(torch.bfloat16), bits, di)
+    q = torch.randn(B, 1, H, D, generator=g).to(torch.bfloat16)
+    iq, iw = torch.randn(B, IH, IC, generator=g), torch.randn(B, IH, generator=g)
+    win = torch.randn(B, W, D, generator=g).to(torch.bfloat16)
+    sink = torch.randn(H, generator=g)
+    out, idx = T.csa_decode_step(q, iq, iw, ix_codes, ix_scale, kv_codes, kv_scale, win, sink, bits, di, dk, k,
+                                 compute_dtype=torch.float32)
+    keys = O.decode(ix_codes.numpy(), ix_scale.numpy(), bits, O.diag(42, IC), "f32")
+    scores = O.index_scores(iq.numpy(), iw.numpy(), keys)
+    wa = np.log1p(np.exp(iw.numpy().astype(np.float64)))
+    assert_topk_matches(idx.numpy(), scores, k,
+                        score_error_bound(iq.numpy(), wa, keys, extra_rel=96 * 2.0 ** -24))
+    want = O.quant_attention(q.float().numpy().reshape(B, H, D), kv_codes.numpy(), kv_scale.numpy(), idx.numpy(),
+                             win.float().numpy(), sink.numpy(), O.diag(42, D), bits, D ** -0.5)
+    np.testing.assert_allclose(out.float().numpy().reshape(B, H, D), want, rtol=1e-2, atol=2e-3)
