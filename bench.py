@@ -12,8 +12,8 @@ cfg3), HCA decode tokens/s (cfg4), chunked-prefill targets/s through the quantis
 256 targets per sequence over cfg3's and cfg4's caches) and the reference microbenchmark shape of
 sparse_sink_attention.
 
-Timing: a settle period (60 ms of continuous launches of the timed call: MI355X ramps its memory
-clocks up over the first ~20 ms of sustained load), W untimed warmup steps, then K steps bracketed
+Timing: a settle period (60 ms of continuous launches of the timed call: the box runs a slower
+phase during the first ~20 ms of sustained load), W untimed warmup steps, then K steps bracketed
 by torch.cuda.synchronize() and HIP events recorded on the stream the kernels run on (torch's
 current stream).  The encode is also timed without the settle period (secondary
 tq_encode_cfg2_from_idle).  Decode steps (indexer +
@@ -58,10 +58,11 @@ SETTLE_S = 0.06  # seconds of continuous launches before each timed section
 
 
 def settle(fn, seconds: float = SETTLE_S) -> None:
-    """Keeps the GPU busy with fn for `seconds` of wall time.  MI355X raises its memory and fabric
-    clocks only after ~20 ms of sustained load: measured on the cfg2 encode, the first ~100 launches
-    after an idle period average 195 us and every later one 171 us.  A timed section that starts
-    from idle would measure that ramp, not the kernel, so each one is preceded by this."""
+    """Keeps the GPU busy with fn for `seconds` of wall time.  Under sustained load the box goes
+    through a slower phase that starts a few ms in and ends about 20 ms in: measured on the cfg2
+    encode, launches 1-100 after an idle period average 195 us and every later one 171 us (the
+    early ones ~164 us, then ~215 us, then steady).  A timed section that starts from idle would
+    measure that transition rather than the kernel, so each one is preceded by this."""
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds:
         for _ in range(8):
@@ -664,8 +665,8 @@ def main():
         ms_i = res["encode_ms_from_idle"]
         secondary["tq_encode_cfg2_from_idle"] = {
             "ms": round(ms_i, 5), "GB/s": round(ENC_BYTES / ms_i / 1e6, 2),
-            "note": "the same K steps after only the W warmup steps, i.e. while the memory clocks ramp up "
-                    "after idle; `value` is timed after a settle period of continuous launches"}
+            "note": "the same K steps after only the W warmup steps, i.e. inside the slower phase of the "
+                    "first ~20 ms of load after idle; `value` is timed after a settle period of continuous launches"}
     else:
         first = next(iter(secondary.values()), {})
         line.update({"value": first.get("tokens_per_s"), "unit": "tokens/s", "ms_per_step": first.get("ms_per_step"),
