@@ -580,6 +580,10 @@ def bench_attention_io(args, dev):
 
 
 def bench_sparse_report_shape(args, dev):
+    """The reference's kernel microbenchmark shape (scripts/benchmark_cuda_kernels.py:12-57, published
+    in TECHNICAL_REPORT.md:228-235): eager calls through the drop-in entry point, as the reference
+    times it, and the same call replayed from a HIP graph (the kernel without the host's per-call
+    cost)."""
     from aetherkv import sparse_sink_attention
 
     g = torch.Generator(device=dev).manual_seed(0)
@@ -587,9 +591,46 @@ def bench_sparse_report_shape(args, dev):
     kv = torch.randn(1, 8192, 2, 128, device=dev, generator=g).half()
     topk = torch.randint(0, 8192, (1, 128, 64), device=dev, generator=g, dtype=torch.int32)
     sink = torch.zeros(16, device=dev).half()
-    ms = timed(lambda: sparse_sink_attention(q, kv, topk, sink, 128 ** -0.5), args.steps, args.warmup)
-    log(f"sparse_sink_attention report shape: {ms * 1e3:.1f} us (reference published 75.9 us)")
-    return {"shape": "fp16 B=1 T=128 H=16 D=128 S=8192 top_k=64", "ms": round(ms, 5), "reference_published_ms": 0.0759}
+    fn = lambda: sparse_sink_attention(q, kv, topk, sink, 128 ** -0.5)  # noqa: E731
+    ms = timed(fn, args.steps, args.warmup)
+    ms_g = timed_graph(fn, args.steps, args.warmup)
+    log(f"sparse_sink_attention report shape: {ms * 1e3:.1f} us eager, {ms_g * 1e3:.1f} us graphed "
+        "(reference published 75.9 us)")
+    return {"shape": "fp16 B=1 T=128 H=16 D=128 S=8192 top_k=64", "ms": round(ms, 5), "ms_graphed": round(ms_g, 5),
+            "reference_published_ms": 0.0759}
+
+
+def bench_tiled_prefill(args, dev):
+    """tiled_prefill_attention (aether_kernels/sparse_attention.py:19-42) at two shapes: T = 256
+    targets over S = 8192 sources (16 heads, bf16, separate K and V), and the per-target call the
+    model makes in its tiled prefill (modeling.py:322,534: q [1, 1, 16, 128] over top-512 blocks +
+    a 128-entry window stacked as K = V)."""
+    from aetherkv import tiled_prefill_attention
+
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(1)
+    B, T, H, S, D = 1, 256, 16, 8192, 128
+    q = torch.randn(B, T, H, D, device=dev, generator=g).to(torch.bfloat16)
+    kv = torch.randn(B, S, 2, D, device=dev, generator=g).to(torch.bfloat16)
+    sink = torch.randn(H, device=dev, generator=g).to(torch.bfloat16)
+    ms = timed(lambda: tiled_prefill_attention(q, kv, sink, D ** -0.5), args.steps, args.warmup)
+    tflops = 4 * B * T * H * S * D / ms / 1e9
+    res["prefill"] = {"shape": "bf16 B=1 T=256 H=16 D=128 S=8192", "ms": round(ms, 5), "tflops": round(tflops, 2),
+                      "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)}
+    log(f"tiled_prefill_attention T={T} S={S}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
+    S1 = 640
+    q1 = torch.randn(1, 1, H, D, device=dev, generator=g).to(torch.bfloat16)
+    src = torch.randn(1, S1, D, device=dev, generator=g).to(torch.bfloat16)
+    kv1 = torch.stack([src, src], dim=2)
+    fn = lambda: tiled_prefill_attention(q1, kv1, sink, D ** -0.5)  # noqa: E731
+    ms1 = timed(fn, args.steps, args.warmup)
+    ms1_g = timed_graph(fn, args.steps, args.warmup)
+    res["model_call"] = {"shape": "bf16 B=1 T=1 H=16 D=128 S=640 (K = V)", "ms": round(ms1, 5),
+                         "ms_graphed": round(ms1_g, 5)}
+    log(f"tiled_prefill_attention per-target call S={S1}: {ms1 * 1e3:.1f} us eager, {ms1_g * 1e3:.1f} us graphed")
+    del q, kv, q1, kv1, src
+    torch.cuda.empty_cache()
+    return res
 
 
 def main():
@@ -638,6 +679,7 @@ def main():
         secondary["code_pages"] = bench_paging(args, dev)
     if args.only in ("all", "sparse"):
         secondary["sparse_sink_attention_report_shape"] = bench_sparse_report_shape(args, dev)
+        secondary["tiled_prefill_attention"] = bench_tiled_prefill(args, dev)
 
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic"}

@@ -8,7 +8,9 @@ Reference: aether_kernels/sparse_attention.py:8-83 (wrappers) and aether_kernels
 * ``csa_indexer_topk(index_q, index_kv, index_weight, k, *, mode="relu_w")``
 * ``hca_compress(buffer_c, buffer_z)``
 
-Outputs are freshly allocated tensors on the inputs' device; kernels run on the current stream.
+Outputs are freshly allocated tensors on the inputs' device; kernels run on the current stream.  The
+attention calls also take a split workspace from torch's caching allocator when the matrix-core
+launch would leave most CUs idle (few targets, many sources).
 """
 from __future__ import annotations
 
@@ -27,6 +29,11 @@ def _check_input(name: str, t: torch.Tensor) -> None:
 def _check_sink(sink: torch.Tensor, heads: int) -> None:
     if not (sink.numel() == 1 or (sink.dim() == 1 and sink.size(0) == heads)):
         raise RuntimeError("sink must be a scalar or a [num_heads] tensor")
+
+
+def _workspace(nbytes: int, device):
+    """Split workspace for the matrix-core attention (torch's caching allocator; None: no split)."""
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
 
 
 def _ext_sparse_sink_attention(q, kv, topk_indices, sink, softmax_scale):
@@ -56,11 +63,15 @@ def _ext_sparse_sink_attention(q, kv, topk_indices, sink, softmax_scale):
         raise RuntimeError("q, kv and sink must share one floating dtype")
     B, T, H, D = q.shape
     out = torch.empty_like(q)
+    L = _lib.lib()
+    K = topk_indices.size(2)
+    ws = _workspace(L.aekv_sink_attention_workspace_size(_lib.dtype_code(q), B, T, H, D, kv.size(1), K), q.device)
     with torch.cuda.device(q.device):
-        _lib.check(_lib.lib().aekv_sparse_sink_attention(
+        _lib.check(L.aekv_sparse_sink_attention_ws(
             _lib.ptr(q), _lib.ptr(kv), _lib.ptr(topk_indices), _lib.dtype_code(topk_indices), _lib.ptr(sink),
-            sink.numel(), _lib.dtype_code(q), B, T, H, D, kv.size(1), topk_indices.size(2), float(softmax_scale),
-            _lib.ptr(out), _lib.stream_of(q)), "aekv_sparse_sink_attention")
+            sink.numel(), _lib.dtype_code(q), B, T, H, D, kv.size(1), K, float(softmax_scale),
+            _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(out), _lib.stream_of(q)),
+            "aekv_sparse_sink_attention")
     return out
 
 
@@ -85,10 +96,13 @@ def _ext_tiled_prefill_attention(q, kv, sink, softmax_scale, tile_size):
         raise RuntimeError("q, kv and sink must share one floating dtype")
     B, T, H, D = q.shape
     out = torch.empty_like(q)
+    L = _lib.lib()
+    ws = _workspace(L.aekv_sink_attention_workspace_size(_lib.dtype_code(q), B, T, H, D, kv.size(1), -1), q.device)
     with torch.cuda.device(q.device):
-        _lib.check(_lib.lib().aekv_tiled_prefill_attention(
+        _lib.check(L.aekv_tiled_prefill_attention_ws(
             _lib.ptr(q), _lib.ptr(kv), _lib.ptr(sink), sink.numel(), _lib.dtype_code(q), B, T, H, D, kv.size(1),
-            float(softmax_scale), int(tile_size), _lib.ptr(out), _lib.stream_of(q)), "aekv_tiled_prefill_attention")
+            float(softmax_scale), int(tile_size), _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(out),
+            _lib.stream_of(q)), "aekv_tiled_prefill_attention")
     return out
 
 

@@ -49,6 +49,23 @@ int launch_hca_prefill_flash(const void* q, const void* kblk, const void* window
                              const int32_t* wstart, const int32_t* wlen, const float* sink, int64_t B, int64_t T,
                              int64_t H, int64_t S, int64_t Wt, float softmax_scale, void* out, hipStream_t st,
                              const char* who);
+// Drop-in sink attention on the matrix cores, head_dim 128, bf16/fp16 (sink_attention_mfma.hip):
+// q [B, T, H, 128], kv [B, S, 2, 128], per-target indices idx [B, T, K] (idx_kind 4/8: int32/int64)
+// or every source (idx_kind 0, K = S).  A workspace (may be null) lets launches with few
+// workgroups split the sources; sink_attention_mfma_workspace gives its size (0: no split).
+bool sink_attention_mfma_supported(int32_t dtype, int64_t D);
+size_t sink_attention_mfma_workspace(bool dense, int64_t B, int64_t T, int64_t H, int64_t S, int64_t K);
+int sink_attention_mfma(const void* q, const void* kv, const void* idx, int idx_kind, const void* sink,
+                        int sink_scalar, int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t S, int64_t K,
+                        float scale, void* ws, size_t ws_bytes, void* out, hipStream_t st, const char* who);
+// The flash kernel for dense calls (prefill_flash.hip): 64 (target, head) rows per workgroup, tiles
+// of dense_flash_tile() sources; with n_split > 1 each row's tiles are split into n_split pieces
+// whose (max, sum, O) go to part (the layout of sink_attention_mfma's combine).
+int64_t dense_flash_row_blocks(int64_t T, int64_t H);
+int64_t dense_flash_tile();
+int launch_dense_flash_attention(const void* q, const void* kv, const void* sink, int sink_scalar, int32_t dtype,
+                                 int64_t B, int64_t T, int64_t H, int64_t S, float softmax_scale, int n_split,
+                                 float* part, void* out, hipStream_t st, const char* who);
 size_t quant_attn_mfma_workspace(int64_t B, int64_t H, int64_t n_src);
 int launch_quant_attn_mfma(const void* q, const void* codes, const float* scale, const int64_t* sel,
                            const void* window, const float* sink, const float* diag, int64_t B, int64_t H, int64_t S,

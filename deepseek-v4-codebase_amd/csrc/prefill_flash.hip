@@ -1,5 +1,13 @@
-// Chunked-prefill HCA attention over dequantised blocks: a flash-style bf16 matrix-core kernel in
-// which 64 (target, head) query rows share every source tile.
+// Flash-style matrix-core sink attention in which 64 (target, head) query rows share every source
+// tile, for two callers:
+//   * chunked-prefill HCA attention over dequantised blocks (bf16, K = V: rows of 256 bytes);
+//   * the dense drop-in tiled_prefill_attention (aether_kernels/sparse_attention.py:19-42, sink
+//     counted once as in aether_2b/modeling.py:158-178) when a call has 64 or more (target, head)
+//     rows: bf16 or fp16 kv [B, S, 2, 128], i.e. rows of 512 bytes holding K then V, every target
+//     over every source.
+// The description below is the HCA use; the dense one is the same kernel with no masks, one
+// source buffer, tiles of 64 512-byte rows (the same 32 KB), V read from the second half of each
+// row, and the fp16 products (v_mfma_f32_32x32x16_f16) for fp16 inputs.
 //
 // Reference: aether_2b/modeling.py:293-325 (_forward_tiled_prefill, HCA): target t attends blocks
 // [0, g_t) and window entries [max(0, t - W + 1), t] with K = V and the per-head sink
@@ -46,29 +54,50 @@ namespace {
 constexpr int kFD = 128;
 constexpr int kFThreads = 256;        // 4 waves
 constexpr int kFRows = 64;            // query rows per workgroup (32 per row half)
-constexpr int kRowBytes = kFD * 2;    // one key of the tile in LDS
-#ifndef AEKV_FLASH_TILE
-#define AEKV_FLASH_TILE 128
-#endif
-constexpr int kFTile = AEKV_FLASH_TILE;  // sources per tile
-constexpr int kKW = kFTile / 2;          // sources per wave and tile
-constexpr int kKB = kKW / 32;            // 32-key score blocks per wave and tile
-constexpr int kChunks = kFTile / 16;     // 16-byte staging chunks per thread and tile
-constexpr int kTileBytes = kFTile * kRowBytes;
-#ifndef AEKV_FLASH_PF
-#define AEKV_FLASH_PF 1
-#endif
-constexpr int kPrefetch = AEKV_FLASH_PF;  // tiles in flight from memory (2 spills registers at 128-key tiles)
-static_assert(kPrefetch == 1 || kPrefetch == 2, "prefetch distance 1 or 2 (register sets alternate with the buffers)");
+constexpr int kTileBytes = 32768;     // one LDS tile buffer
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kFNegInf = -__builtin_inff();
-static_assert(kFTile % 64 == 0 && kFTile <= 128, "tiles are whole 32-key blocks per wave");
 constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: raw 32-bit data, range-checked
+constexpr int kPrefetch = 1;           // tiles in flight from memory (2 spills registers)
 
 typedef __attribute__((ext_vector_type(8))) __bf16 fbf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 ff16x8_t;
 typedef __attribute__((ext_vector_type(16))) float ff32x16_t;
 typedef __attribute__((ext_vector_type(4))) short fi16x4_t;
 typedef __attribute__((address_space(3))) fi16x4_t lds_i16x4_t;
+
+// Source rows of ROWB bytes: 256 (K = V) or 512 (K, then V).  A tile holds kTile rows (32 KB).
+template <int ROWB>
+struct FlashGeom {
+  static_assert(ROWB == 256 || ROWB == 512, "rows of K (= V) or of K then V");
+  static constexpr int kRowBytes = ROWB;
+  static constexpr int kTile = kTileBytes / ROWB;       // sources per tile (128 or 64)
+  static constexpr int kKW = kTile / 2;                 // sources per wave and tile
+  static constexpr int kKB = kKW / 32;                  // 32-key score blocks per wave and tile
+  static constexpr int kCPR = ROWB / 16;                // 16-byte chunks per row
+  static constexpr int kChunks = kTileBytes / (16 * kFThreads);  // staging chunks per thread and tile
+  static constexpr int kVOff = ROWB == 256 ? 0 : 256;   // V's byte offset in a row
+  static constexpr bool kSplit = ROWB == 512;           // the dense caller may split a row's sources
+  static_assert(kKB >= 1, "tiles are whole 32-key blocks per wave");
+};
+
+// The element type's matrix instruction, weight rounding and constants.
+template <int DT>
+struct FlashElem;
+template <>
+struct FlashElem<AEKV_BF16> {
+  typedef fbf16x8_t v8;
+  static constexpr uint32_t kOnePair = 0x3F803F80u;
+  __device__ static ff32x16_t mma(v8 a, v8 b, ff32x16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+  __device__ static uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
+};
+template <>
+struct FlashElem<AEKV_F16> {
+  typedef ff16x8_t v8;
+  static constexpr uint32_t kOnePair = 0x3C003C00u;
+  __device__ static ff32x16_t mma(v8 a, v8 b, ff32x16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+  __device__ static uint32_t pack(float lo, float hi) { return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16); }
+};
 
 // chunk c of key r sits at c ^ chunk_swizzle(r % 16) of its 256-byte LDS row
 __device__ __forceinline__ int chunk_swizzle(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
@@ -103,32 +132,37 @@ __device__ __forceinline__ fi16x4_t lds_read_tr16(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
 }
 
-__device__ __forceinline__ ff32x16_t mfma32(fbf16x8_t a, fbf16x8_t b, ff32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
 struct FlashArgs {
-  const uint16_t* q;      // [B, T, H, 128] bf16
-  const uint16_t* kblk;   // [B, S, 128] bf16 (dequantised blocks)
-  const uint16_t* win;    // [B, Wt, 128] bf16
+  const uint16_t* q;      // [B, T, H, 128]
+  const uint16_t* kblk;   // [B, S, ROWB / 2]: dequantised blocks (K = V), or kv [B, S, 2, 128]
+  const uint16_t* win;    // [B, Wt, ROWB / 2] or null (Wt = 0)
   const int32_t* vis;     // [B * T] or null (all S)
   const int32_t* wstart;  // [B * T] or null (0)
   const int32_t* wlen;    // [B * T] or null (to the end of the window)
-  const float* sink;      // [H]
+  const void* sink;       // [H] or [1] of sink_dt (f32, or the input type)
+  int sink_dt, sink_scalar;
   int64_t S, Wt;
   int T;
   uint32_t gx;            // workgroups per sequence
   int H;
   float scale2;           // softmax scale * log2(e)
-  uint16_t* out;          // [B, T, H, 128] bf16
+  int n_split;            // source pieces per row block (1: the workgroup finishes its rows)
+  float* part;            // [B * T * H, n_split, 132]: max, sum (log2 units), 2 pad, O[128]
+  uint16_t* out;          // [B, T, H, 128]
 };
 
 // Two waves per SIMD (at most 256 registers per lane): the accumulators stay in VGPRs across the
 // loop (the matrix instructions take VGPR operands) instead of moving to AGPRs and back, and the
 // scheduler may spend registers on reading LDS operands ahead of the products.  A launch has about
 // 1.5 workgroups per CU at the bench shape, so more resident waves would not exist anyway.
-__global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void hca_prefill_flash_kernel(
+template <int DT, int ROWB>
+__global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_sink_attn_kernel(
     FlashArgs a) {
+  using Gm = FlashGeom<ROWB>;
+  using E = FlashElem<DT>;
+  using v8 = typename E::v8;
+  constexpr int kRowBytes = Gm::kRowBytes, kFTile = Gm::kTile, kKW = Gm::kKW, kKB = Gm::kKB;
+  constexpr int kCPR = Gm::kCPR, kChunks = Gm::kChunks, kVOff = Gm::kVOff;
   __shared__ __align__(16) uint8_t Ls[2][kTileBytes];  // [buffer][key][swizzled 16-byte chunks]
   __shared__ int s_rng[4][4];                          // per wave: max blocks, min blocks, window lo, hi
   __shared__ float s_ml[2][2][64];                     // key half 1's (m, l) per row half and lane
@@ -140,8 +174,11 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const uint32_t n_wg = gridDim.x;
   uint32_t wgi = blockIdx.x;
   if (n_wg % 8 == 0) wgi = (wgi % 8) * (n_wg / 8) + wgi / 8;
-  const int b = static_cast<int>(wgi / a.gx);
-  const int wrow = static_cast<int>(wgi % a.gx);
+  const uint32_t nsp = Gm::kSplit ? static_cast<uint32_t>(a.n_split) : 1u;
+  const uint32_t per_seq = a.gx * nsp;
+  const int b = static_cast<int>(wgi / per_seq);
+  const int wrow = static_cast<int>((wgi % per_seq) / nsp);
+  const int split = static_cast<int>(wgi % nsp);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int rh = wv & 1, kh = wv >> 1;  // row half, key half
   const int rl = lane & 31, hh = lane >> 5;
@@ -189,26 +226,36 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const int n_bt = (gmax + kFTile - 1) / kFTile;
   const int n_wt = whi > wlo ? (whi - wlo + kFTile - 1) / kFTile : 0;
   const int n_tiles = n_bt + n_wt;
+  // this workgroup's tiles [it0, it1): one piece of n_split
+  const int tps = (n_tiles + static_cast<int>(nsp) - 1) / static_cast<int>(nsp);
+  const int it0 = min(split * tps, n_tiles), it1 = min(it0 + tps, n_tiles);
 
   // the row's query as the B operand of S^T = K Q^T: dims 16 ks + 8 hh .. + 7
-  fbf16x8_t qb[8];
+  v8 qb[8];
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
     if (rv) v = *reinterpret_cast<const uint4*>(a.q + (static_cast<int64_t>(b) * RT + r) * kFD + 16 * ks + 8 * hh);
-    qb[ks] = __builtin_bit_cast(fbf16x8_t, v);
+    qb[ks] = __builtin_bit_cast(v8, v);
   }
   // the queries have landed before any tile load is issued: otherwise the wait for them, merged
   // over the loop's back edge, becomes a wait for every tile load on every iteration
   __builtin_amdgcn_s_waitcnt(0);
 
   // LDS byte offsets, fixed per lane (the tile and block offsets are multiples of 16 keys, which
-  // leave the swizzle unchanged, and become immediates).  Staging: thread tid moves chunk tid % 16
-  // of keys tid / 16 + 16 c.  Row-chunk reads: key kKW kh + 32 kb + rl, chunk 2 ks + hh.
-  // Transpose reads (16-lane group G = lane / 16, s = lane % 16): key kKW kh + 16 c + 4 hh + s / 4
-  // (+ 8 e), dims 32 mb + 16 (G % 2) + 4 (s % 4) .. + 3.
-  const int st_key = tid >> 4;
-  const int st_off = st_key * kRowBytes + (((tid & 15) ^ chunk_swizzle(st_key)) << 4);
+  // leave the swizzle unchanged, and become immediates).  The swizzle permutes the 16 chunks of
+  // each 256-byte half of a row.  Staging: thread tid moves chunk tid % kCPR of keys
+  // tid / kCPR + (256 / kCPR) c.  Row-chunk reads (K): key kKW kh + 32 kb + rl, chunk 2 ks + hh.
+  // Transpose reads (V, 16-lane group G = lane / 16, s = lane % 16): key kKW kh + 16 c + 4 hh +
+  // s / 4 (+ 8 e), dims 32 mb + 16 (G % 2) + 4 (s % 4) .. + 3.
+  // (passes c and c + 2 differ by 16 keys, which keeps the swizzle: two offsets cover every pass)
+  const int st_key = tid / kCPR, st_chunk = tid % kCPR;
+  int st_off[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int key = st_key + c * (kFThreads / kCPR);
+    st_off[c] = key * kRowBytes + (st_chunk & ~15) * 16 + (((st_chunk & 15) ^ chunk_swizzle(key & 15)) << 4);
+  }
   const int kbase = kKW * kh * kRowBytes;
   int soff[8];
 #pragma unroll
@@ -221,16 +268,16 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
       const int key = 4 * hh + (s16 >> 2) + 8 * e;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
-        toff[e][mb] = kbase + key * kRowBytes + (((4 * mb + 2 * (G & 1) + ((s16 & 3) >> 1)) ^ chunk_swizzle(key)) << 4) +
-                      8 * (s16 & 1);
+        toff[e][mb] = kbase + key * kRowBytes + kVOff +
+                      (((4 * mb + 2 * (G & 1) + ((s16 & 3) >> 1)) ^ chunk_swizzle(key)) << 4) + 8 * (s16 & 1);
     }
   }
 
-  const uint8_t* kseq = reinterpret_cast<const uint8_t*>(a.kblk + static_cast<int64_t>(b) * a.S * kFD);
-  const uint8_t* wseq = reinterpret_cast<const uint8_t*>(a.win + static_cast<int64_t>(b) * a.Wt * kFD);
+  const uint8_t* kseq = reinterpret_cast<const uint8_t*>(a.kblk) + static_cast<int64_t>(b) * a.S * kRowBytes;
+  const uint8_t* wseq = reinterpret_cast<const uint8_t*>(a.win) + static_cast<int64_t>(b) * a.Wt * kRowBytes;
   int voff[kChunks];  // thread tid's 16-byte chunks of a tile: bytes 16 tid + 4096 c
 #pragma unroll
-  for (int c = 0; c < kChunks; ++c) voff[c] = 16 * tid + 16 * kRowBytes * c;
+  for (int c = 0; c < kChunks; ++c) voff[c] = 16 * tid + 16 * kFThreads * c;
   // tile it: keys [base, base + TILE) of the blocks (it < n_bt) or of the window, read through a
   // buffer resource whose range ends at the workgroup's last source, so that the rows past it
   // read as zero (never attended) without a branch or an access.  A tile past the last has an
@@ -239,15 +286,16 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const bool blk = it < n_bt;
     const int base = blk ? it * kFTile : wlo + (it - n_bt) * kFTile;
     const int lim = blk ? gmax : whi;
-    const uint8_t* src = (blk ? kseq : wseq) + static_cast<int64_t>(it < n_tiles ? base : 0) * kRowBytes;
-    const int n_bytes = it < n_tiles ? min(lim - base, kFTile) * kRowBytes : 0;
+    const uint8_t* src = (blk ? kseq : wseq) + static_cast<int64_t>(it < it1 ? base : 0) * kRowBytes;
+    const int n_bytes = it < it1 ? min(lim - base, kFTile) * kRowBytes : 0;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), 0, n_bytes, kBufWord3);
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[c], 0, 0));
   };
   auto store_tile = [&](int buf, const uint4 (&v)[kChunks]) {
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) *reinterpret_cast<uint4*>(Ls[buf] + st_off + 16 * kRowBytes * c) = v[c];
+    for (int c = 0; c < kChunks; ++c)
+      *reinterpret_cast<uint4*>(Ls[buf] + st_off[c & 1] + 16 * kFThreads * (c & ~1)) = v[c];
   };
 
   // m_run: the row's running maximum over this wave's keys, in scaled log2 units (the same in both
@@ -256,14 +304,14 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   ff32x16_t O[4], lsum = {};
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) O[mb] = ff32x16_t{};
-  const fbf16x8_t ones = __builtin_bit_cast(fbf16x8_t, make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u));
+  const v8 ones = __builtin_bit_cast(v8, make_uint4(E::kOnePair, E::kOnePair, E::kOnePair, E::kOnePair));
 
   // Tiles are loaded kPrefetch tiles ahead into a ring of register sets (tile j in set j % kPrefetch)
   // and stored to LDS one tile ahead.
   uint4 nv[kPrefetch][kChunks];
 #pragma unroll
-  for (int j = 0; j < kPrefetch; ++j) load_tile(j, nv[j]);
-  if (n_tiles > 0) store_tile(0, nv[0]);
+  for (int j = 0; j < kPrefetch; ++j) load_tile(it0 + j, nv[j]);
+  if (it1 > it0) store_tile(0, nv[0]);
   __syncthreads();
   // one tile; buffer and register-set indices are compile-time constants (LDS offsets are
   // immediates, registers stay registers)
@@ -285,7 +333,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
         for (int u = 0; u < 4; ++u) kv[u] = *reinterpret_cast<const uint4*>(lt + 32 * kRowBytes * kb + soff[4 * k4 + u]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) s[kb] = mfma32(__builtin_bit_cast(fbf16x8_t, kv[u]), qb[4 * k4 + u], s[kb]);
+        for (int u = 0; u < 4; ++u) s[kb] = E::mma(__builtin_bit_cast(v8, kv[u]), qb[4 * k4 + u], s[kb]);
       }
     }
     // masks (only where some row of the workgroup does not see the whole tile)
@@ -329,31 +377,30 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         float p[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * c + j], a.scale2, nm));
-        const fbf16x8_t pb = __builtin_bit_cast(
-            fbf16x8_t, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                                  pack_bf16x2(p[6], p[7])));
-        lsum = mfma32(ones, pb, lsum);
-        fbf16x8_t va[4];  // the chunk's V^T operands, read before their products
+        const v8 pb = __builtin_bit_cast(
+            v8, make_uint4(E::pack(p[0], p[1]), E::pack(p[2], p[3]), E::pack(p[4], p[5]), E::pack(p[6], p[7])));
+        lsum = E::mma(ones, pb, lsum);
+        v8 va[4];  // the chunk's V^T operands, read before their products
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
           const uint8_t* q0 = lt + (32 * kb + 16 * c) * kRowBytes;
           const fi16x4_t lo4 = lds_read_tr16(q0 + toff[0][mb]);
           const fi16x4_t hi4 = lds_read_tr16(q0 + toff[1][mb]);
-          va[mb] = __builtin_bit_cast(fbf16x8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+          va[mb] = __builtin_bit_cast(v8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
         }
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) O[mb] = mfma32(va[mb], pb, O[mb]);
+        for (int mb = 0; mb < 4; ++mb) O[mb] = E::mma(va[mb], pb, O[mb]);
       }
     // the other buffer was last read before the previous barrier
-    if (it + 1 < n_tiles) store_tile(buf ^ 1, nv[nset]);
+    if (it + 1 < it1) store_tile(buf ^ 1, nv[nset]);
     __syncthreads();
   };
   // unrolled over the two buffers so that both indices are constants (a skipped second step
   // leaves the loop, so it does not blur the wait counts on the back edge)
 #pragma unroll 1
-  for (int it = 0; it < n_tiles; it += 2) {
+  for (int it = it0; it < it1; it += 2) {
     step(it, IntC<0>{}, IntC<0>{});
-    if (it + 1 < n_tiles) step(it + 1, IntC<1>{}, IntC<1 % kPrefetch>{});
+    if (it + 1 < it1) step(it + 1, IntC<1>{}, IntC<1 % kPrefetch>{});
   }
 
   // merge the two key halves of each row half (through the tile buffers, free after the last
@@ -374,8 +421,32 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const float f0 = m_run == kFNegInf ? 0.0f : exp2f(m_run - mm);
   const float f1 = m1 == kFNegInf ? 0.0f : exp2f(m1 - mm);
   const float l_run = lsum[0] * f0 + l1 * f1;
+  if (Gm::kSplit && nsp > 1) {
+    // one piece: the row's (max, sum, O) relative to mm, merged with the sink by the combine
+    float* dst = a.part + ((static_cast<int64_t>(b) * RT + r) * a.n_split + split) * (kFD + 4);
+    if (hh == 0) {
+      dst[0] = mm;
+      dst[1] = l_run;
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float4 o;
+        o.x = O[mb][4 * q] * f0 + ob[(mb * 16 + 4 * q) * 64 + lane] * f1;
+        o.y = O[mb][4 * q + 1] * f0 + ob[(mb * 16 + 4 * q + 1) * 64 + lane] * f1;
+        o.z = O[mb][4 * q + 2] * f0 + ob[(mb * 16 + 4 * q + 2) * 64 + lane] * f1;
+        o.w = O[mb][4 * q + 3] * f0 + ob[(mb * 16 + 4 * q + 3) * 64 + lane] * f1;
+        *reinterpret_cast<float4*>(dst + 4 + 32 * mb + 8 * q + 4 * hh) = o;
+      }
+    return;
+  }
   // the sink, counted once: out = O / (l + e^{sink - m}) with m = max(mm, sink)
-  const float sk = a.sink[h] * kLog2e;
+  const int sh = a.sink_scalar ? 0 : h;
+  const float skv = a.sink_dt == AEKV_F32   ? static_cast<const float*>(a.sink)[sh]
+                    : a.sink_dt == AEKV_F16 ? f16_to_f32(static_cast<const uint16_t*>(a.sink)[sh])
+                                            : bf16_to_f32(static_cast<const uint16_t*>(a.sink)[sh]);
+  const float sk = skv * kLog2e;
   const float mf = fmaxf(mm, sk);
   const float fo = mm == kFNegInf ? 0.0f : exp2f(mm - mf);
   const float L = fmaf(l_run, fo, exp2f(sk - mf));
@@ -391,7 +462,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         const int v = 4 * q + i;
         o[i] = O[mb][v] * rs0 + ob[(mb * 16 + v) * 64 + lane] * rs1;
       }
-      *reinterpret_cast<uint2*>(orow + 32 * mb + 8 * q + 4 * hh) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+      *reinterpret_cast<uint2*>(orow + 32 * mb + 8 * q + 4 * hh) = make_uint2(E::pack(o[0], o[1]), E::pack(o[2], o[3]));
     }
 }
 
@@ -403,18 +474,35 @@ size_t hca_prefill_flash_workspace(int64_t B, int64_t S) {
 
 bool hca_prefill_flash_supported(int64_t H, int64_t D) { return D == kFD && H >= 1; }
 
+namespace {
+
+// Grid and index limits shared by both callers; fills the launch fields of a.
+int flash_prepare(FlashArgs& a, int64_t B, int64_t T, int64_t H, int64_t S, int64_t Wt, int tile, float softmax_scale,
+                  const char* who) {
+  const int64_t RT = T * H;
+  const int64_t gx = ceil_div(RT, kFRows);
+  if (gx * B > 0x7fffffff || RT > 0x7fffffff - kFRows) return fail(AEKV_ERR_UNSUPPORTED, "%s: grid too large", who);
+  if (S > 0x7fffffff - tile || Wt > 0x7fffffff - tile)
+    return fail(AEKV_ERR_UNSUPPORTED, "%s: %lld sources / %lld window entries exceed the int32 indexing", who,
+                (long long)S, (long long)Wt);
+  a.T = static_cast<int>(T);
+  a.S = S;
+  a.Wt = Wt;
+  a.H = static_cast<int>(H);
+  a.scale2 = softmax_scale * kLog2e;
+  a.gx = static_cast<uint32_t>(gx);
+  return AEKV_OK;
+}
+
+}  // namespace
+
 int launch_hca_prefill_flash(const void* q, const void* kblk, const void* window, const int32_t* vis,
                              const int32_t* wstart, const int32_t* wlen, const float* sink, int64_t B, int64_t T,
                              int64_t H, int64_t S, int64_t Wt, float softmax_scale, void* out, hipStream_t st,
                              const char* who) {
-  const int64_t RT = T * H;
-  const int64_t gx = ceil_div(RT, kFRows);
-  if (gx * B > 0x7fffffff || RT > 0x7fffffff - kFRows) return fail(AEKV_ERR_UNSUPPORTED, "%s: grid too large", who);
-  if (S > 0x7fffffff - kFTile || Wt > 0x7fffffff - kFTile)
-    return fail(AEKV_ERR_UNSUPPORTED, "%s: %lld blocks / %lld window entries exceed the int32 indexing", who,
-                (long long)S, (long long)Wt);
-  if (RT == 0 || B == 0) return AEKV_OK;
   FlashArgs a{};
+  if (int rc = flash_prepare(a, B, T, H, S, Wt, FlashGeom<256>::kTile, softmax_scale, who)) return rc;
+  if (T * H == 0 || B == 0) return AEKV_OK;
   a.q = static_cast<const uint16_t*>(q);
   a.kblk = static_cast<const uint16_t*>(kblk);
   a.win = static_cast<const uint16_t*>(window);
@@ -422,14 +510,37 @@ int launch_hca_prefill_flash(const void* q, const void* kblk, const void* window
   a.wstart = wstart;
   a.wlen = wlen;
   a.sink = sink;
-  a.T = static_cast<int>(T);
-  a.S = S;
-  a.Wt = Wt;
-  a.H = static_cast<int>(H);
-  a.scale2 = softmax_scale * kLog2e;
+  a.sink_dt = AEKV_F32;
+  a.sink_scalar = 0;
+  a.n_split = 1;
   a.out = static_cast<uint16_t*>(out);
-  a.gx = static_cast<uint32_t>(gx);
-  hipLaunchKernelGGL(hca_prefill_flash_kernel, dim3(static_cast<uint32_t>(gx * B)), dim3(kFThreads), 0, st, a);
+  hipLaunchKernelGGL((flash_sink_attn_kernel<AEKV_BF16, 256>), dim3(a.gx * static_cast<uint32_t>(B)), dim3(kFThreads),
+                     0, st, a);
+  return check_launch(who);
+}
+
+int64_t dense_flash_row_blocks(int64_t T, int64_t H) { return ceil_div(T * H, kFRows); }
+int64_t dense_flash_tile() { return FlashGeom<512>::kTile; }
+
+int launch_dense_flash_attention(const void* q, const void* kv, const void* sink, int sink_scalar, int32_t dtype,
+                                 int64_t B, int64_t T, int64_t H, int64_t S, float softmax_scale, int n_split,
+                                 float* part, void* out, hipStream_t st, const char* who) {
+  FlashArgs a{};
+  if (int rc = flash_prepare(a, B, T, H, S, 0, FlashGeom<512>::kTile, softmax_scale, who)) return rc;
+  if (T * H == 0 || B == 0) return AEKV_OK;
+  if (n_split < 1 || (n_split > 1 && !part)) return fail(AEKV_ERR_VALUE, "%s: bad source split", who);
+  if (static_cast<int64_t>(a.gx) * B * n_split > 0x7fffffff) return fail(AEKV_ERR_UNSUPPORTED, "%s: grid too large", who);
+  a.n_split = n_split;
+  a.part = part;
+  a.q = static_cast<const uint16_t*>(q);
+  a.kblk = static_cast<const uint16_t*>(kv);
+  a.sink = sink;
+  a.sink_dt = dtype;
+  a.sink_scalar = sink_scalar;
+  a.out = static_cast<uint16_t*>(out);
+  const dim3 grid(a.gx * static_cast<uint32_t>(B) * static_cast<uint32_t>(n_split));
+  if (dtype == AEKV_F16) hipLaunchKernelGGL((flash_sink_attn_kernel<AEKV_F16, 512>), grid, dim3(kFThreads), 0, st, a);
+  else hipLaunchKernelGGL((flash_sink_attn_kernel<AEKV_BF16, 512>), grid, dim3(kFThreads), 0, st, a);
   return check_launch(who);
 }
 

@@ -4,8 +4,9 @@
 //    semantics aether_kernels/csrc/sparse_sink_attention_cuda.cu:47-114, oracle
 //    aether_pipeline/serving.py:99-130) and, with dense indices, for tiled_prefill_attention
 //    (aether_kernels/sparse_attention.py:19-42) with the sink counted once as in
-//    aether_2b/modeling.py:158-178.  One wave per (b, t, h); keys streamed in tiles of 64 with an
-//    online softmax; the sink joins the normaliser once at the end.
+//    aether_2b/modeling.py:158-178, for fp32 inputs and head dims other than 128 (bf16/fp16 at
+//    head_dim 128 run on the matrix cores, sink_attention_mfma.hip).  One wave per (b, t, h); keys
+//    streamed in tiles of 64 with an online softmax; the sink joins the normaliser once at the end.
 // 2. quant_attn_partial_kernel + quant_attn_combine_kernel — one decode token per row over
 //    TurboQuant-compressed shared K=V blocks (selected by the CSA indexer, or all blocks for HCA)
 //    plus a bf16 sliding window (aether_2b/serving.py:507-522, :597-625).  Split-KV: each workgroup
@@ -354,7 +355,7 @@ int launch_sparse(int idx_kind, const void* q, const void* kv, const void* topk,
 
 int sparse_common(const void* q, const void* kv, const void* topk, int idx_kind, const void* sink, int64_t sink_numel,
                   int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D, int64_t S, int64_t K, float scale,
-                  void* out, void* stream, const char* who) {
+                  void* ws, size_t ws_bytes, void* out, void* stream, const char* who) {
   if (!is_float_dtype(dtype)) return fail(AEKV_ERR_DTYPE, "%s: dtype %d is not f32/f16/bf16", who, dtype);
   if (B < 0 || T < 0 || H < 0 || D < 0 || S < 0 || K < 0) return fail(AEKV_ERR_SHAPE, "%s: negative size", who);
   if (D > kMaxD) return fail(AEKV_ERR_UNSUPPORTED, "%s: head_dim %lld exceeds %d", who, (long long)D, kMaxD);
@@ -367,6 +368,10 @@ int sparse_common(const void* q, const void* kv, const void* topk, int idx_kind,
     return fail(AEKV_ERR_VALUE, "%s: null pointer", who);
   const hipStream_t st = as_stream(stream);
   const int scalar = sink_numel == 1 ? 1 : 0;
+  if (sink_attention_mfma_supported(dtype, D) && is_aligned(q, 16) && is_aligned(out, 8) &&
+      (K == 0 || is_aligned(kv, 16)) && is_aligned(sink, 2))
+    return sink_attention_mfma(q, kv, topk, idx_kind, sink, scalar, dtype, B, T, H, S, K, scale, ws, ws_bytes, out, st,
+                               who);
   if (dtype == AEKV_F32) launch_sparse<AEKV_F32>(idx_kind, q, kv, topk, sink, scalar, B, T, H, D, S, K, scale, out, st);
   else if (dtype == AEKV_F16) launch_sparse<AEKV_F16>(idx_kind, q, kv, topk, sink, scalar, B, T, H, D, S, K, scale, out, st);
   else launch_sparse<AEKV_BF16>(idx_kind, q, kv, topk, sink, scalar, B, T, H, D, S, K, scale, out, st);
@@ -395,21 +400,44 @@ QLayout qlayout(int64_t B, int64_t H, int64_t D, int64_t n_comp, int64_t W) {
 
 using namespace aekv;
 
+extern "C" int aekv_sparse_sink_attention_ws(const void* q, const void* kv, const void* topk, int32_t idx_dtype,
+                                             const void* sink, int64_t sink_numel, int32_t dtype, int64_t B,
+                                             int64_t T, int64_t H, int64_t D, int64_t S, int64_t K,
+                                             float softmax_scale, void* ws, size_t ws_bytes, void* out,
+                                             void* stream) {
+  if (idx_dtype != AEKV_I32 && idx_dtype != AEKV_I64) return fail(AEKV_ERR_DTYPE, "topk_indices must be int32 or int64");
+  return sparse_common(q, kv, topk, idx_dtype == AEKV_I32 ? 4 : 8, sink, sink_numel, dtype, B, T, H, D, S, K,
+                       softmax_scale, ws, ws_bytes, out, stream, "aekv_sparse_sink_attention");
+}
+
 extern "C" int aekv_sparse_sink_attention(const void* q, const void* kv, const void* topk, int32_t idx_dtype,
                                           const void* sink, int64_t sink_numel, int32_t dtype, int64_t B, int64_t T,
                                           int64_t H, int64_t D, int64_t S, int64_t K, float softmax_scale, void* out,
                                           void* stream) {
-  if (idx_dtype != AEKV_I32 && idx_dtype != AEKV_I64) return fail(AEKV_ERR_DTYPE, "topk_indices must be int32 or int64");
-  return sparse_common(q, kv, topk, idx_dtype == AEKV_I32 ? 4 : 8, sink, sink_numel, dtype, B, T, H, D, S, K,
-                       softmax_scale, out, stream, "aekv_sparse_sink_attention");
+  return aekv_sparse_sink_attention_ws(q, kv, topk, idx_dtype, sink, sink_numel, dtype, B, T, H, D, S, K,
+                                       softmax_scale, nullptr, 0, out, stream);
+}
+
+extern "C" int aekv_tiled_prefill_attention_ws(const void* q, const void* kv, const void* sink, int64_t sink_numel,
+                                               int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D, int64_t S,
+                                               float softmax_scale, int32_t tile_size, void* ws, size_t ws_bytes,
+                                               void* out, void* stream) {
+  if (tile_size <= 0) return fail(AEKV_ERR_VALUE, "tile_size must be positive");
+  return sparse_common(q, kv, nullptr, 0, sink, sink_numel, dtype, B, T, H, D, S, S, softmax_scale, ws, ws_bytes, out,
+                       stream, "aekv_tiled_prefill_attention");
 }
 
 extern "C" int aekv_tiled_prefill_attention(const void* q, const void* kv, const void* sink, int64_t sink_numel,
                                             int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D, int64_t S,
                                             float softmax_scale, int32_t tile_size, void* out, void* stream) {
-  if (tile_size <= 0) return fail(AEKV_ERR_VALUE, "tile_size must be positive");
-  return sparse_common(q, kv, nullptr, 0, sink, sink_numel, dtype, B, T, H, D, S, S, softmax_scale, out, stream,
-                       "aekv_tiled_prefill_attention");
+  return aekv_tiled_prefill_attention_ws(q, kv, sink, sink_numel, dtype, B, T, H, D, S, softmax_scale, tile_size,
+                                         nullptr, 0, out, stream);
+}
+
+extern "C" size_t aekv_sink_attention_workspace_size(int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D,
+                                                     int64_t S, int64_t K) {
+  if (!sink_attention_mfma_supported(dtype, D) || B <= 0 || T <= 0 || H <= 0 || S < 0) return 0;
+  return K < 0 ? sink_attention_mfma_workspace(true, B, T, H, S, S) : sink_attention_mfma_workspace(false, B, T, H, S, K);
 }
 
 extern "C" size_t aekv_quant_attention_workspace_size(int64_t B, int64_t H, int64_t D, int64_t n_comp, int64_t W) {

@@ -166,6 +166,20 @@ int aekv_sparse_sink_attention(const void* q, const void* kv, const void* topk, 
                                int64_t B, int64_t T, int64_t H, int64_t D, int64_t S, int64_t K,
                                float softmax_scale, void* out, void* stream);
 
+/* The same, with a caller-owned workspace (the binding's own allocation in the reference,
+ * bindings.cpp:21-46, happens in the caller here): bf16/fp16 calls at D = 128 whose launch would
+ * leave most CUs idle split each target's sources over several workgroups and merge the pieces.
+ * ws_bytes from aekv_sink_attention_workspace_size(dtype, B, T, H, D, S, K); ws = NULL runs unsplit
+ * (the entry point above); a non-NULL ws must be 256-byte aligned and large enough. */
+int aekv_sparse_sink_attention_ws(const void* q, const void* kv, const void* topk, int32_t idx_dtype,
+                                  const void* sink, int64_t sink_numel, int32_t dtype,
+                                  int64_t B, int64_t T, int64_t H, int64_t D, int64_t S, int64_t K,
+                                  float softmax_scale, void* ws, size_t ws_bytes, void* out, void* stream);
+/* Workspace bytes for the split of aekv_sparse_sink_attention_ws (K sources per target) or, with
+ * K < 0, aekv_tiled_prefill_attention_ws (every target over all S sources); 0: no split. */
+size_t aekv_sink_attention_workspace_size(int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D, int64_t S,
+                                          int64_t K);
+
 /* Sink attention of one bf16 query token per row over TurboQuant-compressed shared K=V blocks plus
  * a bf16 sliding window (the serving engine's decode step, dequantise + gather + concat + attend
  * fused):
@@ -260,6 +274,12 @@ int aekv_rope_rmsnorm(const void* x, int64_t rows, int32_t heads, int32_t d, con
 int aekv_tiled_prefill_attention(const void* q, const void* kv, const void* sink, int64_t sink_numel,
                                  int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D, int64_t S,
                                  float softmax_scale, int32_t tile_size, void* out, void* stream);
+/* The same with a caller-owned workspace (size: aekv_sink_attention_workspace_size(..., K = -1));
+ * see aekv_sparse_sink_attention_ws. */
+int aekv_tiled_prefill_attention_ws(const void* q, const void* kv, const void* sink, int64_t sink_numel,
+                                    int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D, int64_t S,
+                                    float softmax_scale, int32_t tile_size, void* ws, size_t ws_bytes, void* out,
+                                    void* stream);
 
 #ifdef __cplusplus
 }

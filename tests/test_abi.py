@@ -130,6 +130,30 @@ def test_attention_argument_errors(lib):
     assert rc == L.ERR_SHAPE
 
 
+def test_sink_attention_split_workspace(lib):
+    ws = lib.aekv_sink_attention_workspace_size
+    # no split: fp32 and other head dims (VALU kernel), launches that already fill the GPU
+    assert ws(L.F32, 1, 1, 16, 128, 640, -1) == 0
+    assert ws(L.BF16, 1, 1, 16, 64, 640, -1) == 0
+    assert ws(L.F16, 1, 128, 16, 128, 8192, 64) == 0          # the report shape: 128 targets x 2 groups
+    assert ws(L.BF16, 8, 1, 16, 128, 100, 100) == 0           # <= 4 groups of 32 per target
+    # one target over 640 sources: 20 groups -> 5 pieces of 4; the combine's rows are (target, head)
+    assert ws(L.BF16, 1, 1, 16, 128, 640, -1) == 16 * 5 * 132 * 4
+    assert ws(L.BF16, 1, 1, 16, 128, 9999, 640) == 16 * 5 * 132 * 4
+    # T = 256 targets x 16 heads over 8192 sources: 64 flash workgroups -> 8 pieces of 16 tiles
+    assert ws(L.BF16, 1, 256, 16, 128, 8192, -1) == 256 * 16 * 8 * 132 * 4
+    need = ws(L.BF16, 1, 1, 16, 128, 640, -1)
+    rc = lib.aekv_tiled_prefill_attention_ws(FAKE, FAKE, FAKE, 16, L.BF16, 1, 1, 16, 128, 640, 0.1, 256, FAKE,
+                                             need - 1, FAKE, None)
+    assert rc == L.ERR_WORKSPACE and "workspace" in _err(lib)
+    rc = lib.aekv_tiled_prefill_attention_ws(FAKE, FAKE, FAKE, 16, L.BF16, 1, 1, 16, 128, 640, 0.1, 256,
+                                             ctypes.c_void_p(0x10010), need, FAKE, None)
+    assert rc == L.ERR_ALIGN
+    rc = lib.aekv_sparse_sink_attention_ws(FAKE, FAKE, FAKE, L.I32, FAKE, 16, L.F16, 1, 1, 16, 128, 9999, 640, 0.1,
+                                           FAKE, need - 1, FAKE, None)
+    assert rc == L.ERR_WORKSPACE
+
+
 # ---- python surface (host validation, no device) ---------------------------------------------
 def test_polarquant_rejects_bad_bits():
     with pytest.raises(ValueError, match="bits must be 4 or 8"):

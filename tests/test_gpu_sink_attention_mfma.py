@@ -1,0 +1,148 @@
+"""GPU parity of the drop-in attention entry points on their matrix-core path (head_dim 128,
+bf16/fp16) against the oracle.
+
+sparse_sink_attention and tiled_prefill_attention at head_dim 128 in bf16/fp16 run on the matrix
+cores; the tolerance is the reference's own for its CUDA kernel against the torch backend,
+atol = rtol = 5e-3 for fp16/bf16 (tests/test_cuda_runtime.py:33-35 in the reference).  The oracle is
+aether_pipeline/serving.py:99-130 in fp32 with the CUDA kernel's skip of out-of-range indices.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import aetherkv._lib as L
+import oracle as O
+from aetherkv import sparse_sink_attention, tiled_prefill_attention
+from conftest import to_np_f32
+
+pytestmark = pytest.mark.gpu
+
+TOL = 5e-3
+
+
+def _close(got: torch.Tensor, want: np.ndarray):
+    np.testing.assert_allclose(to_np_f32(got), want, rtol=TOL, atol=TOL)
+
+
+def _inputs(seed, B, T, H, S, K, dtype, idx_dtype=torch.int64, lo=0, hi=None, qscale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, T, H, 128, generator=g) * qscale).to(dtype)
+    kv = torch.randn(B, S, 2, 128, generator=g).to(dtype)
+    topk = torch.randint(lo, S if hi is None else hi, (B, T, K), generator=g, dtype=idx_dtype)
+    sink = torch.randn(H, generator=g).to(dtype)
+    return q, kv, topk, sink
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("H,K", [(16, 64), (16, 1), (8, 31), (16, 100), (20, 257), (3, 520)])
+def test_sparse_matrix_core_shapes(dev, dtype, idx_dtype, H, K):
+    # K covers one partial group, 2 / 4 / 8 waves per workgroup and several groups per wave; H = 20
+    # takes two head groups (the second partial), H = 3 and 8 partial columns
+    q, kv, topk, sink = _inputs(11 + H + K, 3, 5, H, 700, K, dtype, idx_dtype)
+    got = sparse_sink_attention(q.to(dev), kv.to(dev), topk.to(dev), sink.to(dev), 128 ** -0.5)
+    assert got.dtype == dtype and got.shape == q.shape
+    want = O.sink_attention(to_np_f32(q), to_np_f32(kv), topk.numpy(), to_np_f32(sink), 128 ** -0.5)
+    _close(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_sparse_matrix_core_invalid_duplicate_and_empty(dev, dtype):
+    q, kv, topk, sink = _inputs(21, 2, 4, 16, 90, 150, dtype, lo=-20, hi=110)  # ~30% skipped
+    topk[0, 1] = -1                                                          # no valid source
+    topk[1, 2] = 7                                                           # one source, 150 times
+    sink_s = sink[:1].clone()                                                # scalar sink
+    got = sparse_sink_attention(q.to(dev), kv.to(dev), topk.to(dev), sink_s.to(dev), 0.09)
+    want = O.sink_attention(to_np_f32(q), to_np_f32(kv), topk.numpy(), to_np_f32(sink_s), 0.09)
+    _close(got, want)
+    assert not bool(got[0, 1].float().abs().sum())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_sparse_matrix_core_peaked_logits_and_sink(dev, dtype):
+    # large logits (a few keys dominate: the running maximum moves between groups) and sinks that
+    # dominate some heads
+    q, kv, topk, sink = _inputs(23, 2, 3, 16, 500, 384, dtype, qscale=4.0)
+    sink = (torch.arange(16) - 8.0).to(dtype) * 3.0
+    got = sparse_sink_attention(q.to(dev), kv.to(dev), topk.to(dev), sink.to(dev), 128 ** -0.5)
+    want = O.sink_attention(to_np_f32(q), to_np_f32(kv), topk.numpy(), to_np_f32(sink), 128 ** -0.5)
+    _close(got, want)
+
+
+def test_sparse_matrix_core_no_sources(dev):
+    # K = 0: every output is zero (the sink alone)
+    q, kv, _, sink = _inputs(25, 2, 3, 16, 40, 1, torch.bfloat16)
+    topk = torch.empty(2, 3, 0, dtype=torch.int64)
+    got = sparse_sink_attention(q.to(dev), kv.to(dev), topk.to(dev), sink.to(dev), 0.1)
+    assert not bool(got.float().abs().sum())
+
+
+def test_sparse_matrix_core_matches_fp32_path(dev):
+    # the same inputs through the fp32 VALU kernel (inputs widened exactly): the two paths agree to
+    # the bf16 output rounding plus the weights' rounding
+    q, kv, topk, sink = _inputs(27, 2, 8, 16, 1000, 200, torch.bfloat16)
+    got = sparse_sink_attention(q.to(dev), kv.to(dev), topk.to(dev), sink.to(dev), 128 ** -0.5)
+    ref = sparse_sink_attention(q.float().to(dev), kv.float().to(dev), topk.to(dev), sink.float().to(dev), 128 ** -0.5)
+    np.testing.assert_allclose(to_np_f32(got), to_np_f32(ref), rtol=TOL, atol=TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,T,S", [(1, 1, 640), (4, 1, 200), (2, 3, 33)])
+def test_tiled_prefill_matrix_core_model_calls(dev, dtype, B, T, S):
+    # modeling.py:322,534 calls tiled_prefill_attention per target: q [B, 1, H, D] over the
+    # target's [blocks; window] sources stacked as K = V
+    g = torch.Generator().manual_seed(31 + S)
+    q = torch.randn(B, T, 16, 128, generator=g).to(dtype)
+    src = torch.randn(B, S, 128, generator=g).to(dtype)
+    kv = torch.stack([src, src], dim=2)
+    sink = torch.randn(16, generator=g).to(dtype)
+    got = tiled_prefill_attention(q.to(dev), kv.to(dev), sink.to(dev), 128 ** -0.5, tile_size=256)
+    idx = np.broadcast_to(np.arange(S), (B, T, S))
+    want = O.sink_attention(to_np_f32(q), to_np_f32(kv), idx, to_np_f32(sink), 128 ** -0.5)
+    _close(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_tiled_prefill_matrix_core_prefill_shape(dev, dtype):
+    # T = 256 targets over S = 8192 sources, 16 heads, separate K and V
+    g = torch.Generator().manual_seed(37)
+    B, T, H, S = 1, 256, 16, 8192
+    q = torch.randn(B, T, H, 128, generator=g).to(dtype)
+    kv = torch.randn(B, S, 2, 128, generator=g).to(dtype)
+    sink = torch.randn(H, generator=g).to(dtype)
+    got = tiled_prefill_attention(q.to(dev), kv.to(dev), sink.to(dev), 128 ** -0.5, tile_size=256)
+    idx = np.broadcast_to(np.arange(S), (B, T, S))
+    want = O.sink_attention(to_np_f32(q), to_np_f32(kv), idx, to_np_f32(sink), 128 ** -0.5, threads=16)
+    _close(got, want)
+
+
+@pytest.mark.parametrize("B,T,S", [(1, 1, 640), (1, 256, 4096)])
+def test_unsplit_entry_points(dev, B, T, S):
+    # the reference-signature C entry points (no workspace: one workgroup per target, or per row
+    # block, over all its sources) against the oracle, at shapes the wrappers split
+    assert L.lib().aekv_sink_attention_workspace_size(L.BF16, B, T, 16, 128, S, -1) > 0
+    g = torch.Generator().manual_seed(41 + T)
+    q = torch.randn(B, T, 16, 128, generator=g).to(torch.bfloat16)
+    kv = torch.randn(B, S, 2, 128, generator=g).to(torch.bfloat16)
+    sink = torch.randn(16, generator=g).to(torch.bfloat16)
+    topk = torch.randint(0, S, (B, T, S), generator=g, dtype=torch.int32)
+    qd, kvd, sd, td = q.to(dev), kv.to(dev), sink.to(dev), topk.to(dev)
+    out_d = torch.empty_like(qd)
+    out_s = torch.empty_like(qd)
+    with torch.cuda.device(dev):
+        L.check(L.lib().aekv_tiled_prefill_attention(L.ptr(qd), L.ptr(kvd), L.ptr(sd), 16, L.BF16, B, T, 16, 128, S,
+                                                     128 ** -0.5, 256, L.ptr(out_d), L.stream_of(qd)), "tiled")
+        L.check(L.lib().aekv_sparse_sink_attention(L.ptr(qd), L.ptr(kvd), L.ptr(td), L.I32, L.ptr(sd), 16, L.BF16, B,
+                                                   T, 16, 128, S, S, 128 ** -0.5, L.ptr(out_s), L.stream_of(qd)),
+                "sparse")
+    torch.cuda.synchronize()
+    want_d = O.sink_attention(to_np_f32(q), to_np_f32(kv), np.broadcast_to(np.arange(S), (B, T, S)),
+                              to_np_f32(sink), 128 ** -0.5, threads=16)
+    _close(out_d, want_d)
+    if T == 1:
+        want_s = O.sink_attention(to_np_f32(q), to_np_f32(kv), topk.numpy(), to_np_f32(sink), 128 ** -0.5)
+        _close(out_s, want_s)
+        # and the wrapper (split into pieces) on the same call
+        _close(sparse_sink_attention(qd, kvd, td, sd, 128 ** -0.5), want_s)
