@@ -19,7 +19,8 @@
 //
 // Work split.  A workgroup (4 waves) owns 64 consecutive rows.  The sources of its targets
 // (blocks [0, max g), window [min start, max end)) stream through LDS in tiles of TILE keys,
-// row-major (key, 128 dims), in two alternating buffers (one barrier per tile).  Wave w takes row
+// row-major (key, 128 dims), in two alternating buffers (one barrier per tile), loaded by buffer
+// loads that write LDS directly (no register staging), one tile ahead.  Wave w takes row
 // half w % 2 (32 rows, lane l holds row l % 32) and key half w / 2 of every tile, so each wave
 // reads half a tile per step for 32 rows: with v_mfma_f32_32x32x16_bf16 every LDS byte feeds
 // twice the matrix work of a 16-row wave over the whole tile.  The two waves of a row half keep
@@ -58,13 +59,13 @@ constexpr int kTileBytes = 32768;     // one LDS tile buffer
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kFNegInf = -__builtin_inff();
 constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: raw 32-bit data, range-checked
-constexpr int kPrefetch = 1;           // tiles in flight from memory (2 spills registers)
 
 typedef __attribute__((ext_vector_type(8))) __bf16 fbf16x8_t;
 typedef __attribute__((ext_vector_type(8))) _Float16 ff16x8_t;
 typedef __attribute__((ext_vector_type(16))) float ff32x16_t;
 typedef __attribute__((ext_vector_type(4))) short fi16x4_t;
 typedef __attribute__((address_space(3))) fi16x4_t lds_i16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Source rows of ROWB bytes: 256 (K = V) or 512 (K, then V).  A tile holds kTile rows (32 KB).
 template <int ROWB>
@@ -74,7 +75,6 @@ struct FlashGeom {
   static constexpr int kTile = kTileBytes / ROWB;       // sources per tile (128 or 64)
   static constexpr int kKW = kTile / 2;                 // sources per wave and tile
   static constexpr int kKB = kKW / 32;                  // 32-key score blocks per wave and tile
-  static constexpr int kCPR = ROWB / 16;                // 16-byte chunks per row
   static constexpr int kChunks = kTileBytes / (16 * kFThreads);  // staging chunks per thread and tile
   static constexpr int kVOff = ROWB == 256 ? 0 : 256;   // V's byte offset in a row
   static constexpr bool kSplit = ROWB == 512;           // the dense caller may split a row's sources
@@ -162,8 +162,11 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   using E = FlashElem<DT>;
   using v8 = typename E::v8;
   constexpr int kRowBytes = Gm::kRowBytes, kFTile = Gm::kTile, kKW = Gm::kKW, kKB = Gm::kKB;
-  constexpr int kCPR = Gm::kCPR, kChunks = Gm::kChunks, kVOff = Gm::kVOff;
-  __shared__ __align__(16) uint8_t Ls[2][kTileBytes];  // [buffer][key][swizzled 16-byte chunks]
+  constexpr int kChunks = Gm::kChunks, kVOff = Gm::kVOff;
+  // the two tile buffers, [key][swizzled 16-byte chunks]: separate arrays, so that the compiler
+  // sees that the loads into one do not write what is read from the other
+  __shared__ __align__(16) uint8_t Ls0[kTileBytes];
+  __shared__ __align__(16) uint8_t Ls1[kTileBytes];
   __shared__ int s_rng[4][4];                          // per wave: max blocks, min blocks, window lo, hi
   __shared__ float s_ml[2][2][64];                     // key half 1's (m, l) per row half and lane
 
@@ -244,18 +247,9 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
   // LDS byte offsets, fixed per lane (the tile and block offsets are multiples of 16 keys, which
   // leave the swizzle unchanged, and become immediates).  The swizzle permutes the 16 chunks of
-  // each 256-byte half of a row.  Staging: thread tid moves chunk tid % kCPR of keys
-  // tid / kCPR + (256 / kCPR) c.  Row-chunk reads (K): key kKW kh + 32 kb + rl, chunk 2 ks + hh.
+  // each 256-byte half of a row.  Row-chunk reads (K): key kKW kh + 32 kb + rl, chunk 2 ks + hh.
   // Transpose reads (V, 16-lane group G = lane / 16, s = lane % 16): key kKW kh + 16 c + 4 hh +
   // s / 4 (+ 8 e), dims 32 mb + 16 (G % 2) + 4 (s % 4) .. + 3.
-  // (passes c and c + 2 differ by 16 keys, which keeps the swizzle: two offsets cover every pass)
-  const int st_key = tid / kCPR, st_chunk = tid % kCPR;
-  int st_off[2];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int key = st_key + c * (kFThreads / kCPR);
-    st_off[c] = key * kRowBytes + (st_chunk & ~15) * 16 + (((st_chunk & 15) ^ chunk_swizzle(key & 15)) << 4);
-  }
   const int kbase = kKW * kh * kRowBytes;
   int soff[8];
 #pragma unroll
@@ -275,14 +269,27 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
   const uint8_t* kseq = reinterpret_cast<const uint8_t*>(a.kblk) + static_cast<int64_t>(b) * a.S * kRowBytes;
   const uint8_t* wseq = reinterpret_cast<const uint8_t*>(a.win) + static_cast<int64_t>(b) * a.Wt * kRowBytes;
-  int voff[kChunks];  // thread tid's 16-byte chunks of a tile: bytes 16 tid + 4096 c
+  // Staging straight into LDS (buffer loads with the LDS bit): pass c of wave wv writes bytes
+  // [4096 c + 1024 wv, + 1024) of the tile buffer, lane l at + 16 l, so lane l loads the global
+  // chunk that the swizzle puts there: key k = (4096 c + 1024 wv + 16 l) / ROWB, slot
+  // j = (1024 wv + 16 l) % ROWB / 16 of it, i.e. chunk (j & 16) + ((j & 15) ^ sigma(k % 16)).  The
+  // pass's keys start at a multiple of 4096 / ROWB keys, so the offsets repeat with period 2
+  // (512-byte rows) or 1 (256-byte rows) in c; the pass's 4096 c goes in the scalar offset.
+  int voff[2];
 #pragma unroll
-  for (int c = 0; c < kChunks; ++c) voff[c] = 16 * tid + 16 * kFThreads * c;
-  // tile it: keys [base, base + TILE) of the blocks (it < n_bt) or of the window, read through a
-  // buffer resource whose range ends at the workgroup's last source, so that the rows past it
-  // read as zero (never attended) without a branch or an access.  A tile past the last has an
-  // empty range: its loads are issued (no branch, so the wait counts stay exact) but touch nothing.
-  auto load_tile = [&](int it, uint4 (&v)[kChunks]) {
+  for (int p = 0; p < 2; ++p) {
+    const int lin = 1024 * wv + 16 * lane;
+    const int kin = lin / kRowBytes, slot = (lin % kRowBytes) / 16;
+    const int ksw = ((4096 / kRowBytes) * p + kin) & 15;
+    voff[p] = kin * kRowBytes + 16 * ((slot & 16) + ((slot & 15) ^ chunk_swizzle(ksw)));
+  }
+  // tile it into LDS buffer buf: keys [base, base + TILE) of the blocks (it < n_bt) or of the
+  // window, read through a buffer resource whose range ends at the workgroup's last source, so that
+  // the rows past it are zero (never attended) without a branch or an access.  A tile past the last
+  // has an empty range: its loads are issued (no branch, so the wait counts stay exact) but touch
+  // no memory.
+  auto load_tile = [&](int it, auto buf_c) {
+    uint8_t* const dst = decltype(buf_c)::value ? Ls1 : Ls0;
     const bool blk = it < n_bt;
     const int base = blk ? it * kFTile : wlo + (it - n_bt) * kFTile;
     const int lim = blk ? gmax : whi;
@@ -290,12 +297,9 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const int n_bytes = it < it1 ? min(lim - base, kFTile) * kRowBytes : 0;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), 0, n_bytes, kBufWord3);
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) v[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[c], 0, 0));
-  };
-  auto store_tile = [&](int buf, const uint4 (&v)[kChunks]) {
-#pragma unroll
     for (int c = 0; c < kChunks; ++c)
-      *reinterpret_cast<uint4*>(Ls[buf] + st_off[c & 1] + 16 * kFThreads * (c & ~1)) = v[c];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + 4096 * c + 1024 * wv), 16, voff[c & 1],
+                                               4096 * c, 0, 0);
   };
 
   // m_run: the row's running maximum over this wave's keys, in scaled log2 units (the same in both
@@ -306,34 +310,31 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   for (int mb = 0; mb < 4; ++mb) O[mb] = ff32x16_t{};
   const v8 ones = __builtin_bit_cast(v8, make_uint4(E::kOnePair, E::kOnePair, E::kOnePair, E::kOnePair));
 
-  // Tiles are loaded kPrefetch tiles ahead into a ring of register sets (tile j in set j % kPrefetch)
-  // and stored to LDS one tile ahead.
-  uint4 nv[kPrefetch][kChunks];
-#pragma unroll
-  for (int j = 0; j < kPrefetch; ++j) load_tile(it0 + j, nv[j]);
-  if (it1 > it0) store_tile(0, nv[0]);
+  // Each tile is loaded into the other LDS buffer while the current one is used; its loads have
+  // landed (this wave's: the wait; every wave's: the barrier) before the step that reads it.  The
+  // compiler does not track the LDS writes of these loads, so both waits are explicit.
+  load_tile(it0, IntC<0>{});
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  // one tile; buffer and register-set indices are compile-time constants (LDS offsets are
-  // immediates, registers stay registers)
-  auto step = [&](int it, auto buf_c, auto set_c) {
+  // one tile; the buffer index is a compile-time constant (LDS offsets are immediates)
+  auto step = [&](int it, auto buf_c) {
     constexpr int buf = decltype(buf_c)::value;  // LDS buffer of tile it
-    constexpr int set = decltype(set_c)::value;  // register set of tile it (free: it is in LDS)
-    constexpr int nset = (set + 1) % kPrefetch;  // register set of tile it + 1
-    load_tile(it + kPrefetch, nv[set]);
-    const uint8_t* lt = Ls[buf];
+    load_tile(it + 1, IntC<buf ^ 1>{});  // the other buffer was last read before the previous barrier
+    const uint8_t* lt = buf ? Ls1 : Ls0;
 
     // S^T for keys 32 kb + 8 q + 4 hh + r of this wave's half tile, row rl (s[kb][4 q + r])
     ff32x16_t s[kKB];
+    {
+      uint4 kv[kKB][8];  // every row chunk of the half tile read before the products
 #pragma unroll
-    for (int kb = 0; kb < kKB; ++kb) {
-      s[kb] = ff32x16_t{};
+      for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
-      for (int k4 = 0; k4 < 2; ++k4) {
-        uint4 kv[4];  // four row chunks read before their products
+        for (int ks = 0; ks < 8; ++ks) kv[kb][ks] = *reinterpret_cast<const uint4*>(lt + 32 * kRowBytes * kb + soff[ks]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) kv[u] = *reinterpret_cast<const uint4*>(lt + 32 * kRowBytes * kb + soff[4 * k4 + u]);
+      for (int kb = 0; kb < kKB; ++kb) {
+        s[kb] = ff32x16_t{};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) s[kb] = E::mma(__builtin_bit_cast(v8, kv[u]), qb[4 * k4 + u], s[kb]);
+        for (int ks = 0; ks < 8; ++ks) s[kb] = E::mma(__builtin_bit_cast(v8, kv[kb][ks]), qb[ks], s[kb]);
       }
     }
     // masks (only where some row of the workgroup does not see the whole tile)
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     if (__builtin_amdgcn_ballot_w64(mt > m_run)) {  // some row's maximum moved up
       const float m_new = fmaxf(m_run, mt);
       const float alpha = m_new == kFNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-      lsum *= alpha;
+      lsum[0] *= alpha;  // the only element read (the products add the same sum to every element)
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) O[mb] *= alpha;
       m_run = m_new;
@@ -391,21 +392,20 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) O[mb] = E::mma(va[mb], pb, O[mb]);
       }
-    // the other buffer was last read before the previous barrier
-    if (it + 1 < it1) store_tile(buf ^ 1, nv[nset]);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
   // unrolled over the two buffers so that both indices are constants (a skipped second step
   // leaves the loop, so it does not blur the wait counts on the back edge)
 #pragma unroll 1
   for (int it = it0; it < it1; it += 2) {
-    step(it, IntC<0>{}, IntC<0>{});
-    if (it + 1 < it1) step(it + 1, IntC<1>{}, IntC<1 % kPrefetch>{});
+    step(it, IntC<0>{});
+    if (it + 1 < it1) step(it + 1, IntC<1>{});
   }
 
   // merge the two key halves of each row half (through the tile buffers, free after the last
   // barrier): key half 1 writes its state, key half 0 combines and stores
-  float* ob = reinterpret_cast<float*>(&Ls[0][0]) + rh * (4 * 16 * 64);  // [mb][v][lane]
+  float* ob = reinterpret_cast<float*>(Ls0) + rh * (4 * 16 * 64);  // [mb][v][lane]
   if (kh == 1) {
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
