@@ -43,21 +43,10 @@ namespace aekv {
 namespace {
 
 constexpr int kThreads = 256;
-#ifndef AEKV_ENC4_THREADS
-#define AEKV_ENC4_THREADS 256
-#endif
-constexpr int kEncThreads = AEKV_ENC4_THREADS;  // encode workgroup size (each workgroup builds the diag-mask table once)
-#ifndef AEKV_ENC4_MAX_BLOCKS
-#define AEKV_ENC4_MAX_BLOCKS 2048
-#endif
-#ifndef AEKV_ENC4_ONE_GROUP
-#define AEKV_ENC4_ONE_GROUP 1  // 0: a grid-stride loop with a two-group register prefetch
-#endif
-constexpr int kDecPasses = 8;  // 4-vector passes per decode wave on large inputs
-#ifndef AEKV_ENC4_MIN_WAVES
-#define AEKV_ENC4_MIN_WAVES 4  // waves per SIMD the register allocation must allow
-#endif
-constexpr int64_t kMaxBlocks = AEKV_ENC4_MAX_BLOCKS;  // grid-stride beyond this many workgroups
+constexpr int kEncThreads = 256;  // encode workgroup size (each workgroup builds the diag-mask table once)
+constexpr int kEncMinWaves = 4;   // waves per SIMD the encode's register allocation must allow
+constexpr int kDecPasses = 8;     // 4-vector passes per decode wave on large inputs
+constexpr int64_t kDecMaxBlocks = 2048;  // the grid-stride decode (smaller inputs): at most this many workgroups
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 constexpr float kMagic8 = 12582920.0f;  // 1.5 * 2^23 + 8: RN(t + kMagic8) = kMagic8 + rne(t), ulp 1
 
@@ -255,7 +244,7 @@ __device__ __forceinline__ void encode_group(const uint4 (&t)[4], const uint4* _
   }
 }
 
-__global__ __launch_bounds__(kEncThreads, AEKV_ENC4_MIN_WAVES) void tq_encode4_d128_bf16_kernel(
+__global__ __launch_bounds__(kEncThreads, kEncMinWaves) void tq_encode4_d128_bf16_kernel(
     const uint4* __restrict__ x, int64_t n_vec, const float* __restrict__ diag, float c, float c7,
     uint4* __restrict__ codes, float* __restrict__ scale) {
   const int lane = threadIdx.x & 63;
@@ -278,33 +267,15 @@ __global__ __launch_bounds__(kEncThreads, AEKV_ENC4_MIN_WAVES) void tq_encode4_d
   // wave index in a scalar register: the code below is wave-uniform
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kEncThreads / 64) +
                        __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  int64_t grp = wave;
+  const int64_t grp = wave;
   if (grp >= n_groups) return;
-#if AEKV_ENC4_ONE_GROUP
   // One group per wave (the launch covers every group): the hardware's turnover of short waves
   // overlaps one wave's loads with other waves' transforms, with no loop whose wait counts the
-  // compiler has to merge over the rare paths.  Measured +8% over the loop below on cfg2.
+  // compiler has to merge over the rare paths (measured 8% faster on cfg2 than a grid-stride loop
+  // with a two-group register prefetch).
   uint4 ta[4];
   load_group(x, grp, n_vec, v, g, ta);
   encode_group(ta, x, grp, n_vec, v, g, dm, s32, s64, sigma, diag, c, c7, codes, scale);
-#else
-  // two load buffers, alternating, so that the next group's loads are in flight during the
-  // current group's transform without register copies.  The loads are unconditional (a wave's
-  // last prefetch re-reads its own group, a cache hit) so that no wait has to cover a skipped load.
-  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * (kEncThreads / 64);
-  uint4 ta[4], tb[4];
-  load_group(x, grp, n_vec, v, g, ta);
-  while (true) {
-    load_group(x, grp + n_waves < n_groups ? grp + n_waves : grp, n_vec, v, g, tb);
-    encode_group(ta, x, grp, n_vec, v, g, dm, s32, s64, sigma, diag, c, c7, codes, scale);
-    grp += n_waves;
-    if (grp >= n_groups) break;
-    load_group(x, grp + n_waves < n_groups ? grp + n_waves : grp, n_vec, v, g, ta);
-    encode_group(tb, x, grp, n_vec, v, g, dm, s32, s64, sigma, diag, c, c7, codes, scale);
-    grp += n_waves;
-    if (grp >= n_groups) break;
-  }
-#endif
 }
 
 // ---- decode: 4-bit codes -> bf16, D = 128 ------------------------------------------------------
@@ -517,8 +488,7 @@ bool launch_encode4_d128_bf16(const void* x, int64_t n_vec, const float* diag, f
   if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(codes) & 15)) return false;
   if (n_vec <= 0) return true;
   const int64_t n_groups = (n_vec + 15) / 16;
-  int64_t blocks = ceil_div(n_groups, kEncThreads / 64);
-  if (!AEKV_ENC4_ONE_GROUP && blocks > kMaxBlocks) blocks = kMaxBlocks;
+  const int64_t blocks = ceil_div(n_groups, kEncThreads / 64);
   if (blocks > 0x7fffffff) return false;
   const float c7 = c * 7.0f;
   hipLaunchKernelGGL(tq_encode4_d128_bf16_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kEncThreads), 0, st,
@@ -539,7 +509,7 @@ bool launch_decode4_d128_bf16(const void* codes, const float* scale, int64_t n_v
   // against 0.59 for the loop); smaller inputs keep the loop's wider grid
   const bool per_wave = n_pass >= int64_t(kDecPasses) * (kThreads / 64) * 2048;
   int64_t blocks = ceil_div(per_wave ? ceil_div(n_pass, int64_t(kDecPasses)) : n_pass, kThreads / 64);
-  if (!per_wave && blocks > kMaxBlocks) blocks = kMaxBlocks;
+  if (!per_wave && blocks > kDecMaxBlocks) blocks = kDecMaxBlocks;
   if (blocks > 0x7fffffff) return false;
   auto kern = per_wave ? tq_decode4_d128_bf16_kernel<kDecPasses> : tq_decode4_d128_bf16_kernel<0>;
   hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st,
