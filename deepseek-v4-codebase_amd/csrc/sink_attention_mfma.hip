@@ -88,7 +88,7 @@ template <int DT, int IDX, int NW>
 __global__ __launch_bounds__(64 * NW) void gather_attn_kernel(GatherArgs a) {
   using E = Elem<DT>;
   using v8 = typename E::v8;
-  __shared__ GatherLds<NW> L;
+  __shared__ __align__(16) GatherLds<NW> L;  // 16-byte aligned: the merge uses 16-byte accesses
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int64_t bt = blockIdx.x;  // b * T + t
   const int h0 = 16 * static_cast<int>(blockIdx.y);
