@@ -64,13 +64,15 @@ struct QAttnMfmaArgs {
   int64_t S, K, n_comp, n_src;
   int H, n_split, split_src;
   float sm_scale, wscale;
-  float* part;            // [B, n_split, H, 2 + 128] (split runs only)
+  float* part;            // [B, n_split, H, kPartStride] (split runs only)
   uint16_t* out;          // [B, H, 128] bf16
 };
 
 // Floats per row of the merge buffer: the 4-float pad puts head h's row at bank 4h, so the 16 heads
 // of one store or load instruction cover all 64 banks.
 constexpr int kObStride = kD + 4;
+// Floats per split result of one (row, head): max, sum, two pad, O[128] (16-byte aligned O).
+constexpr int kPartStride = kD + 4;
 
 // LDS layout (bytes) for NW waves: wave outputs for the merge | wave stats | per-head factors |
 // block ids | WROWS window rows of 256 bytes (the fused decode kernel stages the window there)
@@ -441,7 +443,7 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
     if (a.n_split == 1) {
       inv[h] = 1.0f / L;
     } else {
-      float* dst = a.part + ((b * a.n_split + split) * H + h) * (kD + 2);
+      float* dst = a.part + ((b * a.n_split + split) * H + h) * kPartStride;
       dst[0] = M;
       dst[1] = L;
     }
@@ -464,9 +466,7 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
       const uint2 v = make_uint2(pack_bf16x2(acc[0] * r, acc[1] * r), pack_bf16x2(acc[2] * r, acc[3] * r));
       *reinterpret_cast<uint2*>(a.out + (b * H + h) * kD + d4) = v;
     } else {
-      float* dst = a.part + ((b * a.n_split + split) * H + h) * (kD + 2) + 2 + d4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dst[e] = acc[e];
+      *reinterpret_cast<f32x4_t*>(a.part + ((b * a.n_split + split) * H + h) * kPartStride + 4 + d4) = acc;
     }
   }
 }

@@ -7,54 +7,57 @@
 namespace aekv {
 namespace qattn {
 
-// Split combine: M = max(sink, split maxima), L = e^{sink-M} + sum_s e^{m_s-M} l_s,
-// out = sum_s e^{m_s-M} acc_s / L.  The per-head factors e^{m_s-M} / L go to LDS first (one load
-// round for every split's statistics), then each output sums its splits' partials, all loads of a
-// thread issued together: two dependent memory rounds per row whatever the split count.
-constexpr int kMaxCombineSplits = 256;
-__global__ __launch_bounds__(kThreads) void quant_attn_mfma_combine_kernel(QAttnMfmaArgs a) {
-  __shared__ float st[kMaxCombineSplits * 16 * 2];  // [split][head][m, l]
-  __shared__ float fac[kMaxCombineSplits * 16];     // [split][head] e^{m_s - M} / L
-  const int64_t b = blockIdx.x;
-  const int H = a.H, ns = a.n_split;
-  const float* part = a.part + b * ns * H * (kD + 2);
-  for (int i = threadIdx.x; i < ns * H; i += kThreads) {
-    const float* ps = part + static_cast<int64_t>(i) * (kD + 2);
-    st[2 * i] = ps[0];
-    st[2 * i + 1] = ps[1];
-  }
-  __syncthreads();
-  if (threadIdx.x < H) {
-    const int h = threadIdx.x;
-    const float sk = a.sink[h];
-    float M = sk;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, st[2 * (s * H + h)]);
-    float L = __expf(sk - M);
-    for (int s = 0; s < ns; ++s) {
-      const float ms = st[2 * (s * H + h)];
-      const float f = ms == kNegInf ? 0.0f : __expf(ms - M);
-      fac[s * H + h] = f;
-      L = fmaf(f, st[2 * (s * H + h) + 1], L);
-    }
-    const float r = 1.0f / L;
-    for (int s = 0; s < ns; ++s) fac[s * H + h] *= r;
-  }
-  __syncthreads();
-  // thread -> (head, 4 consecutive dims); the splits' partials are independent loads
-  for (int p = threadIdx.x; p < H * (kD / 4); p += kThreads) {
-    const int h = p / (kD / 4), d4 = 4 * (p % (kD / 4));
-    f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-    for (int s = 0; s < ns; ++s) {
-      const float* ps = part + static_cast<int64_t>(s * H + h) * (kD + 2) + 2 + d4;
-      const float f = fac[s * H + h];
-      acc = f32x4_t{fmaf(f, ps[0], acc[0]), fmaf(f, ps[1], acc[1]), fmaf(f, ps[2], acc[2]), fmaf(f, ps[3], acc[3])};
-    }
-    const uint2 v = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
-    *reinterpret_cast<uint2*>(a.out + (b * H + h) * kD + d4) = v;
-  }
-}
+constexpr int kMaxCombineSplits = 256;  // most source pieces per row
 
+// Split combine: M = max(sink, split maxima), L = e^{sink-M} + sum_s e^{m_s-M} l_s,
+// out = sum_s e^{m_s-M} acc_s / L (the sink counted once, aether_pipeline/serving.py:125-129).  32
+// threads per (row, head), 4 dims each; the splits' (m, l, acc) are loaded in chunks of 8 whose
+// loads are all issued together and merged online, so a row takes one memory round per 8 splits.
+__global__ __launch_bounds__(kThreads) void quant_attn_mfma_combine_kernel(QAttnMfmaArgs a, int64_t rows) {
+  constexpr int kChunk = 8;
+  const int H = a.H, ns = a.n_split;
+  const int64_t rh = static_cast<int64_t>(blockIdx.x) * (kThreads / 32) + (threadIdx.x >> 5);  // row * H + head
+  if (rh >= rows * H) return;
+  const int64_t b = rh / H;
+  const int h = static_cast<int>(rh - b * H), j = threadIdx.x & 31;
+  const float* part = a.part + (b * ns * H + h) * kPartStride;  // split s at + s * H * kPartStride
+  const float sk = a.sink[h];
+  float M = sk, den = sk == kNegInf ? 0.0f : 1.0f;
+  f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < ns; s0 += kChunk) {
+    float m[kChunk], l[kChunk];
+    f32x4_t o[kChunk];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      m[i] = kNegInf;
+      l[i] = 0.0f;
+      o[i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      if (s0 + i < ns) {
+        const float* ps = part + static_cast<int64_t>(s0 + i) * H * kPartStride;
+        m[i] = ps[0];
+        l[i] = ps[1];
+        o[i] = *reinterpret_cast<const f32x4_t*>(ps + 4 + 4 * j);
+      }
+    }
+    float cm = M;
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) cm = fmaxf(cm, m[i]);
+    if (cm == kNegInf) continue;  // nothing yet (no sink, no source)
+    const float r = M == kNegInf ? 0.0f : __expf(M - cm);
+    den *= r;
+    acc *= r;
+    M = cm;
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      const float f = m[i] == kNegInf ? 0.0f : __expf(m[i] - M);
+      den = fmaf(f, l[i], den);
+      acc = f32x4_t{fmaf(f, o[i][0], acc[0]), fmaf(f, o[i][1], acc[1]), fmaf(f, o[i][2], acc[2]), fmaf(f, o[i][3], acc[3])};
+    }
+  }
+  const float r = den > 0.0f ? 1.0f / den : 0.0f;
+  *reinterpret_cast<uint2*>(a.out + rh * kD + 4 * j) =
+      make_uint2(pack_bf16x2(acc[0] * r, acc[1] * r), pack_bf16x2(acc[2] * r, acc[3] * r));
+}
 
 }  // namespace qattn
 
@@ -77,7 +80,7 @@ bool quant_attn_mfma_fits(int64_t rows, int64_t n_src) {
 
 size_t quant_attn_mfma_workspace(int64_t B, int64_t H, int64_t n_src) {
   const int64_t n_split = n_src > 0 ? ceil_div(n_src, split_sources(B, n_src)) : 1;
-  return n_split > 1 ? align_up(static_cast<size_t>(B * n_split * H * (kD + 2)) * 4, 256) : 0;
+  return n_split > 1 ? align_up(static_cast<size_t>(B * n_split * H * kPartStride) * 4, 256) : 0;
 }
 
 int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* scale, const int64_t* sel,
@@ -109,6 +112,8 @@ int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* s
     return fail(AEKV_ERR_UNSUPPORTED, "%s: %lld rows x %lld sources exceed the launch grid", who,
                 static_cast<long long>(rows), static_cast<long long>(a.n_src));
   a.n_split = static_cast<int>(n_split);
+  if (n_split > 1 && (!ws || !is_aligned(ws, 16)))
+    return fail(AEKV_ERR_ALIGN, "%s: the split workspace must be 16-byte aligned", who);
   a.sm_scale = softmax_scale;
   a.wscale = wht_scale(kD);
   a.part = static_cast<float*>(ws);
@@ -127,7 +132,8 @@ int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* s
                      lds, st, a);
   if (int rc = check_launch(who)) return rc;
   if (n_split > 1) {
-    hipLaunchKernelGGL(quant_attn_mfma_combine_kernel, dim3(static_cast<uint32_t>(rows)), dim3(kThreads), 0, st, a);
+    const int64_t n_wg = ceil_div(rows * H, kThreads / 32);
+    hipLaunchKernelGGL(quant_attn_mfma_combine_kernel, dim3(static_cast<uint32_t>(n_wg)), dim3(kThreads), 0, st, a, rows);
     return check_launch(who);
   }
   return AEKV_OK;

@@ -474,7 +474,7 @@ extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const
   if (!ws || ws_bytes < l.part_bytes)
     return fail(AEKV_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who, l.part_bytes, ws_bytes);
   if (quant_attn_mfma_supported(H, D) && quant_attn_mfma_fits(B, n_comp + W) && use_specialised_codec() &&
-      is_aligned(q, 16) && is_aligned(out, 8) &&
+      is_aligned(q, 16) && is_aligned(out, 8) && is_aligned(ws, 16) &&
       is_aligned(diag, 16) && (n_comp == 0 || is_aligned(codes, 16)) && (W == 0 || is_aligned(window, 16)))
     return launch_quant_attn_mfma(q, codes, scale, sel, window, sink, diag, B, H, S, K, all_blocks, W, bits,
                                   softmax_scale, ws, out, as_stream(stream), who);
