@@ -393,14 +393,27 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
   int64_t row[TT];
   bool rok[TT];
   int64_t kr;
+  int64_t bx = blockIdx.x;  // key-range index
   if constexpr (TT == 1) {
     row[0] = blockIdx.y;
     rok[0] = true;
     kr = row[0] / a.T;
   } else {
+    // prefill: the linear workgroup ids are renumbered so that XCD x (linear id L runs on XCD
+    // L % 8, each XCD with its own L2) runs the consecutive range [x n/8, (x+1) n/8) of (row group,
+    // key range) pairs, i.e. whole sequences, whose keys then stay in that XCD's L2 for all of
+    // their target groups
+    int64_t by = blockIdx.y;
+    const uint32_t nx = gridDim.x, n_wg = nx * gridDim.y;
+    if (n_wg % 8 == 0) {
+      const uint32_t L = blockIdx.y * nx + blockIdx.x;
+      const uint32_t w = (L % 8) * (n_wg / 8) + L / 8;
+      by = w / nx;
+      bx = w % nx;
+    }
     const int64_t ngt = (a.T + TT - 1) / TT;
-    kr = blockIdx.y / ngt;
-    const int64_t t0 = (blockIdx.y % ngt) * TT;
+    kr = by / ngt;
+    const int64_t t0 = (by % ngt) * TT;
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
       rok[tt] = t0 + tt < a.T;
@@ -428,7 +441,7 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
   const uint8_t* crow = a.codes + kr * S * RB;
   const float* srow = a.kscale + kr * S;
   constexpr int64_t kGroupKeys = SPW * 64;
-  const int64_t wave_base = (static_cast<int64_t>(blockIdx.x) * 4 + wv) * a.gpw * kGroupKeys;
+  const int64_t wave_base = (bx * 4 + wv) * a.gpw * kGroupKeys;
 #pragma unroll 1
   for (int gi = 0; gi < a.gpw; ++gi) {
     const int64_t kb = wave_base + gi * kGroupKeys;

@@ -484,10 +484,23 @@ __device__ __forceinline__ void attend_row(const QAttnMfmaArgs& a, const int64_t
 }
 
 // One row (or one split of a long row) per workgroup of 64 * NW threads.
+//
+// Workgroups are dispatched round-robin over the 8 XCDs (linear id L on XCD L % 8), each with its
+// own L2.  For prefill rows (T > 1 targets per cache row, rows sequence-major) the linear ids are
+// renumbered so that XCD x runs the consecutive range [x n/8, (x+1) n/8) of (row, split) pairs,
+// i.e. whole sequences, whose code rows then stay in that XCD's L2 for all of their targets.
 template <int BITS, int NW>
 __global__ __launch_bounds__(64 * NW) void quant_attn_mfma_kernel(QAttnMfmaArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
-  attend_row<BITS, NW>(a, blockIdx.y, blockIdx.x, lds, false);
+  int64_t row = blockIdx.y, split = blockIdx.x;
+  const uint32_t nx = gridDim.x, n_wg = nx * gridDim.y;
+  if (a.T > 1 && n_wg % 8 == 0) {
+    const uint32_t L = blockIdx.y * nx + blockIdx.x;
+    const uint32_t w = (L % 8) * (n_wg / 8) + L / 8;
+    row = w / nx;
+    split = w % nx;
+  }
+  attend_row<BITS, NW>(a, row, static_cast<int>(split), lds, false);
 }
 
 }  // namespace qattn
