@@ -7,6 +7,9 @@ Flags that matter for parity:
   -ffp-contract=off                              no silent FMA contraction (bit-exact codec)
   -fhip-fp32-correctly-rounded-divide-sqrt       IEEE division, as torch's fp32 `/`
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed-fp32 VALU ops
+  -mllvm -amdgpu-mfma-vgpr-form                  matrix-instruction results in ordinary VGPRs: otherwise
+                                                 the compiler keeps some accumulators in AGPRs and copies
+                                                 every result to VGPRs for the VALU that consumes it
 """
 from __future__ import annotations
 
@@ -33,6 +36,7 @@ COMMON_FLAGS = [
     "-ffp-contract=off",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
