@@ -146,3 +146,68 @@ def test_unsplit_entry_points(dev, B, T, S):
         _close(out_s, want_s)
         # and the wrapper (split into pieces) on the same call
         _close(sparse_sink_attention(qd, kvd, td, sd, 128 ** -0.5), want_s)
+
+
+def test_misaligned_views_take_the_valu_kernel(dev):
+    # q and kv views one element into their storage are not 16-byte aligned: the call falls back
+    # to the VALU kernel (the wrapper keeps contiguous views as they are), same results
+    g = torch.Generator().manual_seed(43)
+    q0 = torch.randn(2 * 3 * 16 * 128 + 1, generator=g).to(torch.bfloat16)
+    kv0 = torch.randn(2 * 90 * 2 * 128 + 1, generator=g).to(torch.bfloat16)
+    q = q0[1:].view(2, 3, 16, 128)
+    kv = kv0[1:].view(2, 90, 2, 128)
+    topk = torch.randint(0, 90, (2, 3, 70), generator=g)
+    sink = torch.randn(16, generator=g).to(torch.bfloat16)
+    qd, kvd = q0.to(dev)[1:].view(2, 3, 16, 128), kv0.to(dev)[1:].view(2, 90, 2, 128)
+    assert qd.data_ptr() % 16 != 0
+    got = sparse_sink_attention(qd, kvd, topk.to(dev), sink.to(dev), 128 ** -0.5)
+    want = O.sink_attention(to_np_f32(q), to_np_f32(kv), topk.numpy(), to_np_f32(sink), 128 ** -0.5)
+    _close(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_tiled_prefill_flash_many_heads_scalar_sink(dev, dtype):
+    # 20 heads (row blocks of 64 cross target boundaries), scalar sink, S not a multiple of the tile
+    g = torch.Generator().manual_seed(47)
+    B, T, H, S = 2, 7, 20, 1000
+    q = torch.randn(B, T, H, 128, generator=g).to(dtype)
+    kv = torch.randn(B, S, 2, 128, generator=g).to(dtype)
+    sink = torch.randn(1, generator=g).to(dtype)
+    got = tiled_prefill_attention(q.to(dev), kv.to(dev), sink.to(dev), 0.1)
+    idx = np.broadcast_to(np.arange(S), (B, T, S))
+    want = O.sink_attention(to_np_f32(q), to_np_f32(kv), idx, to_np_f32(sink), 0.1)
+    _close(got, want)
+
+
+def test_split_calls_in_a_graph(dev):
+    # the split workspace (taken from torch's allocator inside the capture) and the combine kernel
+    # replayed from a HIP graph, eager work between replays, every replay against the eager result
+    g = torch.Generator().manual_seed(53)
+    q = torch.randn(1, 1, 16, 128, generator=g).to(torch.bfloat16).to(dev)
+    src = torch.randn(1, 640, 128, generator=g).to(torch.bfloat16)
+    kv = torch.stack([src, src], dim=2).to(dev)
+    sink = torch.randn(16, generator=g).to(torch.bfloat16).to(dev)
+    qs = torch.randn(1, 4, 16, 128, generator=g).to(torch.bfloat16).to(dev)
+    kvs = torch.randn(1, 3000, 2, 128, generator=g).to(torch.bfloat16).to(dev)
+    topk = torch.randint(0, 3000, (1, 4, 600), generator=g, dtype=torch.int32).to(dev)
+    want_d = tiled_prefill_attention(q, kv, sink, 128 ** -0.5)
+    want_s = sparse_sink_attention(qs, kvs, topk, sink, 128 ** -0.5)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        tiled_prefill_attention(q, kv, sink, 128 ** -0.5)
+        sparse_sink_attention(qs, kvs, topk, sink, 128 ** -0.5)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_d = tiled_prefill_attention(q, kv, sink, 128 ** -0.5)
+        out_s = sparse_sink_attention(qs, kvs, topk, sink, 128 ** -0.5)
+    for _ in range(3):
+        out_d.zero_()
+        out_s.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_d, want_d) and torch.equal(out_s, want_s)
+        tiled_prefill_attention(qs, kvs, sink, 0.2)  # eager work between replays
