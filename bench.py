@@ -164,6 +164,19 @@ def bench_encode(args, dev, out):
     del y, rec
 
 
+CPU_RUNS = 5  # CPU baseline: median of this many timed runs after one warm-up
+
+
+def median_seconds(fn, runs: int = CPU_RUNS) -> float:
+    """Median wall time of `runs` calls of fn (the caller has run it once as a warm-up)."""
+    times = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return sorted(times)[len(times) // 2]
+
+
 def bench_cpu_encode(out):
     import numpy as np
 
@@ -173,15 +186,11 @@ def bench_cpu_encode(out):
     xb = out.pop("x_host").numpy().view(np.uint16)
     dg = O.diag(42, D2)
     cores = cpu_cores()
-    times = []
-    for _ in range(3):
-        t = time.perf_counter()
-        O.encode(xb, "bf16", 4, dg, threads=cores)
-        times.append(time.perf_counter() - t)
-    med = sorted(times)[1]
+    O.encode(xb, "bf16", 4, dg, threads=cores)
+    med = median_seconds(lambda: O.encode(xb, "bf16", 4, dg, threads=cores))
     log(f"cpu oracle encode (cfg2, {cores} threads): {med:.3f} s, {ENC_BYTES / med / 1e9:.2f} GB/s")
     c_port = {"value": round(ENC_BYTES / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-              "sample": "full cfg2 layer (3,145,728 vectors), median of 3 passes of the C oracle encode "
+              "sample": f"full cfg2 layer (3,145,728 vectors), median of {CPU_RUNS} passes after one warm-up of the C oracle encode "
                         "(oracle/aekv_oracle.c, OpenMP over vectors)"}
     # the reference's own op sequence (turbo_quant.py:127-166 in torch eager ops), all host cores, on a
     # quarter of the layer: 65536 tokens x 12 heads
@@ -192,12 +201,7 @@ def bench_cpu_encode(out):
     xs = torch.from_numpy(xb.reshape(T2, H2, D2)[:n_tok].copy()).view(torch.bfloat16)
     dgt = torch.from_numpy(dg)
     T.encode(xs, 4, dgt)
-    times = []
-    for _ in range(3):
-        t = time.perf_counter()
-        T.encode(xs, 4, dgt)
-        times.append(time.perf_counter() - t)
-    med_t = sorted(times)[1]
+    med_t = median_seconds(lambda: T.encode(xs, 4, dgt))
     bytes_t = ENC_BYTES // 4
     log(f"cpu torch op sequence encode ({n_tok} tokens, {cores} threads): {med_t:.3f} s, "
         f"{bytes_t / med_t / 1e9:.2f} GB/s")
@@ -205,8 +209,8 @@ def bench_cpu_encode(out):
             "cpu": cpu_model(),
             "sample": f"the reference's encode op sequence (turbo_quant.py:127-166: torch.cat butterflies, amax, "
                       f"divide, multiply, round, clamp, nibble pack; oracle/torch_ref.py) on torch CPU with "
-                      f"{cores} threads, over {n_tok} tokens x 12 heads (a quarter of the cfg2 layer), median of 3 "
-                      f"after one warm-up",
+                      f"{cores} threads, over {n_tok} tokens x 12 heads (a quarter of the cfg2 layer), median of "
+                      f"{CPU_RUNS} after one warm-up",
             "c_port": c_port}
 
 
@@ -214,7 +218,7 @@ def bench_cpu_csa(inp, rows, name, bits):
     """The CPU oracle's restatement of the reference decode step (aether_2b/serving.py:597-625) on the
     first `rows` rows of a CSA config, timed on this host: dequantise the index and KV caches (every
     step, as _read_compressed does, or memoised as its cache does), score all blocks (softplus
-    rule), exact top-256, gather + window + sink attention.  Median of 3 after one warm-up."""
+    rule), exact top-256, gather + window + sink attention.  Median of CPU_RUNS after one warm-up."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -243,17 +247,12 @@ def bench_cpu_csa(inp, rows, name, bits):
     res = {"rows": rows, "cores": cores, "kind": "port"}
     for label, dq in (("dequant_every_step", True), ("memoised_dequant", False)):
         step(dq)
-        times = []
-        for _ in range(3):
-            t = time.perf_counter()
-            step(dq)
-            times.append(time.perf_counter() - t)
-        med = sorted(times)[1]
+        med = median_seconds(lambda: step(dq))
         res[label] = {"s_per_step": round(med, 5), "tokens_per_s": round(rows / med, 2)}
     log(f"cpu oracle {name} ({rows} rows, {cores} threads): {res['dequant_every_step']['tokens_per_s']:.1f} tok/s "
         f"dequantising every step, {res['memoised_dequant']['tokens_per_s']:.1f} tok/s memoised")
     res["sample"] = (f"first {rows} rows of {name}: dequant (index f32 + KV bf16), scores, exact top-256, gather + "
-                     f"window + sink attention, C oracle with OpenMP; median of 3")
+                     f"window + sink attention, C oracle with OpenMP; median of {CPU_RUNS} after one warm-up")
     res["torch_op_sequence"] = bench_torch_csa(inp, rows, name, bits)
     return res
 
@@ -261,7 +260,7 @@ def bench_cpu_csa(inp, rows, name, bits):
 def bench_torch_csa(inp, rows, name, bits):
     """The reference decode step's own torch op sequence (oracle/torch_ref.py: serving.py:597-625 with
     the PyTorch attention backend, bf16 attention as the engine runs it) on the first `rows` rows,
-    torch on all host cores; dequantising every step and memoised.  Median of 3 after one warm-up."""
+    torch on all host cores; dequantising every step and memoised.  Median of CPU_RUNS after one warm-up."""
     import torch_ref as T
 
     cores = cpu_cores()
@@ -276,18 +275,13 @@ def bench_torch_csa(inp, rows, name, bits):
             T.csa_decode_step(h["q"], h["index_q"], h["index_w"], h["ix_codes"], h["ix_scale"], h["kv_codes"],
                               h["kv_scale"], h["win"], h["sink"], bits, d64, d128, 256, memo=memo)
         step()
-        times = []
-        for _ in range(3):
-            t = time.perf_counter()
-            step()
-            times.append(time.perf_counter() - t)
-        med = sorted(times)[1]
+        med = median_seconds(step)
         res[label] = {"s_per_step": round(med, 5), "tokens_per_s": round(rows / med, 2)}
     log(f"cpu torch op sequence {name} ({rows} rows, {cores} threads): "
         f"{res['dequant_every_step']['tokens_per_s']:.1f} tok/s dequantising every step, "
         f"{res['memoised_dequant']['tokens_per_s']:.1f} tok/s memoised")
     res["sample"] = (f"first {rows} rows of {name}: the reference's torch ops (decode, einsum, relu, softplus weights, "
-                     f"topk, gather, cat, PyTorch sink attention in bf16); median of 3")
+                     f"topk, gather, cat, PyTorch sink attention in bf16); median of {CPU_RUNS} after one warm-up")
     return res
 
 
