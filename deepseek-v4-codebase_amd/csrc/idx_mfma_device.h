@@ -589,7 +589,10 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
   constexpr int kSlotPer = kHistBins / NT;  // one pass over the slot maxima for S <= 65536
   constexpr int64_t kSlotPass = static_cast<int64_t>(kSlotPer) * NT;
   for (int i = tid; i < kHistBins; i += NT) h[i] = 0u;
-  if (tid == 0) s_cnt[0] = 0u;
+  if (tid == 0) {
+    s_cnt[0] = 0u;
+    s_cnt[1] = 0u;
+  }
   uint32_t mx[kSlotPer];
   auto load_max = [&](int64_t c0) {
 #pragma unroll
@@ -635,9 +638,15 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
   // then one thread per listed slot reads its 16 keys and appends those >= tau
   for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
     if (n_slots > kSlotPass) load_max(c0);  // otherwise mx still holds the only pass
-    __syncthreads();  // h and s_cnt[1] are free
-    if (tid == 0) s_cnt[1] = 0u;
-    __syncthreads();
+    if (c0 > 0) {
+      // a later pass: the previous pass's list (h) and count are free once every thread is here.
+      // The first pass needs no barrier: s_cnt[1] was zeroed with s_cnt[0], and h is last read
+      // before the final barrier of block_threshold (or, when that is skipped, last written
+      // before the histogram's barrier).
+      __syncthreads();
+      if (tid == 0) s_cnt[1] = 0u;
+      __syncthreads();
+    }
     {  // one reservation per wave for all of its slot columns
       bool q[kSlotPer];
       uint64_t m[kSlotPer];
