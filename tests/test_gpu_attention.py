@@ -149,6 +149,24 @@ def test_config4_hca_decode_4bit(dev):
     _close(got.view(B, H, D), _oracle_quant(pq, codes, scale, None, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quant_attention_more_splits_than_a_combine_chunk(dev, bits):
+    # 2 rows of 5000 blocks + 128 window rows: 11 pieces of 512 sources per row, so the split
+    # combine merges two chunks (8 + 3); in row 1 every selected entry past the first 600 is
+    # skipped, so most of its pieces hold no source (max -inf, sum 0)
+    B, H, D, S, W = 2, 12, 128, 5000, 128
+    pq, codes, scale, q, win, sink = _quant_inputs(dev, B, H, D, S, W, bits, 60 + bits)
+    sm = D ** -0.5
+    got = hca_decode(q, codes, scale, win, sink, sm, kv_quant=pq)
+    _close(got.view(B, H, D), _oracle_quant(pq, codes, scale, None, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
+    g = torch.Generator().manual_seed(61)
+    sel = torch.randint(0, S, (B, S), generator=g)
+    sel[1, 600:] = -1
+    sel = sel.to(dev)
+    got = quant_sink_attention(q, codes, scale, sel, win, sink, sm, quant=pq)
+    _close(got.view(B, H, D), _oracle_quant(pq, codes, scale, sel, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
+
+
 def test_config3_csa_decode_end_to_end(dev):
     # benchmark configuration cfg3: B=8, 16384 blocks, 8-bit codes, indexer 4x64 softplus, top-256 + window 128 + sink
     B, H, D, S, W, IH, IC = 8, 12, 128, 16384, 128, 4, 64
