@@ -154,6 +154,19 @@ def bench_encode(args, dev, out):
     ms_d = timed(dec, args.steps, args.warmup)
     log(f"cfg2 decode: {ms_d * 1e3:.1f} us/step, {ENC_BYTES / ms_d / 1e6:.1f} GB/s")
     out["decode_ms"] = ms_d
+    # the practical ceiling of the encode's own traffic: the same bytes, access pattern and
+    # non-temporal stores, no transform (aekv_stream_probe)
+    c2, s2 = torch.empty_like(codes), torch.empty_like(scale)
+    c2p, s2p = L.ptr(c2), L.ptr(s2)
+
+    def probe():
+        L.check(lib.aekv_stream_probe(xp, N_VEC2, c2p, s2p, stream), "stream probe")
+
+    ms_p = timed(probe, args.steps, args.warmup)
+    out["stream_ceiling_gbs"] = ENC_BYTES / ms_p / 1e6
+    log(f"streaming ceiling of the encode's traffic: {ms_p * 1e3:.1f} us, {out['stream_ceiling_gbs']:.1f} GB/s "
+        f"(encode at {ms_p / ms:.3f} of it)")
+    del c2, s2
     # copy-bandwidth reference (torch copy of the same layer)
     y = torch.empty_like(x)
     ms_c = timed(lambda: y.copy_(x), args.steps, args.warmup)
@@ -698,6 +711,11 @@ def main():
                                        "GB/s": round(ENC_BYTES / res["decode_ms"] / 1e6, 2),
                                        "frac": round(ENC_BYTES / res["decode_ms"] / 1e6 / HBM_PEAK_GBS, 4)}
         secondary["copy_GB/s"] = round(res["copy_gbs"], 1)
+        secondary["stream_ceiling"] = {
+            "GB/s": round(res["stream_ceiling_gbs"], 1),
+            "encode_of_ceiling": round(ENC_BYTES / res["encode_ms"] / 1e6 / res["stream_ceiling_gbs"], 4),
+            "what": "aekv_stream_probe: the encode's bytes and access pattern (64 B per lane in, 16 B codes per "
+                    "lane and 4 B scale per vector out, non-temporal stores) with no transform"}
         ms_i = res["encode_ms_from_idle"]
         secondary["tq_encode_cfg2_from_idle"] = {
             "ms": round(ms_i, 5), "GB/s": round(ENC_BYTES / ms_i / 1e6, 2),

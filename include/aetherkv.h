@@ -265,6 +265,13 @@ int aekv_emit_block(const void* c, const void* z, const void* z_bias, int64_t B,
  * normalised with norm_weight[d] bf16 and eps (NULL: none); out [rows, heads, d] bf16 (may alias
  * x).  Rounding points as the reference's bf16 torch ops (bf16 cos/sin and RoPE terms, fp32
  * RMSNorm).  d = 128 or 256. */
+/* Measurement utility, no counterpart in the reference: moves the bytes of a 4-bit D = 128 bf16
+ * encode of n_vec vectors (x [n_vec, 128] bf16 in; codes [n_vec, 64] bytes and scale [n_vec] out)
+ * with the encode kernel's access pattern and non-temporal stores but no transform (the outputs are
+ * xor folds of the inputs).  bench.py times it beside the encode as the practical streaming
+ * ceiling of that traffic.  x and codes 16-byte aligned. */
+int aekv_stream_probe(const void* x, int64_t n_vec, void* codes, float* scale, void* stream);
+
 int aekv_rope_rmsnorm(const void* x, int64_t rows, int32_t heads, int32_t d, const int64_t* positions,
                       int32_t pos_sign, const float* inv_freq, int32_t rope_dim, const void* norm_weight,
                       float eps, void* out, void* stream);
