@@ -44,9 +44,9 @@
 // Softmax in the exp2 domain with the exact running maximum, so a row's largest weight is exactly 1
 // in bf16 and every weight ratio carries one bf16 rounding (a maximum raised only past a margin
 // leaves two, which measurably exceeds the attention tolerance).  The rescale of O and l is a
-// wave-uniform branch taken on tiles that raise some row's maximum.  The normaliser is one more
-// product per 16-key chunk with an all-ones A operand: the sum of the very bf16 weights the
-// numerator used.  Tiles that every row of the workgroup sees in full skip the masks.
+// wave-uniform branch taken on tiles that raise some row's maximum.  The normaliser is the sum of
+// the very bf16 weights the numerator used: each lane adds its own weights of the row with
+// v_dot2_f32_bf16 (f16) against ones, and the two lane halves are added at the end.  Tiles that every row of the workgroup sees in full skip the masks.
 #include "tq_device.h"
 
 namespace aekv {
@@ -62,6 +62,8 @@ constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: raw 32-bit dat
 
 typedef __attribute__((ext_vector_type(8))) __bf16 fbf16x8_t;
 typedef __attribute__((ext_vector_type(8))) _Float16 ff16x8_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 fbf16x2_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 ff16x2_t;
 typedef __attribute__((ext_vector_type(16))) float ff32x16_t;
 typedef __attribute__((ext_vector_type(4))) short fi16x4_t;
 typedef __attribute__((address_space(3))) fi16x4_t lds_i16x4_t;
@@ -90,6 +92,11 @@ struct FlashElem<AEKV_BF16> {
   static constexpr uint32_t kOnePair = 0x3F803F80u;
   __device__ static ff32x16_t mma(v8 a, v8 b, ff32x16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
   __device__ static uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
+  // c + the two values of a packed pair (products with 1.0 are exact)
+  __device__ static float add_pair(uint32_t pr, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(fbf16x2_t, pr), __builtin_bit_cast(fbf16x2_t, kOnePair), c,
+                                           false);
+  }
 };
 template <>
 struct FlashElem<AEKV_F16> {
@@ -97,6 +104,9 @@ struct FlashElem<AEKV_F16> {
   static constexpr uint32_t kOnePair = 0x3C003C00u;
   __device__ static ff32x16_t mma(v8 a, v8 b, ff32x16_t c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
   __device__ static uint32_t pack(float lo, float hi) { return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16); }
+  __device__ static float add_pair(uint32_t pr, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(ff16x2_t, pr), __builtin_bit_cast(ff16x2_t, kOnePair), c, false);
+  }
 };
 
 // chunk c of key r sits at c ^ chunk_swizzle(r % 16) of its 256-byte LDS row
@@ -303,12 +313,11 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   };
 
   // m_run: the row's running maximum over this wave's keys, in scaled log2 units (the same in both
-  // lane halves).  lsum: the row's sum of the bf16 weights (every element holds it).
-  float m_run = kFNegInf;
-  ff32x16_t O[4], lsum = {};
+  // lane halves).  lsum: the sum of this lane's bf16 weights of the row (its half of the keys).
+  float m_run = kFNegInf, lsum = 0.0f;
+  ff32x16_t O[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) O[mb] = ff32x16_t{};
-  const v8 ones = __builtin_bit_cast(v8, make_uint4(E::kOnePair, E::kOnePair, E::kOnePair, E::kOnePair));
 
   // Each tile is loaded into the other LDS buffer while the current one is used; its loads have
   // landed (this wave's: the wait; every wave's: the barrier) before the step that reads it.  The
@@ -364,7 +373,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     if (__builtin_amdgcn_ballot_w64(mt > m_run)) {  // some row's maximum moved up
       const float m_new = fmaxf(m_run, mt);
       const float alpha = m_new == kFNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-      lsum[0] *= alpha;  // the only element read (the products add the same sum to every element)
+      lsum *= alpha;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) O[mb] *= alpha;
       m_run = m_new;
@@ -378,9 +387,9 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
         float p[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * c + j], a.scale2, nm));
-        const v8 pb = __builtin_bit_cast(
-            v8, make_uint4(E::pack(p[0], p[1]), E::pack(p[2], p[3]), E::pack(p[4], p[5]), E::pack(p[6], p[7])));
-        lsum = E::mma(ones, pb, lsum);
+        const uint4 pw = make_uint4(E::pack(p[0], p[1]), E::pack(p[2], p[3]), E::pack(p[4], p[5]), E::pack(p[6], p[7]));
+        const v8 pb = __builtin_bit_cast(v8, pw);
+        lsum = E::add_pair(pw.w, E::add_pair(pw.z, E::add_pair(pw.y, E::add_pair(pw.x, lsum))));
         v8 va[4];  // the chunk's V^T operands, read before their products
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
@@ -402,6 +411,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     step(it, IntC<0>{});
     if (it + 1 < it1) step(it + 1, IntC<1>{});
   }
+  lsum += xor_lane<32>(lsum);  // the row's sum over both lane halves
 
   // merge the two key halves of each row half (through the tile buffers, free after the last
   // barrier): key half 1 writes its state, key half 0 combines and stores
@@ -412,7 +422,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
       for (int v = 0; v < 16; ++v) ob[(mb * 16 + v) * 64 + lane] = O[mb][v];
     s_ml[rh][0][lane] = m_run;
-    s_ml[rh][1][lane] = lsum[0];
+    s_ml[rh][1][lane] = lsum;
   }
   __syncthreads();
   if (kh == 1 || !rv) return;
@@ -420,7 +430,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const float mm = fmaxf(m_run, m1);
   const float f0 = m_run == kFNegInf ? 0.0f : exp2f(m_run - mm);
   const float f1 = m1 == kFNegInf ? 0.0f : exp2f(m1 - mm);
-  const float l_run = lsum[0] * f0 + l1 * f1;
+  const float l_run = lsum * f0 + l1 * f1;
   if (Gm::kSplit && nsp > 1) {
     // one piece: the row's (max, sum, O) relative to mm, merged with the sink by the combine
     float* dst = a.part + ((static_cast<int64_t>(b) * RT + r) * a.n_split + split) * (kFD + 4);
