@@ -32,7 +32,7 @@ SYMBOLS = (
     "aekv_tq_encode", "aekv_tq_decode", "aekv_csa_indexer_workspace_size", "aekv_csa_indexer_topk",
     "aekv_csa_indexer_topk_quant", "aekv_sparse_sink_attention", "aekv_quant_attention_workspace_size",
     "aekv_quant_sink_attention", "aekv_hca_compress", "aekv_tiled_prefill_attention", "aekv_set_generic_kernels",
-    "aekv_emit_block", "aekv_csa_prefill_indexer_topk_quant", "aekv_quant_prefill_workspace_size",
+    "aekv_set_flash_rows", "aekv_emit_block", "aekv_csa_prefill_indexer_topk_quant", "aekv_quant_prefill_workspace_size",
     "aekv_quant_prefill_attention", "aekv_rope_rmsnorm", "aekv_csa_indexer_topk_quant_noalloc",
     "aekv_csa_decode_workspace_size", "aekv_csa_decode_quant", "aekv_sparse_sink_attention_ws",
     "aekv_tiled_prefill_attention_ws", "aekv_sink_attention_workspace_size", "aekv_stream_probe",
@@ -68,6 +68,7 @@ def lib() -> ctypes.CDLL:
         "aekv_max_head_dim": ([], I32_),
         "aekv_max_topk": ([], I32_),
         "aekv_set_generic_kernels": ([ctypes.c_int], ctypes.c_int),
+        "aekv_set_flash_rows": ([ctypes.c_int], ctypes.c_int),
         "aekv_tq_diag": ([I64_, I32_, P], ctypes.c_int),
         "aekv_wht": ([P, I32_, I64_, I32_, P, P], ctypes.c_int),
         "aekv_tq_encode": ([P, I32_, I64_, I32_, I32_, P, P, P, P], ctypes.c_int),

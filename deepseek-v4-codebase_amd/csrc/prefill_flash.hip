@@ -47,15 +47,16 @@
 // wave-uniform branch taken on tiles that raise some row's maximum.  The normaliser is the sum of
 // the very bf16 weights the numerator used: each lane adds its own weights of the row with
 // v_dot2_f32_bf16 (f16) against ones, and the two lane halves are added at the end.  Tiles that every row of the workgroup sees in full skip the masks.
+#include <atomic>
+
 #include "tq_device.h"
 
 namespace aekv {
 namespace {
 
 constexpr int kFD = 128;
-constexpr int kFThreads = 256;        // 4 waves
-constexpr int kFRows = 64;            // query rows per workgroup (32 per row half)
 constexpr int kTileBytes = 32768;     // one LDS tile buffer
+constexpr int kSlotFloats = 4096;     // one wave's merge state in LDS: O of 32 rows x 128 dims
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kFNegInf = -__builtin_inff();
 constexpr int kBufWord3 = 0x00020000;  // buffer resource word 3: raw 32-bit data, range-checked
@@ -70,17 +71,30 @@ typedef __attribute__((address_space(3))) fi16x4_t lds_i16x4_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Source rows of ROWB bytes: 256 (K = V) or 512 (K, then V).  A tile holds kTile rows (32 KB).
-template <int ROWB>
+// A workgroup has RG groups of 32 query rows and splits every tile's keys KS ways: wave w takes
+// row group w % RG and keys [kKW (w / RG), + kKW) of each tile.  Two shapes are instantiated:
+// RG = 2, KS = 2 (4 waves, 64 rows, two workgroups per CU) and, for K = V rows, RG = 3, KS = 4
+// (12 waves, 96 rows, one workgroup and three waves per SIMD).
+template <int ROWB, int RG, int KS>
 struct FlashGeom {
   static_assert(ROWB == 256 || ROWB == 512, "rows of K (= V) or of K then V");
+  static_assert(KS == 2 || KS == 4, "the key splits merge pairwise");
   static constexpr int kRowBytes = ROWB;
+  static constexpr int kWaves = RG * KS, kThreads = 64 * kWaves, kRows = 32 * RG;
+  static constexpr int kWavesPerSimd = kWaves == 4 ? 2 : 3;  // resident waves per SIMD (register budget)
   static constexpr int kTile = kTileBytes / ROWB;       // sources per tile (128 or 64)
-  static constexpr int kKW = kTile / 2;                 // sources per wave and tile
+  static constexpr int kKW = kTile / KS;                // sources per wave and tile
   static constexpr int kKB = kKW / 32;                  // 32-key score blocks per wave and tile
-  static constexpr int kChunks = kTileBytes / (16 * kFThreads);  // staging chunks per thread and tile
+  static constexpr int kLoadWaves = kWaves < 8 ? kWaves : 8;  // waves that stage the tiles
+  static constexpr int kPass = 1024 * kLoadWaves;       // bytes of a tile per staging pass
+  static constexpr int kChunks = kTileBytes / kPass;    // staging passes per tile
   static constexpr int kVOff = ROWB == 256 ? 0 : 256;   // V's byte offset in a row
   static constexpr bool kSplit = ROWB == 512;           // the dense caller may split a row's sources
-  static_assert(kKB >= 1, "tiles are whole 32-key blocks per wave");
+  static constexpr int kSlots = RG * KS / 2;            // merge states in LDS at once (16 KB each)
+  static constexpr int kMergeExtra = kSlots > 4 ? (kSlots - 4) * kSlotFloats * 4 : 16;  // beyond the tiles
+  static_assert(kKB >= 1 && kKW % 32 == 0, "tiles are whole 32-key blocks per wave");
+  static_assert(kTileBytes % kPass == 0 && kPass % ROWB == 0, "whole rows per staging pass");
+  static_assert(kSlots <= 6, "merge slots");
 };
 
 // The element type's matrix instruction, weight rounding and constants.
@@ -165,20 +179,22 @@ struct FlashArgs {
 // loop (the matrix instructions take VGPR operands) instead of moving to AGPRs and back, and the
 // scheduler may spend registers on reading LDS operands ahead of the products.  A launch has about
 // 1.5 workgroups per CU at the bench shape, so more resident waves would not exist anyway.
-template <int DT, int ROWB>
-__global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_sink_attn_kernel(
-    FlashArgs a) {
-  using Gm = FlashGeom<ROWB>;
+template <int DT, int ROWB, int RG, int KS>
+__global__ __launch_bounds__(64 * RG * KS) __attribute__((
+    amdgpu_waves_per_eu(FlashGeom<ROWB, RG, KS>::kWavesPerSimd, FlashGeom<ROWB, RG, KS>::kWavesPerSimd))) void
+flash_sink_attn_kernel(FlashArgs a) {
+  using Gm = FlashGeom<ROWB, RG, KS>;
   using E = FlashElem<DT>;
   using v8 = typename E::v8;
   constexpr int kRowBytes = Gm::kRowBytes, kFTile = Gm::kTile, kKW = Gm::kKW, kKB = Gm::kKB;
-  constexpr int kChunks = Gm::kChunks, kVOff = Gm::kVOff;
+  constexpr int kChunks = Gm::kChunks, kVOff = Gm::kVOff, kPass = Gm::kPass, kWaves = Gm::kWaves;
   // the two tile buffers, [key][swizzled 16-byte chunks]: separate arrays, so that the compiler
   // sees that the loads into one do not write what is read from the other
   __shared__ __align__(16) uint8_t Ls0[kTileBytes];
   __shared__ __align__(16) uint8_t Ls1[kTileBytes];
-  __shared__ int s_rng[4][4];                          // per wave: max blocks, min blocks, window lo, hi
-  __shared__ float s_ml[2][2][64];                     // key half 1's (m, l) per row half and lane
+  __shared__ __align__(16) uint8_t Lm[Gm::kMergeExtra];  // merge slots beyond the tile buffers
+  __shared__ int s_rng[kWaves][4];                     // per wave: max blocks, min blocks, window lo, hi
+  __shared__ float s_ml[Gm::kSlots][2][64];            // (m, l) of the merge slots per lane
 
   // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2): renumber them so
   // that XCD x runs the consecutive range [x n/8, (x+1) n/8), i.e. whole sequences, whose blocks
@@ -192,12 +208,13 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   const int b = static_cast<int>(wgi / per_seq);
   const int wrow = static_cast<int>((wgi % per_seq) / nsp);
   const int split = static_cast<int>(wgi % nsp);
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int rh = wv & 1, kh = wv >> 1;  // row half, key half
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (a scalar register)
+  const int rh = wv % RG, kh = wv / RG;  // row group, key split
   const int rl = lane & 31, hh = lane >> 5;
   const int H = a.H;
   const int RT = a.T * H;
-  const int r = wrow * kFRows + 32 * rh + rl;  // this lane's row
+  const int r = wrow * Gm::kRows + 32 * rh + rl;  // this lane's row
   const bool rv = r < RT;
   const int t = rv ? static_cast<int>(static_cast<uint32_t>(r) / static_cast<uint32_t>(H)) : 0;
   const int h = rv ? r - t * H : 0;
@@ -225,7 +242,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   __syncthreads();
   int gmax = 0, nbmin = 0x7fffffff, wlo = 0x7fffffff, whi = 0;
 #pragma unroll
-  for (int w = 0; w < kFThreads / 64; ++w) {
+  for (int w = 0; w < kWaves; ++w) {
     gmax = max(gmax, s_rng[w][0]);
     nbmin = min(nbmin, s_rng[w][1]);
     wlo = min(wlo, s_rng[w][2]);
@@ -255,42 +272,41 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   // over the loop's back edge, becomes a wait for every tile load on every iteration
   __builtin_amdgcn_s_waitcnt(0);
 
-  // LDS byte offsets, fixed per lane (the tile and block offsets are multiples of 16 keys, which
-  // leave the swizzle unchanged, and become immediates).  The swizzle permutes the 16 chunks of
-  // each 256-byte half of a row.  Row-chunk reads (K): key kKW kh + 32 kb + rl, chunk 2 ks + hh.
-  // Transpose reads (V, 16-lane group G = lane / 16, s = lane % 16): key kKW kh + 16 c + 4 hh +
-  // s / 4 (+ 8 e), dims 32 mb + 16 (G % 2) + 4 (s % 4) .. + 3.
+  // LDS byte offsets per lane (the tile and block offsets are multiples of 16 keys, which leave
+  // the swizzle unchanged, and become immediates).  The swizzle permutes the 16 chunks of each
+  // 256-byte half of a row.
+  //   Row-chunk reads (K): key kKW kh + 32 kb + rl, chunk (2 ks + hh) ^ sigma(rl % 16), i.e.
+  //   byte sA ^ 32 ks with sA = row | 32 (sigma >> 1) | 16 (hh ^ sigma & 1) (the row's byte offset
+  //   is a multiple of 256, so the chunk bits are free).
+  //   Transpose reads (V, 16-lane group G = lane / 16, s = lane % 16): key kKW kh + 16 c + 4 hh +
+  //   s / 4 + 8 e, dims 32 mb + 16 (G % 2) + 4 (s % 4) .. + 3, i.e. chunk 4 mb + x with
+  //   x = 2 (G % 2) + (s % 4) / 2, xor sigma(key) = 4 (s / 4) + (hh | 2 e): byte
+  //   (tA ^ 64 mb ^ 32 e) + 8 e ROWB with tA = row(e = 0) + V offset | 64 (s / 4) | 16 (x ^ hh) | 8 (s % 2).
+  // Two registers instead of 16 offsets; the xors are recomputed per tile where registers are short.
   const int kbase = kKW * kh * kRowBytes;
-  int soff[8];
-#pragma unroll
-  for (int ks = 0; ks < 8; ++ks) soff[ks] = kbase + rl * kRowBytes + (((2 * ks + hh) ^ chunk_swizzle(rl & 15)) << 4);
-  int toff[2][4];
+  int sA, tA;
   {
+    const int sg = chunk_swizzle(rl & 15);
+    sA = (kbase + rl * kRowBytes) | ((sg >> 1) << 5) | ((hh ^ (sg & 1)) << 4);
     const int s16 = lane & 15, G = lane >> 4;
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int key = 4 * hh + (s16 >> 2) + 8 * e;
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-        toff[e][mb] = kbase + key * kRowBytes + kVOff +
-                      (((4 * mb + 2 * (G & 1) + ((s16 & 3) >> 1)) ^ chunk_swizzle(key)) << 4) + 8 * (s16 & 1);
-    }
+    const int x = 2 * (G & 1) + ((s16 & 3) >> 1);
+    tA = (kbase + (4 * hh + (s16 >> 2)) * kRowBytes + kVOff) | ((s16 >> 2) << 6) | ((x ^ hh) << 4) | ((s16 & 1) << 3);
   }
 
   const uint8_t* kseq = reinterpret_cast<const uint8_t*>(a.kblk) + static_cast<int64_t>(b) * a.S * kRowBytes;
   const uint8_t* wseq = reinterpret_cast<const uint8_t*>(a.win) + static_cast<int64_t>(b) * a.Wt * kRowBytes;
-  // Staging straight into LDS (buffer loads with the LDS bit): pass c of wave wv writes bytes
-  // [4096 c + 1024 wv, + 1024) of the tile buffer, lane l at + 16 l, so lane l loads the global
-  // chunk that the swizzle puts there: key k = (4096 c + 1024 wv + 16 l) / ROWB, slot
-  // j = (1024 wv + 16 l) % ROWB / 16 of it, i.e. chunk (j & 16) + ((j & 15) ^ sigma(k % 16)).  The
-  // pass's keys start at a multiple of 4096 / ROWB keys, so the offsets repeat with period 2
-  // (512-byte rows) or 1 (256-byte rows) in c; the pass's 4096 c goes in the scalar offset.
+  // Staging straight into LDS (buffer loads with the LDS bit) by the first kLoadWaves waves
+  // (P = 1024 kLoadWaves bytes per pass): pass c of wave wv writes bytes [P c + 1024 wv, + 1024) of
+  // the tile buffer, lane l at + 16 l, so lane l loads the global chunk that the swizzle puts there:
+  // key k = (P c + 1024 wv + 16 l) / ROWB, slot j = (1024 wv + 16 l) % ROWB / 16 of it, i.e. chunk
+  // (j & 16) + ((j & 15) ^ sigma(k % 16)).  The pass's keys start at a multiple of P / ROWB keys
+  // (8, 16 or 32), so the offsets repeat with period 2 or 1 in c; P c goes in the scalar offset.
   int voff[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     const int lin = 1024 * wv + 16 * lane;
     const int kin = lin / kRowBytes, slot = (lin % kRowBytes) / 16;
-    const int ksw = ((4096 / kRowBytes) * p + kin) & 15;
+    const int ksw = ((kPass / kRowBytes) * p + kin) & 15;
     voff[p] = kin * kRowBytes + 16 * ((slot & 16) + ((slot & 15) ^ chunk_swizzle(ksw)));
   }
   // tile it into LDS buffer buf: keys [base, base + TILE) of the blocks (it < n_bt) or of the
@@ -298,7 +314,9 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   // the rows past it are zero (never attended) without a branch or an access.  A tile past the last
   // has an empty range: its loads are issued (no branch, so the wait counts stay exact) but touch
   // no memory.
-  auto load_tile = [&](int it, auto buf_c) {
+  // (the tile bounds are captured by value: selecting between two captured references puts them
+  // in scratch memory)
+  auto load_tile = [&, gmax, whi, wlo, n_bt, it1, kseq, wseq](int it, auto buf_c) {
     uint8_t* const dst = decltype(buf_c)::value ? Ls1 : Ls0;
     const bool blk = it < n_bt;
     const int base = blk ? it * kFTile : wlo + (it - n_bt) * kFTile;
@@ -306,10 +324,12 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     const uint8_t* src = (blk ? kseq : wseq) + static_cast<int64_t>(it < it1 ? base : 0) * kRowBytes;
     const int n_bytes = it < it1 ? min(lim - base, kFTile) * kRowBytes : 0;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), 0, n_bytes, kBufWord3);
+    if (Gm::kLoadWaves == kWaves || wv < Gm::kLoadWaves) {
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + 4096 * c + 1024 * wv), 16, voff[c & 1],
-                                               4096 * c, 0, 0);
+      for (int c = 0; c < kChunks; ++c)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + kPass * c + 1024 * wv), 16, voff[c & 1],
+                                                 kPass * c, 0, 0);
+    }
   };
 
   // m_run: the row's running maximum over this wave's keys, in scaled log2 units (the same in both
@@ -330,6 +350,8 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     constexpr int buf = decltype(buf_c)::value;  // LDS buffer of tile it
     load_tile(it + 1, IntC<buf ^ 1>{});  // the other buffer was last read before the previous barrier
     const uint8_t* lt = buf ? Ls1 : Ls0;
+    int sa = sA, ta = tA;
+    if constexpr (Gm::kWavesPerSimd > 2) asm volatile("" : "+v"(sa), "+v"(ta));  // not hoisted: recomputed per tile
 
     // S^T for keys 32 kb + 8 q + 4 hh + r of this wave's half tile, row rl (s[kb][4 q + r])
     ff32x16_t s[kKB];
@@ -338,7 +360,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) kv[kb][ks] = *reinterpret_cast<const uint4*>(lt + 32 * kRowBytes * kb + soff[ks]);
+        for (int ks = 0; ks < 8; ++ks) kv[kb][ks] = *reinterpret_cast<const uint4*>(lt + 32 * kRowBytes * kb + (sa ^ (ks << 5)));
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb) {
         s[kb] = ff32x16_t{};
@@ -394,8 +416,8 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
           const uint8_t* q0 = lt + (32 * kb + 16 * c) * kRowBytes;
-          const fi16x4_t lo4 = lds_read_tr16(q0 + toff[0][mb]);
-          const fi16x4_t hi4 = lds_read_tr16(q0 + toff[1][mb]);
+          const fi16x4_t lo4 = lds_read_tr16(q0 + (ta ^ (mb << 6)));
+          const fi16x4_t hi4 = lds_read_tr16(q0 + 8 * kRowBytes + (ta ^ (mb << 6) ^ 32));
           va[mb] = __builtin_bit_cast(v8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
         }
 #pragma unroll
@@ -413,54 +435,74 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
   }
   lsum += xor_lane<32>(lsum);  // the row's sum over both lane halves
 
-  // merge the two key halves of each row half (through the tile buffers, free after the last
-  // barrier): key half 1 writes its state, key half 0 combines and stores
-  float* ob = reinterpret_cast<float*>(Ls0) + rh * (4 * 16 * 64);  // [mb][v][lane]
-  if (kh == 1) {
+  // Merge the KS key splits of each row group through LDS (the tile buffers, free after the last
+  // barrier, then Lm), pairwise: split 2j + 1 writes its (m, l, O) to a slot and split 2j folds it
+  // in; with four splits, split 2 then hands its result to split 0.  Split 0 writes the rows.
+  auto slot = [&](int i) -> float* {  // [mb][v][lane]
+    return i < 2 ? reinterpret_cast<float*>(Ls0) + kSlotFloats * i
+           : i < 4 ? reinterpret_cast<float*>(Ls1) + kSlotFloats * (i - 2)
+                   : reinterpret_cast<float*>(Lm) + kSlotFloats * (i - 4);
+  };
+  auto put = [&](int i) {
+    float* ob = slot(i);
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) ob[(mb * 16 + v) * 64 + lane] = O[mb][v];
-    s_ml[rh][0][lane] = m_run;
-    s_ml[rh][1][lane] = lsum;
+    s_ml[i][0][lane] = m_run;
+    s_ml[i][1][lane] = lsum;
+  };
+  auto fold = [&](int i) {
+    const float* ob = slot(i);
+    const float m1 = s_ml[i][0][lane], l1 = s_ml[i][1][lane];
+    const float mm = fmaxf(m_run, m1);
+    const float f0 = m_run == kFNegInf ? 0.0f : exp2f(m_run - mm);
+    const float f1 = m1 == kFNegInf ? 0.0f : exp2f(m1 - mm);
+    lsum = lsum * f0 + l1 * f1;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) O[mb][v] = O[mb][v] * f0 + ob[(mb * 16 + v) * 64 + lane] * f1;
+    m_run = mm;
+  };
+  {
+    const int pslot = rh * (KS / 2) + (kh >> 1);
+    if (kh & 1) put(pslot);
+    __syncthreads();
+    if (!(kh & 1)) fold(pslot);
+    if constexpr (KS == 4) {
+      __syncthreads();  // every fold above has read its slot
+      if (kh == 2) put(rh * 2);
+      __syncthreads();
+      if (kh == 0) fold(rh * 2);
+    }
   }
-  __syncthreads();
-  if (kh == 1 || !rv) return;
-  const float m1 = s_ml[rh][0][lane], l1 = s_ml[rh][1][lane];
-  const float mm = fmaxf(m_run, m1);
-  const float f0 = m_run == kFNegInf ? 0.0f : exp2f(m_run - mm);
-  const float f1 = m1 == kFNegInf ? 0.0f : exp2f(m1 - mm);
-  const float l_run = lsum * f0 + l1 * f1;
+  if (kh != 0 || !rv) return;
   if (Gm::kSplit && nsp > 1) {
-    // one piece: the row's (max, sum, O) relative to mm, merged with the sink by the combine
+    // one piece: the row's (max, sum, O) relative to its max, merged with the sink by the combine
     float* dst = a.part + ((static_cast<int64_t>(b) * RT + r) * a.n_split + split) * (kFD + 4);
     if (hh == 0) {
-      dst[0] = mm;
-      dst[1] = l_run;
+      dst[0] = m_run;
+      dst[1] = lsum;
     }
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float4 o;
-        o.x = O[mb][4 * q] * f0 + ob[(mb * 16 + 4 * q) * 64 + lane] * f1;
-        o.y = O[mb][4 * q + 1] * f0 + ob[(mb * 16 + 4 * q + 1) * 64 + lane] * f1;
-        o.z = O[mb][4 * q + 2] * f0 + ob[(mb * 16 + 4 * q + 2) * 64 + lane] * f1;
-        o.w = O[mb][4 * q + 3] * f0 + ob[(mb * 16 + 4 * q + 3) * 64 + lane] * f1;
-        *reinterpret_cast<float4*>(dst + 4 + 32 * mb + 8 * q + 4 * hh) = o;
-      }
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4*>(dst + 4 + 32 * mb + 8 * q + 4 * hh) =
+            make_float4(O[mb][4 * q], O[mb][4 * q + 1], O[mb][4 * q + 2], O[mb][4 * q + 3]);
     return;
   }
-  // the sink, counted once: out = O / (l + e^{sink - m}) with m = max(mm, sink)
+  // the sink, counted once: out = O / (l + e^{sink - m}) with m = max(m_run, sink)
   const int sh = a.sink_scalar ? 0 : h;
   const float skv = a.sink_dt == AEKV_F32   ? static_cast<const float*>(a.sink)[sh]
                     : a.sink_dt == AEKV_F16 ? f16_to_f32(static_cast<const uint16_t*>(a.sink)[sh])
                                             : bf16_to_f32(static_cast<const uint16_t*>(a.sink)[sh]);
   const float sk = skv * kLog2e;
-  const float mf = fmaxf(mm, sk);
-  const float fo = mm == kFNegInf ? 0.0f : exp2f(mm - mf);
-  const float L = fmaf(l_run, fo, exp2f(sk - mf));
-  const float rs0 = f0 * fo / L, rs1 = f1 * fo / L;
+  const float mf = fmaxf(m_run, sk);
+  const float fo = m_run == kFNegInf ? 0.0f : exp2f(m_run - mf);
+  const float L = fmaf(lsum, fo, exp2f(sk - mf));
+  const float rs = fo / L;
   uint16_t* orow = a.out + (static_cast<int64_t>(b) * RT + r) * kFD;  // r < RT here
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
@@ -468,10 +510,7 @@ __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     for (int q = 0; q < 4; ++q) {
       float o[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int v = 4 * q + i;
-        o[i] = O[mb][v] * rs0 + ob[(mb * 16 + v) * 64 + lane] * rs1;
-      }
+      for (int i = 0; i < 4; ++i) o[i] = O[mb][4 * q + i] * rs;
       *reinterpret_cast<uint2*>(orow + 32 * mb + 8 * q + 4 * hh) = make_uint2(E::pack(o[0], o[1]), E::pack(o[2], o[3]));
     }
 }
@@ -486,12 +525,16 @@ bool hca_prefill_flash_supported(int64_t H, int64_t D) { return D == kFD && H >=
 
 namespace {
 
+using HcaNarrow = FlashGeom<256, 2, 2>;  // 64 rows, 4 waves
+using HcaWide = FlashGeom<256, 3, 4>;    // 96 rows, 12 waves
+using DenseGeom = FlashGeom<512, 2, 2>;
+
 // Grid and index limits shared by both callers; fills the launch fields of a.
-int flash_prepare(FlashArgs& a, int64_t B, int64_t T, int64_t H, int64_t S, int64_t Wt, int tile, float softmax_scale,
-                  const char* who) {
+int flash_prepare(FlashArgs& a, int64_t B, int64_t T, int64_t H, int64_t S, int64_t Wt, int tile, int rows,
+                  float softmax_scale, const char* who) {
   const int64_t RT = T * H;
-  const int64_t gx = ceil_div(RT, kFRows);
-  if (gx * B > 0x7fffffff || RT > 0x7fffffff - kFRows) return fail(AEKV_ERR_UNSUPPORTED, "%s: grid too large", who);
+  const int64_t gx = ceil_div(RT, rows);
+  if (gx * B > 0x7fffffff || RT > 0x7fffffff - rows) return fail(AEKV_ERR_UNSUPPORTED, "%s: grid too large", who);
   if (S > 0x7fffffff - tile || Wt > 0x7fffffff - tile)
     return fail(AEKV_ERR_UNSUPPORTED, "%s: %lld sources / %lld window entries exceed the int32 indexing", who,
                 (long long)S, (long long)Wt);
@@ -504,14 +547,43 @@ int flash_prepare(FlashArgs& a, int64_t B, int64_t T, int64_t H, int64_t S, int6
   return AEKV_OK;
 }
 
+std::atomic<int> g_hca_rows{0};  // 0: chosen per launch; 64 or 96: forced (aekv_set_flash_rows)
+
+// Compute units of the current device (cached per device).
+int64_t device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64) {
+    if (const int c = cached[dev].load(std::memory_order_relaxed)) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev < 64) cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 }  // namespace
+
+// The 96-row shape when it leaves fewer rows on the busiest CU: two 64-row workgroups or one
+// 96-row workgroup per CU at a time (e.g. 8 x 3072 rows: 384 narrow workgroups put 128 rows on
+// half of the 256 CUs; 256 wide ones put 96 on each).
+bool hca_flash_wide(int64_t B, int64_t T, int64_t H) {
+  const int forced = g_hca_rows.load(std::memory_order_relaxed);
+  if (forced) return forced == HcaWide::kRows;
+  const int64_t cus = device_cus();
+  const int64_t n_narrow = B * ceil_div(T * H, HcaNarrow::kRows), n_wide = B * ceil_div(T * H, HcaWide::kRows);
+  return ceil_div(n_wide, cus) * HcaWide::kRows < ceil_div(n_narrow, 2 * cus) * 2 * HcaNarrow::kRows;
+}
 
 int launch_hca_prefill_flash(const void* q, const void* kblk, const void* window, const int32_t* vis,
                              const int32_t* wstart, const int32_t* wlen, const float* sink, int64_t B, int64_t T,
                              int64_t H, int64_t S, int64_t Wt, float softmax_scale, void* out, hipStream_t st,
                              const char* who) {
   FlashArgs a{};
-  if (int rc = flash_prepare(a, B, T, H, S, Wt, FlashGeom<256>::kTile, softmax_scale, who)) return rc;
+  const bool wide = hca_flash_wide(B, T, H);
+  const int rows = wide ? HcaWide::kRows : HcaNarrow::kRows;
+  if (int rc = flash_prepare(a, B, T, H, S, Wt, HcaNarrow::kTile, rows, softmax_scale, who)) return rc;
   if (T * H == 0 || B == 0) return AEKV_OK;
   a.q = static_cast<const uint16_t*>(q);
   a.kblk = static_cast<const uint16_t*>(kblk);
@@ -524,19 +596,20 @@ int launch_hca_prefill_flash(const void* q, const void* kblk, const void* window
   a.sink_scalar = 0;
   a.n_split = 1;
   a.out = static_cast<uint16_t*>(out);
-  hipLaunchKernelGGL((flash_sink_attn_kernel<AEKV_BF16, 256>), dim3(a.gx * static_cast<uint32_t>(B)), dim3(kFThreads),
-                     0, st, a);
+  const dim3 grid(a.gx * static_cast<uint32_t>(B));
+  if (wide) hipLaunchKernelGGL((flash_sink_attn_kernel<AEKV_BF16, 256, 3, 4>), grid, dim3(HcaWide::kThreads), 0, st, a);
+  else hipLaunchKernelGGL((flash_sink_attn_kernel<AEKV_BF16, 256, 2, 2>), grid, dim3(HcaNarrow::kThreads), 0, st, a);
   return check_launch(who);
 }
 
-int64_t dense_flash_row_blocks(int64_t T, int64_t H) { return ceil_div(T * H, kFRows); }
-int64_t dense_flash_tile() { return FlashGeom<512>::kTile; }
+int64_t dense_flash_row_blocks(int64_t T, int64_t H) { return ceil_div(T * H, DenseGeom::kRows); }
+int64_t dense_flash_tile() { return DenseGeom::kTile; }
 
 int launch_dense_flash_attention(const void* q, const void* kv, const void* sink, int sink_scalar, int32_t dtype,
                                  int64_t B, int64_t T, int64_t H, int64_t S, float softmax_scale, int n_split,
                                  float* part, void* out, hipStream_t st, const char* who) {
   FlashArgs a{};
-  if (int rc = flash_prepare(a, B, T, H, S, 0, FlashGeom<512>::kTile, softmax_scale, who)) return rc;
+  if (int rc = flash_prepare(a, B, T, H, S, 0, DenseGeom::kTile, DenseGeom::kRows, softmax_scale, who)) return rc;
   if (T * H == 0 || B == 0) return AEKV_OK;
   if (n_split < 1 || (n_split > 1 && !part)) return fail(AEKV_ERR_VALUE, "%s: bad source split", who);
   if (static_cast<int64_t>(a.gx) * B * n_split > 0x7fffffff) return fail(AEKV_ERR_UNSUPPORTED, "%s: grid too large", who);
@@ -549,9 +622,16 @@ int launch_dense_flash_attention(const void* q, const void* kv, const void* sink
   a.sink_scalar = sink_scalar;
   a.out = static_cast<uint16_t*>(out);
   const dim3 grid(a.gx * static_cast<uint32_t>(B) * static_cast<uint32_t>(n_split));
-  if (dtype == AEKV_F16) hipLaunchKernelGGL((flash_sink_attn_kernel<AEKV_F16, 512>), grid, dim3(kFThreads), 0, st, a);
-  else hipLaunchKernelGGL((flash_sink_attn_kernel<AEKV_BF16, 512>), grid, dim3(kFThreads), 0, st, a);
+  if (dtype == AEKV_F16)
+    hipLaunchKernelGGL((flash_sink_attn_kernel<AEKV_F16, 512, 2, 2>), grid, dim3(DenseGeom::kThreads), 0, st, a);
+  else hipLaunchKernelGGL((flash_sink_attn_kernel<AEKV_BF16, 512, 2, 2>), grid, dim3(DenseGeom::kThreads), 0, st, a);
   return check_launch(who);
 }
 
 }  // namespace aekv
+
+extern "C" int aekv_set_flash_rows(int rows) {
+  if (rows != 0 && rows != aekv::HcaNarrow::kRows && rows != aekv::HcaWide::kRows)
+    return aekv::fail(AEKV_ERR_VALUE, "aekv_set_flash_rows: rows must be 0, 64 or 96, got %d", rows);
+  return aekv::g_hca_rows.exchange(rows);
+}

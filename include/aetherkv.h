@@ -82,6 +82,13 @@ int32_t aekv_max_topk(void);       /* largest k accepted by the indexer select (
  * environment sets AETHERKV_CODEC=generic).  Both produce identical results.  Returns the
  * previous setting. */
 int aekv_set_generic_kernels(int generic_only);
+/* Workgroup shape of the HCA prefill flash kernel (no reference counterpart; a testing and A/B
+ * aid): 0 = chosen per launch (default), 64 = four waves over 64 (target, head) rows, 96 = twelve
+ * waves over 96 rows.  Both compute the same attention within the bf16 tolerance (they split
+ * and merge each row's keys differently, so single outputs may differ in the last bit).  Returns
+ * the previous setting (0, 64 or 96), or AEKV_ERR_VALUE (1) for any other value, which changes
+ * nothing. */
+int aekv_set_flash_rows(int rows);
 
 /* ---- TurboQuant codec -------------------------------------------------------------------- */
 /* Rademacher diagonal of PolarQuant(seed)._diag(d): MT19937 seeded with seed*10007+d, one

@@ -41,6 +41,16 @@ def _inputs(dev, B, T, H, S, Wt, bits, seed, D=128):
     return pq, codes, scale, q, win, sink
 
 
+@pytest.fixture(params=[64, 96])
+def flash_rows(request):
+    """Run an HCA case on each workgroup shape of the flash kernel (64 rows / 4 waves, 96 rows / 12
+    waves); the default picks one per launch."""
+    from aetherkv import _lib as L
+    prev = L.lib().aekv_set_flash_rows(request.param)
+    yield request.param
+    L.lib().aekv_set_flash_rows(prev)
+
+
 def _oracle_target(pq, codes, scale, sel_np, q_t, win_t, sink, sm):
     B, H, D = q_t.shape
     return O.quant_attention(to_np_f32(q_t), codes.cpu().numpy(), scale.cpu().numpy(), sel_np, to_np_f32(win_t),
@@ -54,11 +64,11 @@ def _oracle_target(pq, codes, scale, sel_np, q_t, win_t, sink, sm):
     (4, 2, 200, 12, 6300, 128, 128, 60, 64),  # the model's HCA shape: a block edge inside the chunk
     (8, 1, 70, 5, 37, 4, 20, 30, 40),       # rows per workgroup not a multiple of the head count
 ])
-def test_hca_prefill_matches_oracle_and_decode(dev, bits, B, T, H, start, M, W, nb, S):
+def test_hca_prefill_matches_oracle_and_decode(dev, flash_rows, bits, B, T, H, start, M, W, nb, S):
     Wt = W - 1 + T
     pq, codes, scale, q, win, sink = _inputs(dev, B, T, H, S, Wt, bits, 7 + T)
     sm = 128 ** -0.5
-    print(f"hca prefill bits={bits} B={B} T={T} H={H} start={start} nb={nb}", flush=True)
+    print(f"hca prefill rows={flash_rows} bits={bits} B={B} T={T} H={H} start={start} nb={nb}", flush=True)
     out = hca_prefill(q, codes, scale, win, sink, sm, kv_quant=pq, start=start, n_blocks=nb, compression=M,
                       sliding_window=W)
     torch.cuda.synchronize()
@@ -176,6 +186,41 @@ def test_multi_target_indexer_many_rows(dev):
         tol = score_error_bound(qn, np.log1p(np.exp(wn.astype(np.float64))), keys,
                                 extra_rel=16 * math.log2(IC) * 2.0 ** -24)
         assert_topk_matches(idx[:, t].cpu().numpy(), scores, k, tol, vt)
+
+
+def test_hca_prefill_chunk_both_workgroup_shapes(dev):
+    # The bench's HCA chunk (B=8, T=256 targets at the end of a 262144-token prompt, 2048 4-bit
+    # blocks, H=12, W=128): 24576 (target, head) rows, where the default launch takes the 96-row
+    # shape on a 256-CU device.  Both shapes against the oracle on sampled targets, against each
+    # other within the tolerance, and the default bit for bit against the shape it picked.
+    from aetherkv import _lib as L
+    B, T, H, S, M, W, bits = 8, 256, 12, 2048, 128, 128, 4
+    start, Wt = S * M - T, W - 1 + T
+    pq, codes, scale, q, win, sink = _inputs(dev, B, T, H, S, Wt, bits, 501)
+    sm = 128 ** -0.5
+    vis, ws, wl = prefill_sources(T, start, S, compression=M, sliding_window=W, window_base=start - (W - 1),
+                                  window_len=Wt)
+    args = dict(quant=pq, visible=vis.to(dev), win_start=ws.to(dev), win_len=wl.to(dev))
+    outs = {}
+    for rows in (0, 64, 96):
+        print(f"hca prefill chunk rows={rows}", flush=True)
+        prev = L.lib().aekv_set_flash_rows(rows)
+        try:
+            outs[rows] = quant_prefill_attention(q, codes, scale, None, win, sink, sm, **args)
+            torch.cuda.synchronize()
+        finally:
+            L.lib().aekv_set_flash_rows(prev)
+    assert torch.equal(outs[0], outs[64]) or torch.equal(outs[0], outs[96])
+    np.testing.assert_allclose(to_np_f32(outs[64]), to_np_f32(outs[96]), rtol=QUANT_RTOL, atol=QUANT_ATOL)
+    for t in (0, 1, 95, 96, 200, T - 1):
+        g, s0, n = int(vis[t]), int(ws[t]), int(wl[t])
+        for b in (0, B - 1):
+            sel = np.arange(g, dtype=np.int64)[None]
+            want = _oracle_target(pq, codes[b:b + 1], scale[b:b + 1], sel, q[b:b + 1, t],
+                                  win[b:b + 1, s0:s0 + n].contiguous(), sink, sm)
+            for rows in (64, 96):
+                np.testing.assert_allclose(to_np_f32(outs[rows][b, t])[None], want, rtol=QUANT_RTOL,
+                                           atol=QUANT_ATOL, err_msg=f"rows {rows} target {t} sequence {b}")
 
 
 def test_prefill_attention_defaults_and_empty_targets(dev):
