@@ -1,5 +1,5 @@
-// Flash-style matrix-core sink attention in which 64 (target, head) query rows share every source
-// tile, for two callers:
+// Flash-style matrix-core sink attention in which the (target, head) query rows of a workgroup (64
+// or 96) share every source tile, for two callers:
 //   * chunked-prefill HCA attention over dequantised blocks (bf16, K = V: rows of 256 bytes);
 //   * the dense drop-in tiled_prefill_attention (aether_kernels/sparse_attention.py:19-42, sink
 //     counted once as in aether_2b/modeling.py:158-178) when a call has 64 or more (target, head)
@@ -17,14 +17,15 @@
 //   row r = t * H + h of sequence b; source j < g_t (block) or window entry e in
 //   [win_start_t, win_start_t + win_len_t).
 //
-// Work split.  A workgroup (4 waves) owns 64 consecutive rows.  The sources of its targets
-// (blocks [0, max g), window [min start, max end)) stream through LDS in tiles of TILE keys,
+// Work split.  A workgroup owns 32 RG consecutive rows (RG row groups of 32).  The sources of its
+// targets (blocks [0, max g), window [min start, max end)) stream through LDS in tiles of TILE keys,
 // row-major (key, 128 dims), in two alternating buffers (one barrier per tile), loaded by buffer
-// loads that write LDS directly (no register staging), one tile ahead.  Wave w takes row
-// half w % 2 (32 rows, lane l holds row l % 32) and key half w / 2 of every tile, so each wave
-// reads half a tile per step for 32 rows: with v_mfma_f32_32x32x16_bf16 every LDS byte feeds
-// twice the matrix work of a 16-row wave over the whole tile.  The two waves of a row half keep
-// separate online-softmax states, merged once at the end through LDS.
+// loads that write LDS directly (no register staging), one tile ahead.  Wave w takes row group
+// w % RG (32 rows, lane l holds row l % 32) and key split w / RG (TILE / KS keys) of every tile:
+// with v_mfma_f32_32x32x16_bf16 every LDS byte feeds twice the matrix work of a 16-row wave.  The
+// KS waves of a row group keep separate online-softmax states, merged once at the end through LDS.
+// Shapes: RG = 2, KS = 2 (4 waves, two workgroups per CU) for both callers; RG = 3, KS = 4 (12
+// waves, one workgroup and three waves per SIMD) for HCA when that balances the CUs better.
 //
 // Matrix layouts (v_mfma_f32_32x32x16_bf16, measured): A lane l holds A[l%32][8(l/32)+j], B lane l
 // holds B[8(l/32)+j][l%32], D lane l register v holds D[8(v/4) + 4(l/32) + v%4][l%32].
