@@ -167,6 +167,42 @@ def test_quant_attention_more_splits_than_a_combine_chunk(dev, bits):
     _close(got.view(B, H, D), _oracle_quant(pq, codes, scale, sel, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
 
 
+def test_split_rows_whatever_the_workspace_holds(dev):
+    # 1516 sources per row: two pieces and the combine.  The workspace's prior contents must not
+    # matter: zeros, all ones and random bytes give bit-identical results, equal to the oracle.
+    from aetherkv.decode import attention_workspace
+    B, H, D, S, W, bits = 3, 12, 128, 1500, 16, 4
+    pq, codes, scale, q, win, sink = _quant_inputs(dev, B, H, D, S, W, bits, 77)
+    sm = D ** -0.5
+    ws = attention_workspace(B, H, D, S, W, dev)
+    outs = []
+    for fill in ("zeros", "ones", "random", "random"):
+        if fill == "zeros":
+            ws.zero_()
+        elif fill == "ones":
+            ws.fill_(255)
+        else:
+            ws.copy_(torch.randint(0, 256, ws.shape, dtype=torch.uint8, device=dev))
+        print(f"split merge, workspace {fill}", flush=True)
+        outs.append(quant_sink_attention(q, codes, scale, None, win, sink, sm, quant=pq, workspace=ws))
+        torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    _close(outs[0].view(B, H, D), _oracle_quant(pq, codes, scale, None, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
+
+
+@pytest.mark.parametrize("S", [130400, 130900])
+def test_quant_attention_most_pieces(dev, S):
+    # one row, S blocks + 128 window rows in pieces of 512: 255 pieces, and 256 (the launch limit);
+    # the combine merges 32 chunks of 8 pieces
+    B, H, D, W, bits = 1, 12, 128, 128, 4
+    pq, codes, scale, q, win, sink = _quant_inputs(dev, B, H, D, S, W, bits, 88)
+    sm = D ** -0.5
+    print(f"quant attention {S + W} sources", flush=True)
+    got = hca_decode(q, codes, scale, win, sink, sm, kv_quant=pq)
+    _close(got.view(B, H, D), _oracle_quant(pq, codes, scale, None, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
+
+
 def test_config3_csa_decode_end_to_end(dev):
     # benchmark configuration cfg3: B=8, 16384 blocks, 8-bit codes, indexer 4x64 softplus, top-256 + window 128 + sink
     B, H, D, S, W, IH, IC = 8, 12, 128, 16384, 128, 4, 64
