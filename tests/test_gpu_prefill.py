@@ -188,6 +188,30 @@ def test_multi_target_indexer_many_rows(dev):
         assert_topk_matches(idx[:, t].cpu().numpy(), scores, k, tol, vt)
 
 
+def test_hca_prefill_window_only(dev, flash_rows):
+    # no compressed block yet (an empty cache): every target attends its window slice and the sink
+    B, T, H, W, bits = 2, 40, 12, 16, 4
+    Wt = W - 1 + T
+    pq = PolarQuant(bits)
+    codes = torch.zeros((B, 0, 64), dtype=torch.uint8, device=dev)
+    scale = torch.zeros((B, 0), dtype=torch.float32, device=dev)
+    q = normal((B, T, H, 128), 401).to(dev)
+    win = normal((B, Wt, 128), 402).to(dev)
+    sink = normal((H,), 403, dtype=torch.float32).to(dev)
+    sm = 128 ** -0.5
+    print(f"hca prefill window only rows={flash_rows}", flush=True)
+    out = hca_prefill(q, codes, scale, win, sink, sm, kv_quant=pq, start=0, n_blocks=0, compression=128,
+                      sliding_window=W)
+    torch.cuda.synchronize()
+    vis, ws, wl = prefill_sources(T, 0, 0, compression=128, sliding_window=W, window_base=T - Wt, window_len=Wt)
+    assert int(vis.max()) == 0
+    for t in range(T):
+        s0, n = int(ws[t]), int(wl[t])
+        want = _oracle_target(pq, codes, scale, np.zeros((B, 0), dtype=np.int64), q[:, t],
+                              win[:, s0:s0 + n].contiguous(), sink, sm)
+        np.testing.assert_allclose(to_np_f32(out[:, t]), want, rtol=QUANT_RTOL, atol=QUANT_ATOL, err_msg=f"target {t}")
+
+
 def test_hca_prefill_chunk_both_workgroup_shapes(dev):
     # The bench's HCA chunk (B=8, T=256 targets at the end of a 262144-token prompt, 2048 4-bit
     # blocks, H=12, W=128): 24576 (target, head) rows, where the default launch takes the 96-row
