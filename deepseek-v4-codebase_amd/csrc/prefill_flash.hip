@@ -47,7 +47,8 @@
 // leaves two, which measurably exceeds the attention tolerance).  The rescale of O and l is a
 // wave-uniform branch taken on tiles that raise some row's maximum.  The normaliser is the sum of
 // the very bf16 weights the numerator used: each lane adds its own weights of the row with
-// v_dot2_f32_bf16 (f16) against ones, and the two lane halves are added at the end.  Tiles that every row of the workgroup sees in full skip the masks.
+// v_dot2_f32_bf16 (f16) against ones, and the two lane halves are added at the end.  Tiles that
+// every row of the workgroup sees in full skip the masks.
 #include <atomic>
 
 #include "tq_device.h"
@@ -80,6 +81,7 @@ template <int ROWB, int RG, int KS>
 struct FlashGeom {
   static_assert(ROWB == 256 || ROWB == 512, "rows of K (= V) or of K then V");
   static_assert(KS == 2 || KS == 4, "the key splits merge pairwise");
+  static_assert(RG * KS == 4 || RG * KS == 12, "4 waves (two workgroups per CU) or 12 (one)");
   static constexpr int kRowBytes = ROWB;
   static constexpr int kWaves = RG * KS, kThreads = 64 * kWaves, kRows = 32 * RG;
   static constexpr int kWavesPerSimd = kWaves == 4 ? 2 : 3;  // resident waves per SIMD (register budget)
