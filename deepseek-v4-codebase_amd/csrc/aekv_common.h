@@ -157,9 +157,10 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // fp32 score -> uint32 whose unsigned order equals the float order (-inf smallest).
+// (negative: every bit flipped; otherwise the sign bit set: u ^ (sign mask | 0x80000000))
 __device__ __forceinline__ uint32_t order_key(float s) {
-  uint32_t u = __builtin_bit_cast(uint32_t, s);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  const uint32_t u = __builtin_bit_cast(uint32_t, s);
+  return u ^ (static_cast<uint32_t>(static_cast<int32_t>(u) >> 31) | 0x80000000u);
 }
 __device__ __forceinline__ float order_key_inv(uint32_t k) {
   uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;

@@ -10,9 +10,11 @@
 // and v_mfma_i32_16x16x64_i8 computes the exact integer dots I_i = d_i . codes_j for 16 keys at a
 // time (A rows = 4 heads x 4 digits; B columns = keys; 4-bit codes enter as 16*code, the nibble
 // shifted to the top of its byte).  The 16x16 result leaves each lane with the four digit dots of
-// one (head, key); they are combined in fp32 with the head weight folded in, clamped (relu), summed
-// over heads across lane groups and multiplied by scale_j.  The only approximation is r (relative
-// ~2^-27 of max|q~_h|) and three fp32 roundings, i.e. fp32-level scores.
+// one (head, key); the digit pairs are joined exactly in int32 (|I_i| <= 64 * 128 * 128 = 2^20, so
+// 2^7 I_0 + I_1 and 2^7 I_2 + I_3 stay below 2^28), converted and combined in fp32 with the head
+// weight folded in, clamped (relu), summed over heads across lane groups and multiplied by
+// scale_j.  The only approximation is r (relative ~2^-27 of max|q~_h|) and at most four fp32
+// roundings, i.e. fp32-level scores.
 //
 // Kernels (one stream, in order):
 //   score  (wide grid)  rotates the row's query and splits the digits in LDS (per workgroup),
@@ -45,7 +47,7 @@ constexpr int kHistBins = 4096;      // slot-max histogram bins (key >> 16 below
 constexpr int kCandCap = 4096;       // candidates a row's workgroup collects in LDS (fast route)
 constexpr int kMaxMfmaK = 1024;
 constexpr int kMaxNrb = 4;           // row blocks of 4 heads (IH <= 16)
-constexpr int64_t kMaxKeys = int64_t(1) << 30;
+constexpr int64_t kMaxKeys = int64_t(1) << 24;  // byte offsets within a key row fit in 32 bits (2^24 x 128)
 constexpr int kScoreTT = 4;          // prefill rows sharing each key group in the score kernel
 constexpr int64_t kScoreTargetWG = 2048;  // score workgroups the launch aims for
 
@@ -438,39 +440,45 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
     query_fragments<BITS, IC, NRB>(a, static_cast<int>(row[tt]), dig, hf, hb, A[tt], f[tt], lo[tt], hi[tt]);
   }
 
+  // key-row bases (wave-uniform) and 32-bit offsets within the rows (S <= kMaxKeys)
   const uint8_t* crow = a.codes + kr * S * RB;
-  const float* srow = a.kscale + kr * S;
+  const uint8_t* srow = reinterpret_cast<const uint8_t*>(a.kscale + kr * S);
   constexpr int64_t kGroupKeys = SPW * 64;
   const int64_t wave_base = (bx * 4 + wv) * a.gpw * kGroupKeys;
+  int nvi[TT];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) nvi[tt] = static_cast<int>(nv[tt]);
+  const int nv_maxi = static_cast<int>(nv_max);
 #pragma unroll 1
   for (int gi = 0; gi < a.gpw; ++gi) {
-    const int64_t kb = wave_base + gi * kGroupKeys;
-    if (kb >= nv_max) break;  // wave-uniform
+    const int64_t kb64 = wave_base + gi * kGroupKeys;
+    if (kb64 >= nv_max) break;  // wave-uniform
+    const int kb = static_cast<int>(kb64);
     uint32_t raw[SPW][4][KS][LW];
     float scl[SPW];
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
 #pragma unroll
       for (int tq = 0; tq < 4; ++tq) {
-        const int64_t j = kb + 64 * s + 16 * tq + (lane & 15);
-        const int64_t jr = j < nv_max ? j : 0;  // nv_max >= 1 here; keys past a row's count are dropped
+        const int j = kb + 64 * s + 16 * tq + (lane & 15);
+        const uint32_t jr = j < nv_maxi ? static_cast<uint32_t>(j) : 0u;  // nv_max >= 1 here; keys past a row's count are dropped
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           if constexpr (BITS == 8) {
-            const uint4 v = *reinterpret_cast<const uint4*>(crow + jr * RB + 64 * ks + 16 * g);
+            const uint4 v = *reinterpret_cast<const uint4*>(crow + (jr * RB + 64 * ks + 16 * g));
             raw[s][tq][ks][0] = v.x;
             raw[s][tq][ks][1] = v.y;
             raw[s][tq][ks][2] = v.z;
             raw[s][tq][ks][3] = v.w;
           } else {
-            const uint2 v = *reinterpret_cast<const uint2*>(crow + jr * RB + 32 * ks + 8 * g);
+            const uint2 v = *reinterpret_cast<const uint2*>(crow + (jr * RB + 32 * ks + 8 * g));
             raw[s][tq][ks][0] = v.x;
             raw[s][tq][ks][1] = v.y;
           }
         }
       }
-      const int64_t jo = kb + 64 * s + lane;
-      scl[s] = srow[jo < nv_max ? jo : 0];
+      const int jo = kb + 64 * s + lane;
+      scl[s] = *reinterpret_cast<const float*>(srow + (jo < nv_maxi ? static_cast<uint32_t>(jo) * 4u : 0u));
     }
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
@@ -488,10 +496,10 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
                                   static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
           }
         }
-      const int64_t jo = kb + 64 * s + lane;
+      const int jo = kb + 64 * s + lane;
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
-        if (TT > 1 && kb + 64 * s >= nv[tt]) continue;  // wave-uniform: this row has no key in the slot group
+        if (TT > 1 && kb + 64 * s >= nvi[tt]) continue;  // wave-uniform: this row has no key in the slot group
         float tq_t[4];
 #pragma unroll
         for (int tq = 0; tq < 4; ++tq) {
@@ -506,28 +514,29 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
           float t = 0.0f;
 #pragma unroll
           for (int rb = 0; rb < NRB; ++rb) {
-            float v = static_cast<float>(acc[rb][0]) * f[tt][rb][0];
-            v = fmaf(static_cast<float>(acc[rb][1]), f[tt][rb][1], v);
-            v = fmaf(static_cast<float>(acc[rb][2]), f[tt][rb][2], v);
-            v = fmaf(static_cast<float>(acc[rb][3]), f[tt][rb][3], v);
-            t += __builtin_amdgcn_fmed3f(v, lo[tt][rb], hi[tt][rb]);
+            // f[d] = F 2^-7d: F (2^7 I_0 + I_1) 2^-7 + F (2^7 I_2 + I_3) 2^-21, the pairs exact in int32
+            const int p01 = acc[rb][0] * 128 + acc[rb][1], p23 = acc[rb][2] * 128 + acc[rb][3];
+            const float v = fmaf(static_cast<float>(p23), f[tt][rb][3], static_cast<float>(p01) * f[tt][rb][1]);
+            const float m = __builtin_amdgcn_fmed3f(v, lo[tt][rb], hi[tt][rb]);
+            t = rb == 0 ? m : t + m;
           }
           tq_t[tq] = t;
         }
-        // sum over the four head groups; lane l keeps key kb + 64s + l, i.e. tq = l / 16
-        const float mine = row_sums_scatter(tq_t);
-        const bool ok = jo < nv[tt];
+        // sum over the four head groups; lane l keeps key kb + 64s + l, i.e. tq = l / 16.  The + 0
+        // turns a -0 sum into +0 (a zero score has one order key)
+        const float mine = row_sums_scatter(tq_t) + 0.0f;
+        const bool ok = jo < nvi[tt];
         const uint32_t key = ok ? order_key(mine * scl[s]) : 0u;
-        uint32_t* krow = a.keys + row[tt] * a.ks;
-        uint32_t* mrow = a.smax + row[tt] * a.ms;
-        if (ok) krow[jo] = key;
+        uint8_t* krow = reinterpret_cast<uint8_t*>(a.keys + row[tt] * a.ks);
+        uint8_t* mrow = reinterpret_cast<uint8_t*>(a.smax + row[tt] * a.ms);
+        if (ok) *reinterpret_cast<uint32_t*>(krow + static_cast<uint32_t>(jo) * 4u) = key;
         // max of the 16-key slot of lanes 16u .. 16u+15, stored by its first lane
         uint32_t mx = key;
         mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<1>(__builtin_bit_cast(float, mx))));
         mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<2>(__builtin_bit_cast(float, mx))));
         mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<4>(__builtin_bit_cast(float, mx))));
         mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<8>(__builtin_bit_cast(float, mx))));
-        if ((lane & 15) == 0 && ok) mrow[jo >> 4] = mx;
+        if ((lane & 15) == 0 && ok) *reinterpret_cast<uint32_t*>(mrow + static_cast<uint32_t>(jo >> 4) * 4u) = mx;
       }
     }
   }
