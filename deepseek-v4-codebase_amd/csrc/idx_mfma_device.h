@@ -34,6 +34,8 @@
 // which continues with the row's attention in the same workgroup.
 #pragma once
 
+#include <type_traits>
+
 #include <algorithm>
 
 #include "aekv_common.h"
@@ -449,11 +451,13 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
 #pragma unroll
   for (int tt = 0; tt < TT; ++tt) nvi[tt] = static_cast<int>(nv[tt]);
   const int nv_maxi = static_cast<int>(nv_max);
-#pragma unroll 1
-  for (int gi = 0; gi < a.gpw; ++gi) {
-    const int64_t kb64 = wave_base + gi * kGroupKeys;
-    if (kb64 >= nv_max) break;  // wave-uniform
-    const int kb = static_cast<int>(kb64);
+  int nv_mini = nv_maxi;
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) nv_mini = min(nv_mini, nvi[tt]);
+  // one group of SPW slots from key kb; FULL: every key of the group is visible to every row (no
+  // bounds checks)
+  auto group = [&](const int kb, auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
     uint32_t raw[SPW][4][KS][LW];
     float scl[SPW];
 #pragma unroll
@@ -461,7 +465,8 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
 #pragma unroll
       for (int tq = 0; tq < 4; ++tq) {
         const int j = kb + 64 * s + 16 * tq + (lane & 15);
-        const uint32_t jr = j < nv_maxi ? static_cast<uint32_t>(j) : 0u;  // nv_max >= 1 here; keys past a row's count are dropped
+        // keys past a row's count read key 0 (nv_max >= 1 here) and are dropped
+        const uint32_t jr = FULL || j < nv_maxi ? static_cast<uint32_t>(j) : 0u;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           if constexpr (BITS == 8) {
@@ -478,7 +483,7 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
         }
       }
       const int jo = kb + 64 * s + lane;
-      scl[s] = *reinterpret_cast<const float*>(srow + (jo < nv_maxi ? static_cast<uint32_t>(jo) * 4u : 0u));
+      scl[s] = *reinterpret_cast<const float*>(srow + (FULL || jo < nv_maxi ? static_cast<uint32_t>(jo) * 4u : 0u));
     }
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
@@ -499,7 +504,7 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
       const int jo = kb + 64 * s + lane;
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
-        if (TT > 1 && kb + 64 * s >= nvi[tt]) continue;  // wave-uniform: this row has no key in the slot group
+        if (!FULL && TT > 1 && kb + 64 * s >= nvi[tt]) continue;  // wave-uniform: this row has no key in the slot group
         float tq_t[4];
 #pragma unroll
         for (int tq = 0; tq < 4; ++tq) {
@@ -525,7 +530,7 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
         // sum over the four head groups; lane l keeps key kb + 64s + l, i.e. tq = l / 16.  The + 0
         // turns a -0 sum into +0 (a zero score has one order key)
         const float mine = row_sums_scatter(tq_t) + 0.0f;
-        const bool ok = jo < nvi[tt];
+        const bool ok = FULL || jo < nvi[tt];
         const uint32_t key = ok ? order_key(mine * scl[s]) : 0u;
         uint8_t* krow = reinterpret_cast<uint8_t*>(a.keys + row[tt] * a.ks);
         uint8_t* mrow = reinterpret_cast<uint8_t*>(a.smax + row[tt] * a.ms);
@@ -539,6 +544,13 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
         if ((lane & 15) == 0 && ok) *reinterpret_cast<uint32_t*>(mrow + static_cast<uint32_t>(jo >> 4) * 4u) = mx;
       }
     }
+  };
+#pragma unroll 1
+  for (int gi = 0; gi < a.gpw; ++gi) {
+    const int64_t kb64 = wave_base + gi * kGroupKeys;
+    if (kb64 >= nv_max) break;  // wave-uniform
+    if (kb64 + kGroupKeys <= nv_mini) group(static_cast<int>(kb64), std::true_type{});
+    else group(static_cast<int>(kb64), std::false_type{});
   }
 }
 
