@@ -94,6 +94,8 @@ struct MfmaIdxArgs {
   int64_t ks;            // key row stride: S rounded up to a multiple of 16 (whole slots)
   uint32_t* smax;        // [B][ms]                   max order key of each 16-key slot
   int64_t ms;            // slot-max row stride: ceil(S / 16) rounded up to a multiple of 4
+  int skip_keys;         // 1: the score kernel stores only the slot maxima; the select recomputes
+                         //    the keys of the slots it reads (and all of them if its candidates overflow)
 };
 
 struct WsLayout {
@@ -374,6 +376,75 @@ __device__ __forceinline__ void query_fragments(const MfmaIdxArgs& a, int b, int
   }
 }
 
+// ---- per-key scoring shared by the score kernel and the select's recomputation ---------------
+// Raw code words of key j for lane group g (the B operand's k-step dims of the lane).
+template <int BITS, int KS, int LW>
+__device__ __forceinline__ void load_key_codes(const uint8_t* crow, uint32_t j, int g, uint32_t (&raw)[KS][LW]) {
+  constexpr uint32_t RB = BITS == 8 ? 64 * KS : 32 * KS;  // code bytes per key
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if constexpr (BITS == 8) {
+      const uint4 v = *reinterpret_cast<const uint4*>(crow + (j * RB + 64 * ks + 16 * g));
+      raw[ks][0] = v.x;
+      raw[ks][1] = v.y;
+      raw[ks][2] = v.z;
+      raw[ks][3] = v.w;
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2*>(crow + (j * RB + 32 * ks + 8 * g));
+      raw[ks][0] = v.x;
+      raw[ks][1] = v.y;
+    }
+  }
+}
+
+// The B operand (int8 codes; 4-bit codes as 16 * code) of one 16-key block from its raw words.
+template <int BITS, int KS, int LW>
+__device__ __forceinline__ void build_bop(const uint32_t (&raw)[KS][LW], i32x4_t (&Bop)[KS]) {
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if constexpr (BITS == 8) {
+      Bop[ks] = i32x4_t{static_cast<int>(raw[ks][0]), static_cast<int>(raw[ks][1]), static_cast<int>(raw[ks][2]),
+                        static_cast<int>(raw[ks][3])};
+    } else {
+      const uint32_t x = raw[ks][0], y = raw[ks][1];
+      Bop[ks] = i32x4_t{static_cast<int>((x << 4) & 0xF0F0F0F0u), static_cast<int>(x & 0xF0F0F0F0u),
+                        static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
+    }
+  }
+}
+
+// Score (before the key's scale) of lane l's key, key l % 16 of block l / 16 of the four blocks
+// Bop[tq], for one row (A, f, lo, hi): the 4-head x 4-digit products, the digit pairs joined
+// exactly in int32, the weights, the clamp, and the sum over heads (+ 0 turns -0 into +0, so that
+// a zero score has one order key).
+template <int NRB, int KS>
+__device__ __forceinline__ float lane_score(const i32x4_t (&A)[NRB][KS], const i32x4_t (&Bop)[4][KS],
+                                            const float (&f)[NRB][4], const float (&lo)[NRB], const float (&hi)[NRB]) {
+  float tq_t[4];
+#pragma unroll
+  for (int tq = 0; tq < 4; ++tq) {
+    i32x4_t acc[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) acc[rb] = i32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb) acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[rb][ks], Bop[tq][ks], acc[rb], 0, 0, 0);
+    float t = 0.0f;
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      // f[d] = F 2^-7d: F (2^7 I_0 + I_1) 2^-7 + F (2^7 I_2 + I_3) 2^-21, the pairs exact in int32
+      const int p01 = acc[rb][0] * 128 + acc[rb][1], p23 = acc[rb][2] * 128 + acc[rb][3];
+      const float v = fmaf(static_cast<float>(p23), f[rb][3], static_cast<float>(p01) * f[rb][1]);
+      const float m = __builtin_amdgcn_fmed3f(v, lo[rb], hi[rb]);
+      t = rb == 0 ? m : t + m;
+    }
+    tq_t[tq] = t;
+  }
+  // sum over the four head groups; lane l keeps the key of block l / 16
+  return row_sums_scatter(tq_t) + 0.0f;
+}
+
 // ---- score: keys -> order keys + the max of every 16-key slot ----------------------------------
 // A wave scores groups of SPW slots of 64 keys; lane l keeps key base + 64s + l of slot s.  All
 // loads of a group are issued before its matrix work.  With TT > 1 a workgroup scores TT rows
@@ -467,20 +538,7 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
         const int j = kb + 64 * s + 16 * tq + (lane & 15);
         // keys past a row's count read key 0 (nv_max >= 1 here) and are dropped
         const uint32_t jr = FULL || j < nv_maxi ? static_cast<uint32_t>(j) : 0u;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          if constexpr (BITS == 8) {
-            const uint4 v = *reinterpret_cast<const uint4*>(crow + (jr * RB + 64 * ks + 16 * g));
-            raw[s][tq][ks][0] = v.x;
-            raw[s][tq][ks][1] = v.y;
-            raw[s][tq][ks][2] = v.z;
-            raw[s][tq][ks][3] = v.w;
-          } else {
-            const uint2 v = *reinterpret_cast<const uint2*>(crow + (jr * RB + 32 * ks + 8 * g));
-            raw[s][tq][ks][0] = v.x;
-            raw[s][tq][ks][1] = v.y;
-          }
-        }
+        load_key_codes<BITS, KS, LW>(crow, jr, g, raw[s][tq]);
       }
       const int jo = kb + 64 * s + lane;
       scl[s] = *reinterpret_cast<const float*>(srow + (FULL || jo < nv_maxi ? static_cast<uint32_t>(jo) * 4u : 0u));
@@ -489,52 +547,17 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
     for (int s = 0; s < SPW; ++s) {
       i32x4_t Bop[4][KS];
 #pragma unroll
-      for (int tq = 0; tq < 4; ++tq)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          if constexpr (BITS == 8) {
-            Bop[tq][ks] = i32x4_t{static_cast<int>(raw[s][tq][ks][0]), static_cast<int>(raw[s][tq][ks][1]),
-                                  static_cast<int>(raw[s][tq][ks][2]), static_cast<int>(raw[s][tq][ks][3])};
-          } else {
-            const uint32_t x = raw[s][tq][ks][0], y = raw[s][tq][ks][1];
-            Bop[tq][ks] = i32x4_t{static_cast<int>((x << 4) & 0xF0F0F0F0u), static_cast<int>(x & 0xF0F0F0F0u),
-                                  static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
-          }
-        }
+      for (int tq = 0; tq < 4; ++tq) build_bop<BITS, KS, LW>(raw[s][tq], Bop[tq]);
       const int jo = kb + 64 * s + lane;
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
         if (!FULL && TT > 1 && kb + 64 * s >= nvi[tt]) continue;  // wave-uniform: this row has no key in the slot group
-        float tq_t[4];
-#pragma unroll
-        for (int tq = 0; tq < 4; ++tq) {
-          i32x4_t acc[NRB];
-#pragma unroll
-          for (int rb = 0; rb < NRB; ++rb) acc[rb] = i32x4_t{0, 0, 0, 0};
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int rb = 0; rb < NRB; ++rb)
-              acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tt][rb][ks], Bop[tq][ks], acc[rb], 0, 0, 0);
-          float t = 0.0f;
-#pragma unroll
-          for (int rb = 0; rb < NRB; ++rb) {
-            // f[d] = F 2^-7d: F (2^7 I_0 + I_1) 2^-7 + F (2^7 I_2 + I_3) 2^-21, the pairs exact in int32
-            const int p01 = acc[rb][0] * 128 + acc[rb][1], p23 = acc[rb][2] * 128 + acc[rb][3];
-            const float v = fmaf(static_cast<float>(p23), f[tt][rb][3], static_cast<float>(p01) * f[tt][rb][1]);
-            const float m = __builtin_amdgcn_fmed3f(v, lo[tt][rb], hi[tt][rb]);
-            t = rb == 0 ? m : t + m;
-          }
-          tq_t[tq] = t;
-        }
-        // sum over the four head groups; lane l keeps key kb + 64s + l, i.e. tq = l / 16.  The + 0
-        // turns a -0 sum into +0 (a zero score has one order key)
-        const float mine = row_sums_scatter(tq_t) + 0.0f;
+        const float mine = lane_score<NRB, KS>(A[tt], Bop, f[tt], lo[tt], hi[tt]);
         const bool ok = FULL || jo < nvi[tt];
         const uint32_t key = ok ? order_key(mine * scl[s]) : 0u;
         uint8_t* krow = reinterpret_cast<uint8_t*>(a.keys + row[tt] * a.ks);
         uint8_t* mrow = reinterpret_cast<uint8_t*>(a.smax + row[tt] * a.ms);
-        if (ok) *reinterpret_cast<uint32_t*>(krow + static_cast<uint32_t>(jo) * 4u) = key;
+        if (ok && !a.skip_keys) *reinterpret_cast<uint32_t*>(krow + static_cast<uint32_t>(jo) * 4u) = key;
         // max of the 16-key slot of lanes 16u .. 16u+15, stored by its first lane
         uint32_t mx = key;
         mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<1>(__builtin_bit_cast(float, mx))));
@@ -577,10 +600,16 @@ __device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
 // 1024-thread instance at 73 VGPRs fits one) for launches of many rows with k <= 512.
 // sel_lds (nullable): the row's output indices also go there as int32 (-1 padding), for a caller
 // that continues with them in the same workgroup.
-template <int NT, int CAP>
+// RBITS != 0 (with RIC, RNRB: the index codes' bits, dims and row blocks): the score kernel stored
+// no keys (skip_keys), so the keys of the listed slots are recomputed here from the codes with the
+// score kernel's own operations (bit for bit the same order keys); if the candidates overflow LDS,
+// every key of the row is recomputed into the key buffer first and the radix route reads it.
+template <int NT, int CAP, int RBITS = 0, int RIC = 64, int RNRB = 1>
 __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, int64_t* __restrict__ out_idx,
                                            float* __restrict__ out_score, int32_t* __restrict__ sel_lds) {
   constexpr int NW = NT / 64;
+  constexpr bool kRecompute = RBITS != 0;
+  constexpr int RKS = RIC / 64, RLW = RBITS == 8 ? 4 : 2;
   __shared__ uint64_t cbuf[CAP];  // candidates: keys ck[] then indices ci[], or sort words
   __shared__ __align__(16) uint32_t h[kHistBins];
   __shared__ uint64_t sel[kMaxMfmaK];
@@ -614,6 +643,33 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
     s_cnt[0] = 0u;
     s_cnt[1] = 0u;
   }
+  // the row's query fragments for the recomputation (the score kernel's query_fragments)
+  i32x4_t rA[RNRB][RKS];
+  float rf[RNRB][4], rlo[RNRB], rhi[RNRB];
+  const uint8_t* rcrow = a.codes + (static_cast<int64_t>(b) / a.T) * a.S * (RBITS == 8 ? RIC : RIC / 2);
+  const float* rsrow = a.kscale + (static_cast<int64_t>(b) / a.T) * a.S;
+  // order keys of the keys of slots sl[0..3] (-1: none), one per lane: lane l gets key l % 16 of
+  // slot sl[l / 16] (index *j, valid when the slot exists and the key is visible)
+  auto slot_keys = [&](const int (&sl)[4], uint32_t& key, uint32_t& j, bool& ok) {
+    uint32_t raw[4][RKS][RLW];
+    const int g = lane >> 4;
+#pragma unroll
+    for (int tq = 0; tq < 4; ++tq) {
+      const int64_t jt = sl[tq] >= 0 ? 16 * static_cast<int64_t>(sl[tq]) + (lane & 15) : 0;
+      load_key_codes<RBITS, RKS, RLW>(rcrow, static_cast<uint32_t>(jt < nv ? jt : 0), g, raw[tq]);
+    }
+    const int mine_slot = g == 0 ? sl[0] : g == 1 ? sl[1] : g == 2 ? sl[2] : sl[3];
+    const int64_t jm = mine_slot >= 0 ? 16 * static_cast<int64_t>(mine_slot) + (lane & 15) : 0;
+    ok = mine_slot >= 0 && jm < nv;
+    j = static_cast<uint32_t>(jm);
+    const float scl = rsrow[ok ? jm : 0];
+    i32x4_t Bop[4][RKS];
+#pragma unroll
+    for (int tq = 0; tq < 4; ++tq) build_bop<RBITS, RKS, RLW>(raw[tq], Bop[tq]);
+    const float sc = lane_score<RNRB, RKS>(rA, Bop, rf, rlo, rhi);
+    key = ok ? order_key(sc * scl) : 0u;
+  };
+
   uint32_t mx[kSlotPer];
   auto load_max = [&](int64_t c0) {
 #pragma unroll
@@ -622,12 +678,25 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
       mx[r] = sl < n_slots ? mrow[sl] : 0u;
     }
   };
-  // the row's largest slot max anchors the histogram
+  // the row's largest slot max anchors the histogram (with the recomputation, the query
+  // fragments are built while the first slot maxima are loading)
   uint32_t mloc = 0u;
-  for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
-    load_max(c0);
+  if constexpr (kRecompute) {
+    __shared__ int8_t rdig[4][16][RIC];
+    __shared__ float rhf[16][4], rhb[16][2];
+    load_max(0);
+    query_fragments<RBITS, RIC, RNRB>(a, b, rdig, rhf, rhb, rA, rf, rlo, rhi);
+    for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
+      if (c0 > 0) load_max(c0);
 #pragma unroll
-    for (int r = 0; r < kSlotPer; ++r) mloc = mloc > mx[r] ? mloc : mx[r];  // mx is 0 past the end
+      for (int r = 0; r < kSlotPer; ++r) mloc = mloc > mx[r] ? mloc : mx[r];  // mx is 0 past the end
+    }
+  } else {
+    for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
+      load_max(c0);
+#pragma unroll
+      for (int r = 0; r < kSlotPer; ++r) mloc = mloc > mx[r] ? mloc : mx[r];  // mx is 0 past the end
+    }
   }
   mloc = wave_max_u32(mloc);
   if (lane == 0) s_tot[wv] = mloc;
@@ -690,7 +759,24 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
     }
     __syncthreads();
     const int n_list = static_cast<int>(s_cnt[1]);
-    for (int li = tid; li < n_list; li += NT) {
+    if constexpr (kRecompute) {
+      // four listed slots per wave step (the matrix products need the whole wave)
+      for (int p0 = 4 * wv; p0 < n_list; p0 += 4 * NW) {
+        int sl[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sl[q] = p0 + q < n_list ? static_cast<int>(c0 + h[p0 + q]) : -1;
+        uint32_t key, j;
+        bool ok;
+        slot_keys(sl, key, j, ok);
+        const bool take = ok && key >= tau;
+        const uint32_t p = wave_reserve<1>(&s_cnt[0], take ? 1u : 0u);
+        if (take && p < static_cast<uint32_t>(CAP)) {
+          ck[p] = key;
+          ci[p] = j;
+        }
+      }
+    }
+    for (int li = kRecompute ? n_list : tid; li < n_list; li += NT) {
       const int64_t sl = c0 + h[li];
       uint32_t kw[16];
 #pragma unroll
@@ -720,6 +806,23 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
   __syncthreads();
   const uint32_t n_cand = s_cnt[0];
   const bool fast = n_cand <= static_cast<uint32_t>(CAP);
+  if constexpr (kRecompute) {
+    if (!fast) {
+      // the candidates overflow LDS: every key of the row goes to the key buffer for the radix
+      // route (global writes of this workgroup, read by it after the barrier)
+      uint32_t* kw = a.keys + static_cast<int64_t>(b) * a.ks;
+      for (int64_t p0 = 4 * wv; p0 < n_slots; p0 += 4 * NW) {
+        int sl[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sl[q] = p0 + q < n_slots ? static_cast<int>(p0 + q) : -1;
+        uint32_t key, j;
+        bool ok;
+        slot_keys(sl, key, j, ok);
+        if (ok) kw[j] = key;
+      }
+      __syncthreads();
+    }
+  }
   const int n = fast ? static_cast<int>(n_cand) : 0;
 
   // ---- 2a. up to NT candidates (the usual case): sort them all, emit the first kk ----
@@ -887,9 +990,11 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
   }
 }
 
+// The 512-thread instance serves launches of many rows: bounded to 80 VGPRs (six waves per SIMD),
+// so that three rows share a CU.
 template <int NT, int CAP>
-__global__ __launch_bounds__(NT) void idx_mfma_final_kernel(MfmaIdxArgs a, int64_t* __restrict__ out_idx,
-                                                            float* __restrict__ out_score) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 512 ? 6 : 1))) void idx_mfma_final_kernel(
+    MfmaIdxArgs a, int64_t* __restrict__ out_idx, float* __restrict__ out_score) {
   select_row<NT, CAP>(a, blockIdx.x, out_idx, out_score, nullptr);
 }
 
