@@ -94,8 +94,6 @@ struct MfmaIdxArgs {
   int64_t ks;            // key row stride: S rounded up to a multiple of 16 (whole slots)
   uint32_t* smax;        // [B][ms]                   max order key of each 16-key slot
   int64_t ms;            // slot-max row stride: ceil(S / 16) rounded up to a multiple of 4
-  int skip_keys;         // 1: the score kernel stores only the slot maxima; the select recomputes
-                         //    the keys of the slots it reads (and all of them if its candidates overflow)
 };
 
 struct WsLayout {
@@ -557,7 +555,7 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
         const uint32_t key = ok ? order_key(mine * scl[s]) : 0u;
         uint8_t* krow = reinterpret_cast<uint8_t*>(a.keys + row[tt] * a.ks);
         uint8_t* mrow = reinterpret_cast<uint8_t*>(a.smax + row[tt] * a.ms);
-        if (ok && !a.skip_keys) *reinterpret_cast<uint32_t*>(krow + static_cast<uint32_t>(jo) * 4u) = key;
+        if (ok) *reinterpret_cast<uint32_t*>(krow + static_cast<uint32_t>(jo) * 4u) = key;
         // max of the 16-key slot of lanes 16u .. 16u+15, stored by its first lane
         uint32_t mx = key;
         mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<1>(__builtin_bit_cast(float, mx))));
@@ -600,16 +598,10 @@ __device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
 // 1024-thread instance at 73 VGPRs fits one) for launches of many rows with k <= 512.
 // sel_lds (nullable): the row's output indices also go there as int32 (-1 padding), for a caller
 // that continues with them in the same workgroup.
-// RBITS != 0 (with RIC, RNRB: the index codes' bits, dims and row blocks): the score kernel stored
-// no keys (skip_keys), so the keys of the listed slots are recomputed here from the codes with the
-// score kernel's own operations (bit for bit the same order keys); if the candidates overflow LDS,
-// every key of the row is recomputed into the key buffer first and the radix route reads it.
-template <int NT, int CAP, int RBITS = 0, int RIC = 64, int RNRB = 1>
+template <int NT, int CAP>
 __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, int64_t* __restrict__ out_idx,
                                            float* __restrict__ out_score, int32_t* __restrict__ sel_lds) {
   constexpr int NW = NT / 64;
-  constexpr bool kRecompute = RBITS != 0;
-  constexpr int RKS = RIC / 64, RLW = RBITS == 8 ? 4 : 2;
   __shared__ uint64_t cbuf[CAP];  // candidates: keys ck[] then indices ci[], or sort words
   __shared__ __align__(16) uint32_t h[kHistBins];
   __shared__ uint64_t sel[kMaxMfmaK];
@@ -643,33 +635,6 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
     s_cnt[0] = 0u;
     s_cnt[1] = 0u;
   }
-  // the row's query fragments for the recomputation (the score kernel's query_fragments)
-  i32x4_t rA[RNRB][RKS];
-  float rf[RNRB][4], rlo[RNRB], rhi[RNRB];
-  const uint8_t* rcrow = a.codes + (static_cast<int64_t>(b) / a.T) * a.S * (RBITS == 8 ? RIC : RIC / 2);
-  const float* rsrow = a.kscale + (static_cast<int64_t>(b) / a.T) * a.S;
-  // order keys of the keys of slots sl[0..3] (-1: none), one per lane: lane l gets key l % 16 of
-  // slot sl[l / 16] (index *j, valid when the slot exists and the key is visible)
-  auto slot_keys = [&](const int (&sl)[4], uint32_t& key, uint32_t& j, bool& ok) {
-    uint32_t raw[4][RKS][RLW];
-    const int g = lane >> 4;
-#pragma unroll
-    for (int tq = 0; tq < 4; ++tq) {
-      const int64_t jt = sl[tq] >= 0 ? 16 * static_cast<int64_t>(sl[tq]) + (lane & 15) : 0;
-      load_key_codes<RBITS, RKS, RLW>(rcrow, static_cast<uint32_t>(jt < nv ? jt : 0), g, raw[tq]);
-    }
-    const int mine_slot = g == 0 ? sl[0] : g == 1 ? sl[1] : g == 2 ? sl[2] : sl[3];
-    const int64_t jm = mine_slot >= 0 ? 16 * static_cast<int64_t>(mine_slot) + (lane & 15) : 0;
-    ok = mine_slot >= 0 && jm < nv;
-    j = static_cast<uint32_t>(jm);
-    const float scl = rsrow[ok ? jm : 0];
-    i32x4_t Bop[4][RKS];
-#pragma unroll
-    for (int tq = 0; tq < 4; ++tq) build_bop<RBITS, RKS, RLW>(raw[tq], Bop[tq]);
-    const float sc = lane_score<RNRB, RKS>(rA, Bop, rf, rlo, rhi);
-    key = ok ? order_key(sc * scl) : 0u;
-  };
-
   uint32_t mx[kSlotPer];
   auto load_max = [&](int64_t c0) {
 #pragma unroll
@@ -681,22 +646,10 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
   // the row's largest slot max anchors the histogram (with the recomputation, the query
   // fragments are built while the first slot maxima are loading)
   uint32_t mloc = 0u;
-  if constexpr (kRecompute) {
-    __shared__ int8_t rdig[4][16][RIC];
-    __shared__ float rhf[16][4], rhb[16][2];
-    load_max(0);
-    query_fragments<RBITS, RIC, RNRB>(a, b, rdig, rhf, rhb, rA, rf, rlo, rhi);
-    for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
-      if (c0 > 0) load_max(c0);
+  for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
+    load_max(c0);
 #pragma unroll
-      for (int r = 0; r < kSlotPer; ++r) mloc = mloc > mx[r] ? mloc : mx[r];  // mx is 0 past the end
-    }
-  } else {
-    for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
-      load_max(c0);
-#pragma unroll
-      for (int r = 0; r < kSlotPer; ++r) mloc = mloc > mx[r] ? mloc : mx[r];  // mx is 0 past the end
-    }
+    for (int r = 0; r < kSlotPer; ++r) mloc = mloc > mx[r] ? mloc : mx[r];  // mx is 0 past the end
   }
   mloc = wave_max_u32(mloc);
   if (lane == 0) s_tot[wv] = mloc;
@@ -759,24 +712,7 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
     }
     __syncthreads();
     const int n_list = static_cast<int>(s_cnt[1]);
-    if constexpr (kRecompute) {
-      // four listed slots per wave step (the matrix products need the whole wave)
-      for (int p0 = 4 * wv; p0 < n_list; p0 += 4 * NW) {
-        int sl[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sl[q] = p0 + q < n_list ? static_cast<int>(c0 + h[p0 + q]) : -1;
-        uint32_t key, j;
-        bool ok;
-        slot_keys(sl, key, j, ok);
-        const bool take = ok && key >= tau;
-        const uint32_t p = wave_reserve<1>(&s_cnt[0], take ? 1u : 0u);
-        if (take && p < static_cast<uint32_t>(CAP)) {
-          ck[p] = key;
-          ci[p] = j;
-        }
-      }
-    }
-    for (int li = kRecompute ? n_list : tid; li < n_list; li += NT) {
+    for (int li = tid; li < n_list; li += NT) {
       const int64_t sl = c0 + h[li];
       uint32_t kw[16];
 #pragma unroll
@@ -806,23 +742,6 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
   __syncthreads();
   const uint32_t n_cand = s_cnt[0];
   const bool fast = n_cand <= static_cast<uint32_t>(CAP);
-  if constexpr (kRecompute) {
-    if (!fast) {
-      // the candidates overflow LDS: every key of the row goes to the key buffer for the radix
-      // route (global writes of this workgroup, read by it after the barrier)
-      uint32_t* kw = a.keys + static_cast<int64_t>(b) * a.ks;
-      for (int64_t p0 = 4 * wv; p0 < n_slots; p0 += 4 * NW) {
-        int sl[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sl[q] = p0 + q < n_slots ? static_cast<int>(p0 + q) : -1;
-        uint32_t key, j;
-        bool ok;
-        slot_keys(sl, key, j, ok);
-        if (ok) kw[j] = key;
-      }
-      __syncthreads();
-    }
-  }
   const int n = fast ? static_cast<int>(n_cand) : 0;
 
   // ---- 2a. up to NT candidates (the usual case): sort them all, emit the first kk ----

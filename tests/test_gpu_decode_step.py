@@ -71,6 +71,39 @@ def test_decode_step_equals_separate_entry_points(dev, B, S, H, IH, IC, W, k, kv
     np.testing.assert_allclose(to_np_f32(out).reshape(B, H, 128), want, rtol=1e-2, atol=2e-3)
 
 
+@pytest.mark.parametrize("ix_bits", [4, 8])
+@pytest.mark.parametrize("n_special", [300, 100])
+def test_decode_step_exact_ties(dev, ix_bits, n_special):
+    # Every index key is the same code row (equal scores); n_special keys get twice the scale.  With
+    # 100 specials the k-th key is one of ~20000 equal keys, so the fused select's candidates
+    # overflow its LDS list and it recomputes every key of the row before the radix route.
+    B, S, H, IH, IC, W, k = 2, 20000, 12, 4, 64, 32, 256
+    kvq, ixq = PolarQuant(4), PolarQuant(ix_bits)
+    kv_codes, kv_scale = kvq.encode(normal((B, S, 128), 31, device=dev))
+    row = normal((1, 1, IC), 5, dtype=torch.bfloat16)
+    ix_codes, ix_scale = ixq.encode(row.expand(B, S, IC).contiguous().to(dev))
+    iq = normal((B, IH, IC), 6, dtype=torch.float32)
+    keyf = ixq.decode(ix_codes[:1, :1], ix_scale[:1, :1], out_dtype=torch.float32).cpu()[0, 0]
+    iq = torch.where((iq @ keyf)[..., None] < 0, -iq, iq).to(dev)   # positive dots: nonzero scores
+    iw = torch.ones(B, IH, device=dev)
+    g = torch.Generator().manual_seed(9)
+    ix_scale = ix_scale.clone()
+    for b in range(B):
+        ix_scale[b, torch.randperm(S, generator=g)[:n_special].to(dev)] *= 2
+    q = normal((B, 1, H, 128), 7, device=dev)
+    win = normal((B, W, 128), 8, device=dev)
+    sink = normal((H,), 9, dtype=torch.float32, device=dev)
+    sm = 128 ** -0.5
+    print(f"decode step exact ties bits={ix_bits} specials={n_special}", flush=True)
+    out, idx, sc = csa_decode_step(q, iq, iw, ix_codes, ix_scale, kv_codes, kv_scale, win, sink, sm, k, kv_quant=kvq,
+                                   index_quant=ixq, return_scores=True)
+    idx1, sc1 = csa_indexer_topk_quant(iq, iw, ix_codes, ix_scale, k, quant=ixq, return_scores=True)
+    out1 = quant_sink_attention(q, kv_codes, kv_scale, idx1, win, sink, sm, quant=kvq)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, idx1) and torch.equal(sc, sc1)
+    assert torch.equal(out, out1)
+
+
 @pytest.mark.parametrize("k,W", [(600, 128), (512, 600)])
 def test_decode_step_outside_the_fused_limits(dev, k, W):
     # k > 512 or k + W > 1024: the entry point runs the indexer and the attention entry points in turn
