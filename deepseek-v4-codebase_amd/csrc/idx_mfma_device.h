@@ -255,6 +255,35 @@ __device__ void block_threshold(const uint32_t* h, uint32_t need, uint32_t* s_to
   __syncthreads();
 }
 
+// Redundant per-wave search of the top 64 * PER of NB bins: every wave that calls it reads the same
+// bins and gets the same bin t (no LDS writes, no barrier).  False when those bins hold fewer than
+// need (then t is untouched and the caller searches all bins).
+template <int NB, int PER>
+__device__ __forceinline__ bool wave_top_threshold(const uint32_t* h, uint32_t need, uint32_t& t_out) {
+  constexpr int kLow = NB - 64 * PER;
+  const int lane = threadIdx.x & 63;
+  uint32_t v[PER];
+  load_bins<PER>(h + kLow, lane, v);
+  uint32_t sum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) sum += v[i];
+  const uint32_t incl = wave_suffix_sum(sum), excl = incl - sum;
+  if (__builtin_amdgcn_readfirstlane(incl) < need) return false;  // lane 0's suffix is the total
+  const uint64_t hit = __builtin_amdgcn_ballot_w64(excl < need && incl >= need);  // exactly one lane
+  uint32_t t = 0u, c = excl;
+  bool done = false;
+#pragma unroll
+  for (int i = PER - 1; i >= 0; --i) {
+    if (!done && c + v[i] >= need) {
+      t = static_cast<uint32_t>(PER * lane + i);
+      done = true;
+    }
+    c += v[i];
+  }
+  t_out = kLow + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(t), __builtin_ctzll(hit)));
+  return true;
+}
+
 // Wave-only variant over 64 * PER bins (called by one whole wave); the result lands in s_res[0..2].
 template <int PER>
 __device__ void wave_threshold(const uint32_t* h, uint32_t need, uint32_t* s_res) {
@@ -643,8 +672,7 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
       mx[r] = sl < n_slots ? mrow[sl] : 0u;
     }
   };
-  // the row's largest slot max anchors the histogram (with the recomputation, the query
-  // fragments are built while the first slot maxima are loading)
+  // the row's largest slot max anchors the histogram
   uint32_t mloc = 0u;
   for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
     load_max(c0);
@@ -670,11 +698,21 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
   }
   __syncthreads();
   uint32_t tau = 0u;
+  // Usually the kk-th largest slot max lies within 4 binades of the row's maximum: every wave finds
+  // its bin among the top kTopBins bins by itself, and no barrier follows.  The list below is then
+  // written to h while other waves may still read those bins, so it stays below them; a longer list
+  // sends the row to the radix levels over all of its keys.
+  constexpr int kTopBins = 512;
+  constexpr int kListCap = kHistBins - kTopBins;
+  bool list_cut = false;
   if (static_cast<int64_t>(kk) <= n_slots) {
-    uint32_t t, ab, ct;
-    block_threshold<NT, kHistBins / NT>(h, kk, s_tot, s_res, t, ab, ct);
-    (void)ab;
-    (void)ct;
+    uint32_t t;
+    if (!wave_top_threshold<kHistBins, kTopBins / 64>(h, kk, t)) {  // the same outcome in every wave
+      uint32_t ab, ct;
+      block_threshold<NT, kHistBins / NT>(h, kk, s_tot, s_res, t, ab, ct);
+      (void)ab;
+      (void)ct;
+    }
     tau = t > 0u ? (top - (kHistBins - 1 - t)) << 16 : 0u;
   }
   // qualifying slots (max >= tau) are compacted into a list (in h, free until the radix levels),
@@ -683,9 +721,9 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
     if (n_slots > kSlotPass) load_max(c0);  // otherwise mx still holds the only pass
     if (c0 > 0) {
       // a later pass: the previous pass's list (h) and count are free once every thread is here.
-      // The first pass needs no barrier: s_cnt[1] was zeroed with s_cnt[0], and h is last read
-      // before the final barrier of block_threshold (or, when that is skipped, last written
-      // before the histogram's barrier).
+      // The first pass needs no barrier: s_cnt[1] was zeroed with s_cnt[0], and h's list part
+      // [0, kListCap) is last read before the final barrier of block_threshold (or, when that is
+      // skipped, last written before the histogram's barrier).
       __syncthreads();
       if (tid == 0) s_cnt[1] = 0u;
       __syncthreads();
@@ -706,12 +744,14 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
       base = __builtin_amdgcn_readfirstlane(base);
 #pragma unroll
       for (int r = 0; r < kSlotPer; ++r) {
-        if (q[r]) h[base + static_cast<uint32_t>(mbcnt64(m[r]))] = static_cast<uint32_t>(tid + r * NT);
+        const uint32_t pos = base + static_cast<uint32_t>(mbcnt64(m[r]));
+        if (q[r] && pos < static_cast<uint32_t>(kListCap)) h[pos] = static_cast<uint32_t>(tid + r * NT);
         base += static_cast<uint32_t>(__builtin_popcountll(m[r]));
       }
     }
     __syncthreads();
-    const int n_list = static_cast<int>(s_cnt[1]);
+    list_cut = list_cut || s_cnt[1] > static_cast<uint32_t>(kListCap);
+    const int n_list = min(static_cast<int>(s_cnt[1]), kListCap);
     for (int li = tid; li < n_list; li += NT) {
       const int64_t sl = c0 + h[li];
       uint32_t kw[16];
@@ -741,7 +781,7 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
   }
   __syncthreads();
   const uint32_t n_cand = s_cnt[0];
-  const bool fast = n_cand <= static_cast<uint32_t>(CAP);
+  const bool fast = n_cand <= static_cast<uint32_t>(CAP) && !list_cut;
   const int n = fast ? static_cast<int>(n_cand) : 0;
 
   // ---- 2a. up to NT candidates (the usual case): sort them all, emit the first kk ----

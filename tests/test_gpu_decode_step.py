@@ -71,13 +71,16 @@ def test_decode_step_equals_separate_entry_points(dev, B, S, H, IH, IC, W, k, kv
     np.testing.assert_allclose(to_np_f32(out).reshape(B, H, 128), want, rtol=1e-2, atol=2e-3)
 
 
-@pytest.mark.parametrize("ix_bits", [4, 8])
-@pytest.mark.parametrize("n_special", [300, 100])
-def test_decode_step_exact_ties(dev, ix_bits, n_special):
-    # Every index key is the same code row (equal scores); n_special keys get twice the scale.  With
-    # 100 specials the k-th key is one of ~20000 equal keys, so the fused select's candidates
-    # overflow its LDS list and it recomputes every key of the row before the radix route.
-    B, S, H, IH, IC, W, k = 2, 20000, 12, 4, 64, 32, 256
+@pytest.mark.parametrize("ix_bits,n_special,S", [(4, 300, 20000), (8, 300, 20000), (4, 100, 20000), (8, 100, 20000),
+                                                  (4, 100, 65536), (4, "spread", 20000), (4, "spread", 65536)])
+def test_decode_step_exact_ties(dev, ix_bits, n_special, S):
+    # Every index key is the same code row (equal scores).  With an integer n_special, that many
+    # keys get twice the scale: with 100 the k-th key is one of all the other, equal keys, so the
+    # fused select's candidates overflow its LDS list and the radix levels run over every stored
+    # key of the row (at S = 65536 every slot qualifies, more than its slot list holds).  "spread":
+    # 300 keys get scales 2^(1 + 12 i / 300) times the common one, which puts the k-th largest slot
+    # maximum ~10 binades below the row's largest, past the select's per-wave threshold search.
+    B, H, IH, IC, W, k = 2, 12, 4, 64, 32, 256
     kvq, ixq = PolarQuant(4), PolarQuant(ix_bits)
     kv_codes, kv_scale = kvq.encode(normal((B, S, 128), 31, device=dev))
     row = normal((1, 1, IC), 5, dtype=torch.bfloat16)
@@ -89,12 +92,16 @@ def test_decode_step_exact_ties(dev, ix_bits, n_special):
     g = torch.Generator().manual_seed(9)
     ix_scale = ix_scale.clone()
     for b in range(B):
-        ix_scale[b, torch.randperm(S, generator=g)[:n_special].to(dev)] *= 2
+        if n_special == "spread":
+            mult = torch.tensor([2.0 ** (1 + 12 * i / 300) for i in range(300)], dtype=torch.float32, device=dev)
+            ix_scale[b, torch.randperm(S, generator=g)[:300].to(dev)] *= mult[:, None]
+        else:
+            ix_scale[b, torch.randperm(S, generator=g)[:n_special].to(dev)] *= 2
     q = normal((B, 1, H, 128), 7, device=dev)
     win = normal((B, W, 128), 8, device=dev)
     sink = normal((H,), 9, dtype=torch.float32, device=dev)
     sm = 128 ** -0.5
-    print(f"decode step exact ties bits={ix_bits} specials={n_special}", flush=True)
+    print(f"decode step exact ties bits={ix_bits} specials={n_special} S={S}", flush=True)
     out, idx, sc = csa_decode_step(q, iq, iw, ix_codes, ix_scale, kv_codes, kv_scale, win, sink, sm, k, kv_quant=kvq,
                                    index_quant=ixq, return_scores=True)
     idx1, sc1 = csa_indexer_topk_quant(iq, iw, ix_codes, ix_scale, k, quant=ixq, return_scores=True)

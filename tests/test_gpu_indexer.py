@@ -133,20 +133,28 @@ def test_quant_indexer_shapes_both_paths(dev, indexer_path, B, S, IH, IC, bits, 
     _quant_case(dev, B, S, IH, IC, bits, 50 + S % 97, mode=mode, k=k, valid=valid)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("n_special", [300, 100])
-def test_quant_indexer_exact_ties_take_lowest_indices(dev, indexer_path, bits, n_special):
-    # Every key is the same code row (equal scores); n_special keys get twice the scale (exactly
-    # twice the score).  300 specials put the k-th key inside a small tied group; 100 specials
-    # leave 156 picks among ~20000 equal keys (the threshold bin overflows any candidate list).
-    B, S, IH, IC, k = 2, 20000, 4, 64, 256
+def _equal_key_rows(dev, B, S, IH, IC, bits):
+    """Every key the same code row (equal scores before the scales), queries with positive dots."""
     pq = PolarQuant(bits)
     row = normal((1, 1, IC), 5, dtype=torch.bfloat16)
     codes, scale = pq.encode(row.expand(B, S, IC).contiguous().to(dev))
     q = normal((B, IH, IC), 6, dtype=torch.float32)
     keyf = pq.decode(codes[:1, :1], scale[:1, :1], out_dtype=torch.float32).cpu()[0, 0]
     q = torch.where((q @ keyf)[..., None] < 0, -q, q).to(dev)   # positive dots: nonzero scores
-    w = torch.ones(B, IH, device=dev)
+    return pq, codes, scale, q, torch.ones(B, IH, device=dev)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("n_special", [300, 100])
+@pytest.mark.parametrize("S", [20000, 65536])
+def test_quant_indexer_exact_ties_take_lowest_indices(dev, indexer_path, bits, n_special, S):
+    # Every key is the same code row (equal scores); n_special keys get twice the scale (exactly
+    # twice the score).  300 specials put the k-th key inside a small tied group; 100 specials
+    # leave 156 picks among all the other, equal keys (the threshold bin overflows any candidate
+    # list; at S = 65536 every one of the 4096 slots qualifies, more than the select's slot list
+    # holds).
+    B, IH, IC, k = 2, 4, 64, 256
+    pq, codes, scale, q, w = _equal_key_rows(dev, B, S, IH, IC, bits)
     g = torch.Generator().manual_seed(9)
     special = [torch.randperm(S, generator=g)[:n_special].sort().values for _ in range(B)]
     scale = scale.clone()
@@ -163,6 +171,29 @@ def test_quant_indexer_exact_ties_take_lowest_indices(dev, indexer_path, bits, n
     s = sc.cpu()
     top = min(n_special, k)
     assert torch.all(s[:, :top] == s[:, :1]) and torch.all(s[:, top:] * 2 == s[:, :1])
+
+
+@pytest.mark.parametrize("S", [20000, 65536])
+def test_quant_indexer_top_keys_spread_over_many_binades(dev, indexer_path, S):
+    # 300 keys at random positions get scales spread over 12 binades (2^(1 + 12 i / 300) times the
+    # common one, each a factor 1.028 apart); the top 256 of them are the answer, in scale order.
+    # The k-th largest slot maximum then lies ~10 binades below the row's largest, further down
+    # than the select's first, per-wave threshold search looks; its whole-histogram search finds it.
+    B, IH, IC, k, n_sp = 2, 4, 64, 256, 300
+    pq, codes, scale, q, w = _equal_key_rows(dev, B, S, IH, IC, 4)
+    g = torch.Generator().manual_seed(13)
+    mult = torch.tensor([2.0 ** (1 + 12 * i / n_sp) for i in range(n_sp)], dtype=torch.float32)
+    scale = scale.clone()
+    want = []
+    for b in range(B):
+        pos = torch.randperm(S, generator=g)[:n_sp]
+        scale[b, pos.to(dev)] *= mult.to(dev)[:, None]
+        want.append(pos.flip(0)[:k])   # largest multiplier first
+    idx, sc = csa_indexer_topk_quant(q, w, codes, scale, k, quant=pq, return_scores=True)
+    idx, sc = idx.cpu(), sc.cpu()
+    for b in range(B):
+        assert torch.equal(idx[b], want[b]), (b, idx[b][:8], want[b][:8])
+        assert torch.all(sc[b, 1:] < sc[b, :-1])
 
 
 def test_fp32_indexer_default_rule_is_the_reference_functions(dev):
