@@ -123,9 +123,14 @@ __device__ __forceinline__ RowSources attend_sources(const QAttnMfmaArgs& a, con
   int32_t* sidx = reinterpret_cast<int32_t*>(lds + QLay<NW>::idx);
   RowSources r;
   r.cb = b / a.T;
-  r.n_comp = a.vis ? min<int64_t>(max(a.vis[b], 0), a.n_comp) : a.n_comp;
-  r.w0 = a.wstart ? min<int64_t>(max(a.wstart[b], 0), a.Wt) : 0;
-  r.wl = a.wlen ? min<int64_t>(max(a.wlen[b], 0), a.Wt - r.w0) : a.Wt - r.w0;
+  // the per-row counts are requested together, before any is used (one memory round)
+  int32_t vis = 0, ws = 0, wl = 0;
+  if (a.vis) vis = a.vis[b];
+  if (a.wstart) ws = a.wstart[b];
+  if (a.wlen) wl = a.wlen[b];
+  r.n_comp = a.vis ? min<int64_t>(max(vis, 0), a.n_comp) : a.n_comp;
+  r.w0 = a.wstart ? min<int64_t>(max(ws, 0), a.Wt) : 0;
+  r.wl = a.wlen ? min<int64_t>(max(wl, 0), a.Wt - r.w0) : a.Wt - r.w0;
   r.src0 = static_cast<int64_t>(split) * a.split_src;
   r.src1 = min<int64_t>(r.n_comp + r.wl, r.src0 + a.split_src);
   if (a.sel && !sel_in_lds) {
@@ -154,27 +159,35 @@ __device__ __forceinline__ void attend_prologue(const QAttnMfmaArgs& a, const in
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
   const int H = a.H;
   // The lane's 32 dims, for every key it holds: element j of k-step ks (bf16x8) is dim
-  // 16*(2ks + (j >> 2)) + 4g + (j & 3).  dsign: the diagonal's sign bits for those dims, per
-  // packed bf16 pair (dword e of k-step ks).
+  // 16*(2ks + (j >> 2)) + 4g + (j & 3).  Every load (the diagonal at those dims, the query row of
+  // head c16) is issued before any is used: one memory round.  Lanes past the heads read head 0's
+  // row and use zeros.
+  const bool has_head = c16 < H;
+  const uint16_t* qr = a.q + (b * H + (has_head ? c16 : 0)) * kD + 4 * g;
+  float4 dg[4][2];
+  uint2 lo[4], hi[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+    for (int hv = 0; hv < 2; ++hv) dg[ks][hv] = *reinterpret_cast<const float4*>(a.diag + 16 * (2 * ks + hv) + 4 * g);
+    lo[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks));
+    hi[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks + 1));
+  }
+  // dsign: the diagonal's sign bits for the lane's dims, per packed bf16 pair (dword e of k-step ks)
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
     for (int hv = 0; hv < 2; ++hv) {
-      const float4 dg = *reinterpret_cast<const float4*>(a.diag + 16 * (2 * ks + hv) + 4 * g);
-      f.dsign[ks][2 * hv] = (dg.x < 0.0f ? 0x8000u : 0u) | (dg.y < 0.0f ? 0x80000000u : 0u);
-      f.dsign[ks][2 * hv + 1] = (dg.z < 0.0f ? 0x8000u : 0u) | (dg.w < 0.0f ? 0x80000000u : 0u);
+      const float4 d = dg[ks][hv];
+      f.dsign[ks][2 * hv] = (d.x < 0.0f ? 0x8000u : 0u) | (d.y < 0.0f ? 0x80000000u : 0u);
+      f.dsign[ks][2 * hv + 1] = (d.z < 0.0f ? 0x8000u : 0u) | (d.w < 0.0f ? 0x80000000u : 0u);
     }
   // queries (times the diagonal) as the B operand of S^T: lane (head c16), the lane's dims
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    uint2 lo = make_uint2(0u, 0u), hi = make_uint2(0u, 0u);
-    if (c16 < H) {
-      const uint16_t* qr = a.q + (b * H + c16) * kD + 4 * g;
-      lo = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks));
-      hi = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks + 1));
-    }
-    f.qb[ks] = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x ^ f.dsign[ks][0], lo.y ^ f.dsign[ks][1], hi.x ^ f.dsign[ks][2],
-                                                       hi.y ^ f.dsign[ks][3]));
+    const uint4 w = make_uint4(lo[ks].x ^ f.dsign[ks][0], lo[ks].y ^ f.dsign[ks][1], hi[ks].x ^ f.dsign[ks][2],
+                               hi[ks].y ^ f.dsign[ks][3]);
+    f.qb[ks] = __builtin_bit_cast(bf16x8_t, has_head ? w : make_uint4(0u, 0u, 0u, 0u));
   }
   // H64 rows 16a + c16 as int8 +-1 over the lane's code indices (the A operand of the dequantise).
   // Byte `by` of dword dw holds H64[16a + c16][c] = (-1)^parity((16a + c16) & c) for the code index
