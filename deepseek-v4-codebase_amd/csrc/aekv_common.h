@@ -131,6 +131,14 @@ __device__ __forceinline__ float xor_lane(float v) {
   return __builtin_bit_cast(float, i);
 }
 
+// p[i] when p is set, else dflt.  The load is unconditional (from `fallback`, any readable word,
+// when p is null), so it joins the caller's other loads in one memory round: a load under a branch
+// is given its own wait by the compiler.
+__device__ __forceinline__ int32_t load_or(const int32_t* p, int64_t i, const void* fallback, int32_t dflt) {
+  const int32_t v = *(p ? p + i : static_cast<const int32_t*>(fallback));
+  return p ? v : dflt;
+}
+
 __device__ __forceinline__ float xor_lane_rt(float v, int hl) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_ds_bpermute(static_cast<int>(((threadIdx.x & 63) ^ hl) << 2), __builtin_bit_cast(int, v)));

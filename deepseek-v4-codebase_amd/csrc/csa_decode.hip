@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kFusedThreads) void csa_decode_fused_kernel(idx::Mf
   qattn::attend_prologue<KV_BITS>(qa, b, f);
   idx::select_row<kFusedThreads, kFusedCap>(ia, b, out_idx, out_score, reinterpret_cast<int32_t*>(lds + FusedLay::idx));
   __builtin_amdgcn_s_waitcnt(0);  // the window's direct loads (vmcnt) before the barrier in attend_main
-  const qattn::RowSources rs = qattn::attend_sources<8>(qa, b, 0, lds, true);
+  const qattn::RowSources rs = qattn::attend_sources<8>(qa, b, 0, nullptr);
   qattn::attend_main<KV_BITS, 8>(qa, b, 0, lds, f, rs, win_lds);
 }
 

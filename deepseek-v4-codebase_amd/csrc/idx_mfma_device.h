@@ -298,24 +298,48 @@ __device__ void wave_threshold(const uint32_t* h, uint32_t need, uint32_t* s_res
 }
 
 // ---- query side: rotation, digits, A fragments (once per workgroup, in LDS) --------------------
-// Wave wv rotates heads wv, wv+4, .. (< 4*NRB); lane l holds elements l + 64e of the head.
+// Wave wv rotates heads wv + 4i (i < NRB); lane l holds elements l + 64e of the head.
 // q~ = _wht(diag * q): stages h = 1..32 pair lanes (xor_lane), stage 64 pairs e = 0 and 1.  Then
 // every lane assembles its A fragments (4 heads x 4 digits per row block) and combine constants.
+//
+// The query values, the diagonal and the head weights of a row, requested by query_loads for every
+// row of the workgroup before any is used (one memory round; heads past IH read head 0's values).
+template <int IC, int NRB>
+struct QueryRaw {
+  float q[NRB][IC / 64];
+  float dg[IC / 64];
+  float w[NRB];
+};
+
+template <int IC, int NRB>
+__device__ __forceinline__ void query_loads(const MfmaIdxArgs& a, int b, QueryRaw<IC, NRB>& r) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int e = 0; e < IC / 64; ++e) r.dg[e] = a.diag[lane + 64 * e];
+#pragma unroll
+  for (int i = 0; i < NRB; ++i) {
+    const int h = wv + 4 * i < a.IH ? wv + 4 * i : 0;
+#pragma unroll
+    for (int e = 0; e < IC / 64; ++e) r.q[i][e] = a.q[(static_cast<int64_t>(b) * a.IH + h) * IC + lane + 64 * e];
+    r.w[i] = a.w[static_cast<int64_t>(b) * a.IH + h];
+  }
+}
+
 template <int BITS, int IC, int NRB>
-__device__ __forceinline__ void query_fragments(const MfmaIdxArgs& a, int b, int8_t (*dig)[16][IC], float (*hf)[4],
-                                                float (*hb)[2], i32x4_t (&A)[NRB][IC / 64], float (&f)[NRB][4],
-                                                float (&lo)[NRB], float (&hi)[NRB]) {
+__device__ __forceinline__ void query_fragments(const MfmaIdxArgs& a, const QueryRaw<IC, NRB>& raw,
+                                                int8_t (*dig)[16][IC], float (*hf)[4], float (*hb)[2],
+                                                i32x4_t (&A)[NRB][IC / 64], float (&f)[NRB][4], float (&lo)[NRB],
+                                                float (&hi)[NRB]) {
   constexpr int KS = IC / 64;
   constexpr int EPL = IC / 64;
   const int IH = a.IH;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
-  for (int h = wv; h < 4 * NRB; h += 4) {
+#pragma unroll
+  for (int i = 0; i < NRB; ++i) {
+    const int h = wv + 4 * i;
     float v[EPL];
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const int c = lane + 64 * e;
-      v[e] = h < IH ? a.q[(static_cast<int64_t>(b) * IH + h) * IC + c] * a.diag[c] : 0.0f;
-    }
+    for (int e = 0; e < EPL; ++e) v[e] = h < IH ? raw.q[i][e] * raw.dg[e] : 0.0f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
       float x = v[e];
@@ -356,10 +380,12 @@ __device__ __forceinline__ void query_fragments(const MfmaIdxArgs& a, int b, int
         dig[d][h][lane + 64 * e] = static_cast<int8_t>(di);
       }
     }
+    // the head's weight (wave-uniform): read out before the lane-0 branch, so that its load is not
+    // moved into that branch and given a wait of its own
+    const float wr = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, raw.w[i])));
     if (lane == 0) {
       float wa = 0.0f, lw = -__builtin_inff(), hw = __builtin_inff();
       if (h < IH) {
-        const float wr = a.w[static_cast<int64_t>(b) * IH + h];
         if (a.mode == AEKV_IDX_SOFTPLUS) {
           wa = softplus_f32(wr);
           lw = 0.0f;
@@ -525,7 +551,8 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
   int64_t nv[TT], nv_max = 0;
 #pragma unroll
   for (int tt = 0; tt < TT; ++tt) {
-    nv[tt] = rok[tt] ? visible(a, static_cast<int>(row[tt])) : 0;
+    // (unconditional loads, requested with the query's: absent counts give all S)
+    nv[tt] = rok[tt] ? min<int64_t>(S, max(0, load_or(a.valid, row[tt], a.q, 0x7fffffff))) : 0;
     nv_max = max(nv_max, nv[tt]);
   }
 
@@ -534,10 +561,15 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
   __shared__ float hb[16][2];  // per head: clamp bounds
   i32x4_t A[TT][NRB][KS];
   float f[TT][NRB][4], lo[TT][NRB], hi[TT][NRB];
+  {
+    QueryRaw<IC, NRB> raw[TT];
 #pragma unroll
-  for (int tt = 0; tt < TT; ++tt) {
-    if (tt > 0) __syncthreads();  // the previous row's fragments have been read out of LDS
-    query_fragments<BITS, IC, NRB>(a, static_cast<int>(row[tt]), dig, hf, hb, A[tt], f[tt], lo[tt], hi[tt]);
+    for (int tt = 0; tt < TT; ++tt) query_loads<IC, NRB>(a, static_cast<int>(row[tt]), raw[tt]);
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      if (tt > 0) __syncthreads();  // the previous row's fragments have been read out of LDS
+      query_fragments<BITS, IC, NRB>(a, raw[tt], dig, hf, hb, A[tt], f[tt], lo[tt], hi[tt]);
+    }
   }
 
   // key-row bases (wave-uniform) and 32-bit offsets within the rows (S <= kMaxKeys)

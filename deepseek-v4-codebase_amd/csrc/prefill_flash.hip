@@ -223,13 +223,24 @@ flash_sink_attn_kernel(FlashArgs a) {
   const int h = rv ? r - t * H : 0;
   const int64_t bt = static_cast<int64_t>(b) * a.T + t;
 
-  // the row's sources: blocks [0, nb), window entries [w0, w1)
-  int nb = 0, w0 = 0, w1 = 0;
-  if (rv) {
-    nb = a.vis ? static_cast<int>(min<int64_t>(max(a.vis[bt], 0), a.S)) : static_cast<int>(a.S);
-    w0 = a.wstart ? static_cast<int>(min<int64_t>(max(a.wstart[bt], 0), a.Wt)) : 0;
-    w1 = w0 + (a.wlen ? static_cast<int>(min<int64_t>(max(a.wlen[bt], 0), a.Wt - w0)) : static_cast<int>(a.Wt) - w0);
+  // Every load of the prologue is issued before any is used (one memory round): the row's source
+  // counts first, then its query (lanes past the rows read row 0 and use zeros), so that the
+  // bounds' wait leaves the query loads in flight.
+  // (absent counts: all S blocks, window from 0 to its end)
+  const int32_t c_vis = load_or(a.vis, bt, a.q, 0x7fffffff), c_ws = load_or(a.wstart, bt, a.q, 0);
+  const int32_t c_wl = load_or(a.wlen, bt, a.q, 0x7fffffff);
+  uint4 qv[8];
+  {
+    const uint16_t* qp = a.q + (static_cast<int64_t>(b) * RT + (rv ? r : 0)) * kFD + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qv[ks] = *reinterpret_cast<const uint4*>(qp + 16 * ks);
   }
+  // the row's sources: blocks [0, nb), window entries [w0, w1) (computed for every lane, then
+  // masked: a branch on rv would take the count loads, and their wait, into it)
+  const int nb_r = static_cast<int>(min<int64_t>(max(c_vis, 0), a.S));
+  const int w0_r = static_cast<int>(min<int64_t>(max(c_ws, 0), a.Wt));
+  const int wl_r = static_cast<int>(min<int64_t>(max(c_wl, 0), a.Wt - w0_r));
+  const int nb = rv ? nb_r : 0, w0 = rv ? w0_r : 0, w1 = rv ? w0_r + wl_r : 0;
   // the workgroup's bounds: reduced within each wave, then over the 4 waves through LDS
   {
     const bool hw = rv && w1 > w0;
@@ -266,11 +277,7 @@ flash_sink_attn_kernel(FlashArgs a) {
   // the row's query as the B operand of S^T = K Q^T: dims 16 ks + 8 hh .. + 7
   v8 qb[8];
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (rv) v = *reinterpret_cast<const uint4*>(a.q + (static_cast<int64_t>(b) * RT + r) * kFD + 16 * ks + 8 * hh);
-    qb[ks] = __builtin_bit_cast(v8, v);
-  }
+  for (int ks = 0; ks < 8; ++ks) qb[ks] = __builtin_bit_cast(v8, rv ? qv[ks] : make_uint4(0u, 0u, 0u, 0u));
   // the queries have landed before any tile load is issued: otherwise the wait for them, merged
   // over the loop's back edge, becomes a wait for every tile load on every iteration
   __builtin_amdgcn_s_waitcnt(0);

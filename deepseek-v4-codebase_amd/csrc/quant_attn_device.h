@@ -114,33 +114,55 @@ struct RowSources {
   int64_t cb, n_comp, w0, wl, src0, src1;
 };
 
-// The row's source ranges; unless sel_in_lds, the selected block ids of [src0, src1) are copied to
-// LDS (-1: skipped), to be read after the next barrier.
+// The workgroup's selected block ids (entry i of its piece in thread i % (64 NW), slot i / (64 NW)).
+template <int NW>
+struct RowSel {
+  int64_t v[kSplitSrc / (64 * NW)];
+};
+
+// The row's source ranges.  With sv, the selected block ids of the workgroup's piece are requested
+// as well, over the whole piece of the row's selection (in bounds; entries past the visible count
+// are never read), so that they need not wait for the counts; store_sel puts them in LDS.
 template <int NW>
 __device__ __forceinline__ RowSources attend_sources(const QAttnMfmaArgs& a, const int64_t b, const int split,
-                                                     unsigned char* lds, const bool sel_in_lds) {
+                                                     RowSel<NW>* sv) {
   constexpr int kT = 64 * NW;
-  int32_t* sidx = reinterpret_cast<int32_t*>(lds + QLay<NW>::idx);
   RowSources r;
   r.cb = b / a.T;
   // the per-row counts are requested together, before any is used (one memory round)
-  int32_t vis = 0, ws = 0, wl = 0;
-  if (a.vis) vis = a.vis[b];
-  if (a.wstart) ws = a.wstart[b];
-  if (a.wlen) wl = a.wlen[b];
-  r.n_comp = a.vis ? min<int64_t>(max(vis, 0), a.n_comp) : a.n_comp;
-  r.w0 = a.wstart ? min<int64_t>(max(ws, 0), a.Wt) : 0;
-  r.wl = a.wlen ? min<int64_t>(max(wl, 0), a.Wt - r.w0) : a.Wt - r.w0;
+  // (absent counts: all n_comp blocks, window from 0 to its end)
+  const int32_t vis = load_or(a.vis, b, a.q, 0x7fffffff), ws = load_or(a.wstart, b, a.q, 0);
+  const int32_t wl = load_or(a.wlen, b, a.q, 0x7fffffff);
+  r.n_comp = min<int64_t>(max(vis, 0), a.n_comp);
+  r.w0 = min<int64_t>(max(ws, 0), a.Wt);
+  r.wl = min<int64_t>(max(wl, 0), a.Wt - r.w0);
   r.src0 = static_cast<int64_t>(split) * a.split_src;
-  r.src1 = min<int64_t>(r.n_comp + r.wl, r.src0 + a.split_src);
-  if (a.sel && !sel_in_lds) {
-    const int64_t nsel = min<int64_t>(r.src1, r.n_comp) - r.src0;
-    for (int64_t i = threadIdx.x; i < nsel; i += kT) {
-      const int64_t blk = a.sel[b * a.K + r.src0 + i];
-      sidx[i] = blk >= 0 && blk < a.S ? static_cast<int32_t>(blk) : -1;
+  if (sv) {
+    const int64_t n_piece = min<int64_t>(a.K - r.src0, a.split_src);
+#pragma unroll
+    for (int j = 0; j < kSplitSrc / kT; ++j) {
+      const int64_t i = threadIdx.x + static_cast<int64_t>(j) * kT;
+      sv->v[j] = i < n_piece ? a.sel[b * a.K + r.src0 + i] : -1;
     }
   }
+  r.src1 = min<int64_t>(r.n_comp + r.wl, r.src0 + a.split_src);
   return r;
+}
+
+// The selected block ids of [src0, min(src1, n_comp)) into LDS (-1: skipped), read after the next
+// barrier.
+template <int NW>
+__device__ __forceinline__ void store_sel(const QAttnMfmaArgs& a, const RowSources& r, const RowSel<NW>& sv,
+                                          unsigned char* lds) {
+  constexpr int kT = 64 * NW;
+  int32_t* sidx = reinterpret_cast<int32_t*>(lds + QLay<NW>::idx);
+  const int64_t nsel = min<int64_t>(r.src1, r.n_comp) - r.src0;
+#pragma unroll
+  for (int j = 0; j < kSplitSrc / kT; ++j) {
+    const int64_t i = threadIdx.x + static_cast<int64_t>(j) * kT;
+    const int64_t blk = sv.v[j];
+    if (i < nsel) sidx[i] = blk >= 0 && blk < a.S ? static_cast<int32_t>(blk) : -1;
+  }
 }
 
 
@@ -485,14 +507,16 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
 }
 
 
-// attend_sources + attend_prologue + attend_main: the selected block ids' loads are in flight while
-// the per-lane constants are computed.
+// attend_sources + attend_prologue + store_sel + attend_main: the row's counts, its selected block
+// ids and the prologue's loads are requested in one memory round.
 template <int BITS, int NW>
 __device__ __forceinline__ void attend_row(const QAttnMfmaArgs& a, const int64_t b, const int split,
-                                           unsigned char* lds, const bool sel_in_lds) {
-  const RowSources rs = attend_sources<NW>(a, b, split, lds, sel_in_lds);
+                                           unsigned char* lds) {
+  RowSel<NW> sv;
+  const RowSources rs = attend_sources<NW>(a, b, split, a.sel ? &sv : nullptr);
   AttnFrags<BITS> f;
   attend_prologue<BITS>(a, b, f);
+  if (a.sel) store_sel<NW>(a, rs, sv, lds);
   attend_main<BITS, NW>(a, b, split, lds, f, rs, nullptr);
 }
 
@@ -513,7 +537,7 @@ __global__ __launch_bounds__(64 * NW) void quant_attn_mfma_kernel(QAttnMfmaArgs 
     row = w / nx;
     split = w % nx;
   }
-  attend_row<BITS, NW>(a, row, static_cast<int>(split), lds, false);
+  attend_row<BITS, NW>(a, row, static_cast<int>(split), lds);
 }
 
 }  // namespace qattn
