@@ -561,17 +561,6 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
   __shared__ float hb[16][2];  // per head: clamp bounds
   i32x4_t A[TT][NRB][KS];
   float f[TT][NRB][4], lo[TT][NRB], hi[TT][NRB];
-  {
-    QueryRaw<IC, NRB> raw[TT];
-#pragma unroll
-    for (int tt = 0; tt < TT; ++tt) query_loads<IC, NRB>(a, static_cast<int>(row[tt]), raw[tt]);
-#pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-      if (tt > 0) __syncthreads();  // the previous row's fragments have been read out of LDS
-      query_fragments<BITS, IC, NRB>(a, raw[tt], dig, hf, hb, A[tt], f[tt], lo[tt], hi[tt]);
-    }
-  }
-
   // key-row bases (wave-uniform) and 32-bit offsets within the rows (S <= kMaxKeys)
   const uint8_t* crow = a.codes + kr * S * RB;
   const uint8_t* srow = reinterpret_cast<const uint8_t*>(a.kscale + kr * S);
@@ -584,36 +573,57 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
   int nv_mini = nv_maxi;
 #pragma unroll
   for (int tt = 0; tt < TT; ++tt) nv_mini = min(nv_mini, nvi[tt]);
-  // one group of SPW slots from key kb; FULL: every key of the group is visible to every row (no
-  // bounds checks)
-  auto group = [&](const int kb, auto full_c) {
-    constexpr bool FULL = decltype(full_c)::value;
+  // one group of SPW slots from key kb: its codes and scales (keys at or past lim read key 0;
+  // CLAMP false: none is), then the scores; FULL: every key of the group is visible to every row
+  // (no bounds checks)
+  struct GroupRaw {
     uint32_t raw[SPW][4][KS][LW];
     float scl[SPW];
+  };
+  auto load_group = [&](const int kb, auto clamp_c, const int lim, GroupRaw& gr) {
+    constexpr bool CLAMP = decltype(clamp_c)::value;
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
 #pragma unroll
       for (int tq = 0; tq < 4; ++tq) {
         const int j = kb + 64 * s + 16 * tq + (lane & 15);
-        // keys past a row's count read key 0 (nv_max >= 1 here) and are dropped
-        const uint32_t jr = FULL || j < nv_maxi ? static_cast<uint32_t>(j) : 0u;
-        load_key_codes<BITS, KS, LW>(crow, jr, g, raw[s][tq]);
+        const uint32_t jr = !CLAMP || j < lim ? static_cast<uint32_t>(j) : 0u;
+        load_key_codes<BITS, KS, LW>(crow, jr, g, gr.raw[s][tq]);
       }
       const int jo = kb + 64 * s + lane;
-      scl[s] = *reinterpret_cast<const float*>(srow + (FULL || jo < nv_maxi ? static_cast<uint32_t>(jo) * 4u : 0u));
+      gr.scl[s] = *reinterpret_cast<const float*>(srow + (!CLAMP || jo < lim ? static_cast<uint32_t>(jo) * 4u : 0u));
     }
+  };
+  // The first memory round: the rows' counts (above), their queries and, for single-target rows, the
+  // wave's first key group, which does not depend on the query (keys past S read key 0; those past
+  // a row's count are dropped when scored).
+  const bool preload = TT == 1 && a.gpw > 1;  // wave-uniform
+  GroupRaw g0;
+  {
+    QueryRaw<IC, NRB> raw[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) query_loads<IC, NRB>(a, static_cast<int>(row[tt]), raw[tt]);
+    if (preload && wave_base < S) load_group(static_cast<int>(wave_base), std::true_type{}, static_cast<int>(S), g0);
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      if (tt > 0) __syncthreads();  // the previous row's fragments have been read out of LDS
+      query_fragments<BITS, IC, NRB>(a, raw[tt], dig, hf, hb, A[tt], f[tt], lo[tt], hi[tt]);
+    }
+  }
+  auto score_group = [&](const int kb, auto full_c, const GroupRaw& gr) {
+    constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
       i32x4_t Bop[4][KS];
 #pragma unroll
-      for (int tq = 0; tq < 4; ++tq) build_bop<BITS, KS, LW>(raw[s][tq], Bop[tq]);
+      for (int tq = 0; tq < 4; ++tq) build_bop<BITS, KS, LW>(gr.raw[s][tq], Bop[tq]);
       const int jo = kb + 64 * s + lane;
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
         if (!FULL && TT > 1 && kb + 64 * s >= nvi[tt]) continue;  // wave-uniform: this row has no key in the slot group
         const float mine = lane_score<NRB, KS>(A[tt], Bop, f[tt], lo[tt], hi[tt]);
         const bool ok = FULL || jo < nvi[tt];
-        const uint32_t key = ok ? order_key(mine * scl[s]) : 0u;
+        const uint32_t key = ok ? order_key(mine * gr.scl[s]) : 0u;
         uint8_t* krow = reinterpret_cast<uint8_t*>(a.keys + row[tt] * a.ks);
         uint8_t* mrow = reinterpret_cast<uint8_t*>(a.smax + row[tt] * a.ms);
         if (ok) *reinterpret_cast<uint32_t*>(krow + static_cast<uint32_t>(jo) * 4u) = key;
@@ -627,12 +637,34 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
       }
     }
   };
+  auto group = [&](const int kb, auto full_c) {
+    GroupRaw gr;
+    // keys past a row's count read key 0 (nv_max >= 1 here) and are dropped
+    load_group(kb, std::integral_constant<bool, !decltype(full_c)::value>{}, nv_maxi, gr);
+    score_group(kb, full_c, gr);
+  };
 #pragma unroll 1
   for (int gi = 0; gi < a.gpw; ++gi) {
     const int64_t kb64 = wave_base + gi * kGroupKeys;
     if (kb64 >= nv_max) break;  // wave-uniform
-    if (kb64 + kGroupKeys <= nv_mini) group(static_cast<int>(kb64), std::true_type{});
-    else group(static_cast<int>(kb64), std::false_type{});
+    const bool full = kb64 + kGroupKeys <= nv_mini;
+    if (preload && gi == 0) {
+      // the preloaded codes enter here (the operands built from them are not hoisted above the
+      // query phase, where they would hold registers)
+#pragma unroll
+      for (int s = 0; s < SPW; ++s)
+#pragma unroll
+        for (int tq = 0; tq < 4; ++tq)
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int w = 0; w < LW; ++w) asm volatile("" : "+v"(g0.raw[s][tq][ks][w]));
+      if (full) score_group(static_cast<int>(kb64), std::true_type{}, g0);
+      else score_group(static_cast<int>(kb64), std::false_type{}, g0);
+    } else {
+      if (full) group(static_cast<int>(kb64), std::true_type{});
+      else group(static_cast<int>(kb64), std::false_type{});
+    }
   }
 }
 
