@@ -345,6 +345,7 @@ __device__ __forceinline__ void row_stages8(float (&a)[8], float s8, float s16, 
 
 // Decodes the four vectors of pass `pv` (vectors 4pv .. 4pv+3) from the lane's code dword `w` and
 // its vector's scale `s`.
+template <bool NT>
 __device__ __forceinline__ void decode_pass(uint32_t w, float s, int64_t pv, int64_t n_vec, int row, int chunk,
                                             const float (&sg)[4], float sc, uint32_t dsig0, uint32_t dsig1,
                                             uint32_t dsig2, uint32_t dsig3, const uint8_t* __restrict__ codes,
@@ -390,7 +391,12 @@ __device__ __forceinline__ void decode_pass(uint32_t w, float s, int64_t pv, int
   const uint32_t o1 = pack_bf16x2(fmaf(a[2], sc, 0.0f), fmaf(a[3], sc, 0.0f)) ^ dsig1;
   const uint32_t o2 = pack_bf16x2(fmaf(a[4], sc, 0.0f), fmaf(a[5], sc, 0.0f)) ^ dsig2;
   const uint32_t o3 = pack_bf16x2(fmaf(a[6], sc, 0.0f), fmaf(a[7], sc, 0.0f)) ^ dsig3;
-  if (v < n_vec) *reinterpret_cast<uint4*>(out + v * 128 + 8 * chunk) = make_uint4(o0, o1, o2, o3);
+  if (v < n_vec) {
+    if constexpr (NT)  // a layer-sized output streams past the caches
+      __builtin_nontemporal_store(u32x4_t{o0, o1, o2, o3}, reinterpret_cast<u32x4_t*>(out + v * 128 + 8 * chunk));
+    else
+      *reinterpret_cast<uint4*>(out + v * 128 + 8 * chunk) = make_uint4(o0, o1, o2, o3);
+  }
 }
 
 // PP > 0: PP consecutive 4-vector passes per wave, all loads issued first, no loop (the launch
@@ -433,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void tq_decode4_d128_bf16_kernel(const ui
 #pragma unroll
     for (int i = 0; i < PP; ++i)
       if (p0 + i < n_pass)
-        decode_pass(wq[i], sq[i], p0 + i, n_vec, row, chunk, sg, sc, dsig[0], dsig[1], dsig[2], dsig[3], cb, scale,
+        decode_pass<true>(wq[i], sq[i], p0 + i, n_vec, row, chunk, sg, sc, dsig[0], dsig[1], dsig[2], dsig[3], cb, scale,
                     diag, c, out);
     return;
   }
@@ -449,7 +455,7 @@ __global__ __launch_bounds__(kThreads) void tq_decode4_d128_bf16_kernel(const ui
     float sn;
     load(pv + n_waves < n_pass ? pv + n_waves : pv, wn, sn);
     __builtin_amdgcn_sched_barrier(0);
-    decode_pass(w, s, pv, n_vec, row, chunk, sg, sc, dsig[0], dsig[1], dsig[2], dsig[3], cb, scale, diag, c, out);
+    decode_pass<false>(w, s, pv, n_vec, row, chunk, sg, sc, dsig[0], dsig[1], dsig[2], dsig[3], cb, scale, diag, c, out);
     pv += n_waves;
     if (pv >= n_pass) break;
     w = wn;
