@@ -245,8 +245,9 @@ __device__ __forceinline__ void attend_prologue(const QAttnMfmaArgs& a, const in
 
 // The row's attention over its sources (after attend_sources and attend_prologue).  win_lds
 // (nullable): the cache row's window entries 0 .. Wt-1 staged in LDS (win_chunk layout) instead of
-// read from global memory.
-template <int BITS, int NW>
+// read from global memory.  PIPE: a wave requests its next group's rows before decoding the
+// current one (the 4-wave prefill instance, whose register budget has room for them).
+template <int BITS, int NW, bool PIPE = false>
 __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_t b, const int split,
                                             unsigned char* lds, const AttnFrags<BITS>& f, const RowSources& rs,
                                             const unsigned char* win_lds) {
@@ -275,13 +276,18 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
   const float kscale_unit = (BITS == 4 ? 1.0f / 16.0f : 1.0f) * a.wscale;
 
   const int n_groups = src1 > src0 ? static_cast<int>((src1 - src0 + kGroup - 1) / kGroup) : 0;
-#pragma unroll 1
-  for (int G = wv; G < n_groups; G += kW) {
-    // both blocks' rows are requested before either is decoded (two gathers in flight)
+  // group G's sources (32 per group): both blocks' rows are requested before either is decoded
+  struct GroupIn {
     int kind[2];  // 0 empty, 1 code row, 2 window row
     uint32_t cw[2][2][BITS == 8 ? 4 : 2];
     float sraw[2];
     uint2 wv2[2][4][2];
+  };
+  auto fetch = [&](const int G, GroupIn& in) {
+    int (&kind)[2] = in.kind;
+    auto& cw = in.cw;
+    float (&sraw)[2] = in.sraw;
+    auto& wv2 = in.wv2;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       // lane (key c16 of block kb): its source, code bytes (two halves) or window dims
@@ -339,6 +345,12 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
       }
     }
 
+  };
+  auto consume = [&](const int G, const GroupIn& in) {
+    const int (&kind)[2] = in.kind;
+    const auto& cw = in.cw;
+    const float (&sraw)[2] = in.sraw;
+    const auto& wv2 = in.wv2;
     bf16x8_t kf[2][4];
     bool okk[2];
 #pragma unroll
@@ -449,6 +461,25 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
       // O^T[nb][i] = O[head c16][dim 16nb + 4g + i] (times diag, removed at the end)
       O[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, O[nb], 0, 0, 0);
     }
+  };
+  if constexpr (PIPE) {
+    // the next group's rows are requested before this group is decoded
+    GroupIn cur, nxt;
+    if (wv < n_groups) fetch(wv, cur);
+#pragma unroll 1
+    for (int G = wv; G < n_groups; G += kW) {
+      const bool more = G + kW < n_groups;  // wave-uniform
+      if (more) fetch(G + kW, nxt);
+      consume(G, cur);
+      if (more) cur = nxt;
+    }
+  } else {
+#pragma unroll 1
+    for (int G = wv; G < n_groups; G += kW) {
+      GroupIn in;
+      fetch(G, in);
+      consume(G, in);
+    }
   }
 
   // ---- merge the waves (and the sink, unless this is one split of several) ----
@@ -517,7 +548,7 @@ __device__ __forceinline__ void attend_row(const QAttnMfmaArgs& a, const int64_t
   AttnFrags<BITS> f;
   attend_prologue<BITS>(a, b, f);
   if (a.sel) store_sel<NW>(a, rs, sv, lds);
-  attend_main<BITS, NW>(a, b, split, lds, f, rs, nullptr);
+  attend_main<BITS, NW, NW == 4>(a, b, split, lds, f, rs, nullptr);
 }
 
 // One row (or one split of a long row) per workgroup of 64 * NW threads.
