@@ -13,10 +13,13 @@ constexpr int kMaxCombineSplits = 256;  // most source pieces per row
 // out = sum_s e^{m_s-M} acc_s / L (the sink counted once, aether_pipeline/serving.py:125-129).  32
 // threads per (row, head), 4 dims each; the splits' (m, l, acc) are loaded in chunks of 8 whose
 // loads are all issued together and merged online, so a row takes one memory round per 8 splits.
-__global__ __launch_bounds__(kThreads) void quant_attn_mfma_combine_kernel(QAttnMfmaArgs a, int64_t rows) {
+// Workgroups of kCombineThreads (two (row, head) pairs): a decode step's few hundred pairs then
+// spread over as many CUs, instead of queueing their loads on a few.
+constexpr int kCombineThreads = 64;
+__global__ __launch_bounds__(kCombineThreads) void quant_attn_mfma_combine_kernel(QAttnMfmaArgs a, int64_t rows) {
   constexpr int kChunk = 8;
   const int H = a.H, ns = a.n_split;
-  const int64_t rh = static_cast<int64_t>(blockIdx.x) * (kThreads / 32) + (threadIdx.x >> 5);  // row * H + head
+  const int64_t rh = static_cast<int64_t>(blockIdx.x) * (kCombineThreads / 32) + (threadIdx.x >> 5);  // row * H + head
   if (rh >= rows * H) return;
   const int64_t b = rh / H;
   const int h = static_cast<int>(rh - b * H), j = threadIdx.x & 31;
@@ -132,8 +135,9 @@ int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* s
                      lds, st, a);
   if (int rc = check_launch(who)) return rc;
   if (n_split > 1) {
-    const int64_t n_wg = ceil_div(rows * H, kThreads / 32);
-    hipLaunchKernelGGL(quant_attn_mfma_combine_kernel, dim3(static_cast<uint32_t>(n_wg)), dim3(kThreads), 0, st, a, rows);
+    const int64_t n_wg = ceil_div(rows * H, kCombineThreads / 32);
+    hipLaunchKernelGGL(quant_attn_mfma_combine_kernel, dim3(static_cast<uint32_t>(n_wg)), dim3(kCombineThreads), 0, st, a,
+                       rows);
     return check_launch(who);
   }
   return AEKV_OK;
