@@ -191,6 +191,18 @@ def test_split_rows_whatever_the_workspace_holds(dev):
     _close(outs[0].view(B, H, D), _oracle_quant(pq, codes, scale, None, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
 
 
+@pytest.mark.parametrize("B,H", [(3, 5), (1, 1)])
+def test_split_rows_odd_row_head_count(dev, B, H):
+    # 1516 sources per row: three pieces of 512 and the combine, whose workgroups hold two
+    # (row, head) pairs; an odd rows x heads leaves the last workgroup's second pair empty
+    D, S, W, bits = 128, 1500, 16, 4
+    pq, codes, scale, q, win, sink = _quant_inputs(dev, B, H, D, S, W, bits, 91 + H)
+    sm = D ** -0.5
+    print(f"split rows B={B} H={H}", flush=True)
+    got = hca_decode(q, codes, scale, win, sink, sm, kv_quant=pq)
+    _close(got.view(B, H, D), _oracle_quant(pq, codes, scale, None, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
+
+
 @pytest.mark.parametrize("S", [130400, 130900])
 def test_quant_attention_most_pieces(dev, S):
     # one row, S blocks + 128 window rows in pieces of 512: 255 pieces, and 256 (the launch limit);
