@@ -270,14 +270,15 @@ __global__ __launch_bounds__(64 * NW) void gather_attn_kernel(GatherArgs a) {
 // Merges the source pieces of each (target, head) row: M = max(sink, piece maxima),
 // L = 2^(sink - M) + sum_p 2^(m_p - M) l_p, out = sum_p 2^(m_p - M) O_p / L (log2 units), as an
 // online merge over chunks of 8 pieces whose loads are all issued together.  32 threads per row,
-// 4 dims each.
-template <int DT>
-__global__ __launch_bounds__(256) void sink_attn_combine_kernel(const float* __restrict__ part, int n_split,
-                                                                const uint16_t* __restrict__ sink, int sink_scalar,
-                                                                int H, int64_t rows, uint16_t* __restrict__ out) {
+// 4 dims each, NT / 32 rows per workgroup: 8, or 2 when 8 would leave CUs without a workgroup, so
+// that a call of few rows spreads its loads over as many CUs.
+template <int DT, int NT>
+__global__ __launch_bounds__(NT) void sink_attn_combine_kernel(const float* __restrict__ part, int n_split,
+                                                               const uint16_t* __restrict__ sink, int sink_scalar,
+                                                               int H, int64_t rows, uint16_t* __restrict__ out) {
   using E = Elem<DT>;
   constexpr int kChunk = 8;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (NT / 32) + (threadIdx.x >> 5);
   if (row >= rows) return;
   const int j = threadIdx.x & 31;
   const float* p = part + row * n_split * kPartStride;
@@ -422,16 +423,23 @@ int sink_attention_mfma(const void* q, const void* kv, const void* idx, int idx_
   }
   if (p.n_split == 1) return AEKV_OK;
   const int64_t n = rows * H;
-  if (ceil_div(n, 8) > 0x7fffffffLL) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many rows", who);
-  const dim3 grid(static_cast<uint32_t>(ceil_div(n, 8)));
+  const int nt = ceil_div(n, int64_t(8)) >= 256 ? 256 : 64;
+  const int64_t n_wg = ceil_div(n, static_cast<int64_t>(nt / 32));
+  if (n_wg > 0x7fffffffLL) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many rows", who);
+  const dim3 grid(static_cast<uint32_t>(n_wg));
   const uint16_t* sk = static_cast<const uint16_t*>(sink);
   uint16_t* o = static_cast<uint16_t*>(out);
-  if (dtype == AEKV_BF16)
-    hipLaunchKernelGGL(sink_attn_combine_kernel<AEKV_BF16>, grid, dim3(256), 0, st, part, p.n_split, sk, sink_scalar,
-                       static_cast<int>(H), n, o);
-  else
-    hipLaunchKernelGGL(sink_attn_combine_kernel<AEKV_F16>, grid, dim3(256), 0, st, part, p.n_split, sk, sink_scalar,
-                       static_cast<int>(H), n, o);
+  const int hh = static_cast<int>(H);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(nt), 0, st, part, p.n_split, sk, sink_scalar, hh, n, o);
+  };
+  if (dtype == AEKV_BF16) {
+    if (nt == 256) launch(sink_attn_combine_kernel<AEKV_BF16, 256>);
+    else launch(sink_attn_combine_kernel<AEKV_BF16, 64>);
+  } else {
+    if (nt == 256) launch(sink_attn_combine_kernel<AEKV_F16, 256>);
+    else launch(sink_attn_combine_kernel<AEKV_F16, 64>);
+  }
   return check_launch(who);
 }
 
