@@ -112,6 +112,33 @@ def timed_graph(fn, steps: int, warmup: int, inner: int = GRAPH_STEPS):
     return ms
 
 
+# Infinity Cache (MALL) of MI355X: a step's caches that fit in it stay there across replays of the
+# same inputs.  The cold timing rotates enough distinct layer caches that more than twice this much
+# is touched between two visits of one layer.
+MALL_BYTES = 256 << 20
+
+
+def timed_graph_layers(fns, steps: int, warmup: int):
+    """Average ms per call when the calls fns[0], fns[1], ... (one per layer, each on its own
+    caches) are captured in that order in one HIP graph and the graph is replayed: the engine's
+    token step visits every layer once (aether_2b/serving.py:709-721), so a layer's caches are cold
+    again by its next visit whenever the layers' working sets together exceed the caches."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for fn in fns[:3]:
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for fn in fns:
+            fn()
+    ms = timed(g.replay, max(1, steps // 4), max(1, warmup // 4)) / len(fns)
+    del g
+    return ms
+
+
 def cpu_cores() -> int:
     try:
         return len(os.sched_getaffinity(0))
@@ -175,6 +202,47 @@ def bench_encode(args, dev, out):
     if not args.no_cpu_baseline:
         out["x_host"] = x.view(torch.int16).cpu()
     del y, rec
+
+
+def bench_codec_shapes(args, dev):
+    """The engine's other TurboQuant shapes over the same 805 MB of bf16 input as cfg2 (seed 1, 2%
+    outliers): 8-bit D=128 (cfg1/cfg3's KV blocks, turbo_quant.py:150-154), and 4- and 8-bit D=64
+    (the CSA index keys, aether_2b/serving.py:567-577), encode and decode, GB/s of algorithmic bytes
+    (D*2 in + codes + 4 B scale per vector)."""
+    from aetherkv import PolarQuant
+    from aetherkv.synthetic import normal_with_outliers
+    import aetherkv._lib as L
+
+    lib = L.lib()
+    x = normal_with_outliers((T2, H2, D2), 1, device=dev)
+    res = {}
+    for bits, D in ((8, 128), (4, 64), (8, 64)):
+        n_vec = x.numel() // D
+        cb = D if bits == 8 else D // 2
+        pq = PolarQuant(bits)
+        codes = torch.empty((n_vec, cb), dtype=torch.int8 if bits == 8 else torch.uint8, device=dev)
+        scale = torch.empty((n_vec,), dtype=torch.float32, device=dev)
+        rec = torch.empty((n_vec, D), dtype=torch.bfloat16, device=dev)
+        diag = pq._diag(D, dev)
+        stream = L.stream_of(x)
+        xp, dp, cp, sp, rp = L.ptr(x), L.ptr(diag), L.ptr(codes), L.ptr(scale), L.ptr(rec)
+        nbytes = n_vec * (2 * D + cb + 4)
+        enc = lambda: L.check(lib.aekv_tq_encode(xp, L.BF16, n_vec, D, bits, dp, cp, sp, stream), "encode")  # noqa
+        dec = lambda: L.check(lib.aekv_tq_decode(cp, sp, n_vec, D, bits, dp, rp, L.BF16, stream), "decode")  # noqa
+        ms_e = timed(enc, args.steps, args.warmup)
+        ms_d = timed(dec, args.steps, args.warmup)
+        key = f"{bits}bit_d{D}"
+        res[key] = {"vectors": n_vec, "bytes": nbytes,
+                    "encode": {"ms": round(ms_e, 5), "GB/s": round(nbytes / ms_e / 1e6, 1),
+                               "frac": round(nbytes / ms_e / 1e6 / HBM_PEAK_GBS, 4)},
+                    "decode": {"ms": round(ms_d, 5), "GB/s": round(nbytes / ms_d / 1e6, 1),
+                               "frac": round(nbytes / ms_d / 1e6 / HBM_PEAK_GBS, 4)}}
+        log(f"codec {key}: encode {ms_e * 1e3:.1f} us ({res[key]['encode']['GB/s']:.0f} GB/s), decode "
+            f"{ms_d * 1e3:.1f} us ({res[key]['decode']['GB/s']:.0f} GB/s)")
+        del codes, scale, rec
+    del x
+    torch.cuda.empty_cache()
+    return res
 
 
 CPU_RUNS = 5  # CPU baseline: median of this many timed runs after one warm-up
@@ -329,6 +397,15 @@ def make_csa_inputs(dev, B, S, bits, seed, outliers):
     )
 
 
+def csa_step_bytes(B, S, bits, k=256, H=12, D=128, W=128, IH=4, IC=64):
+    """Algorithmic bytes of one CSA decode step: the index scan (codes + scale of every block), the
+    k selected KV rows (codes + scale), the bf16 window, q in and out, the index query and weights,
+    and the selected indices out."""
+    row_bytes = (D if bits == 8 else D // 2) + 4
+    ix_bytes = (IC if bits == 8 else IC // 2) + 4
+    return B * (S * ix_bytes + k * row_bytes + W * D * 2 + H * D * 2 * 2 + IH * IC * 4 + IH * 4 + k * 8)
+
+
 def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
     from aetherkv.decode import (attention_workspace, csa_decode_step, csa_indexer_topk_quant, decode_workspace,
                                  indexer_workspace, quant_sink_attention)
@@ -343,6 +420,7 @@ def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
     idx = torch.empty((B, k), dtype=torch.int64, device=dev)
     out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
     pq = inp["pq"]
+    step_bytes = csa_step_bytes(B, S, bits)
 
     def index_only():
         csa_indexer_topk_quant(inp["index_q"], inp["index_w"], inp["ix_codes"], inp["ix_scale"], k, quant=pq,
@@ -363,25 +441,42 @@ def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
                         workspace=ws_s, out_idx=idx, out=out)
 
     ms_eager = timed(step, args.steps, args.warmup)
-    ms = timed_graph(step, args.steps, args.warmup)
+    ms_warm = timed_graph(step, args.steps, args.warmup)
     ms_sep = timed_graph(step_separate, args.steps, args.warmup)
     ms_i = timed_graph(index_only, args.steps, args.warmup)
     ms_a = timed_graph(attn_only, args.steps, args.warmup)
-    row_bytes = (D if bits == 8 else D // 2) + 4
-    ix_bytes = (64 if bits == 8 else 32) + 4
-    step_bytes = B * (S * ix_bytes + k * row_bytes + 128 * D * 2 + H * D * 2 * 2)
+    cpu = bench_cpu_csa(inp, cpu_rows, name, bits) if cpu_rows else None
+
+    # cold: L layers' caches (layer 0 = the inputs above, layer l > 0 seeded seed + 10007 l), one step
+    # per layer in one graph, sharing one workspace and output as the engine's layer loop would
+    n_layers = max(8, -(-2 * MALL_BYTES // step_bytes) + 1)
+    layers = [inp] + [make_csa_inputs(dev, B, S, bits, seed + 10007 * l, outliers) for l in range(1, n_layers)]
+
+    def layer_step(li):
+        x = layers[li]
+        return lambda: csa_decode_step(x["q"], x["index_q"], x["index_w"], x["ix_codes"], x["ix_scale"],
+                                       x["kv_codes"], x["kv_scale"], x["win"], x["sink"], D ** -0.5, k,
+                                       kv_quant=pq, index_quant=pq, workspace=ws_s, out_idx=idx, out=out)
+
+    ms = timed_graph_layers([layer_step(li) for li in range(n_layers)], args.steps, args.warmup)
     res = {"B": B, "S": S, "bits": bits, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / ms * 1e3, 1),
-           "ms_per_step_eager": round(ms_eager, 5), "timing": f"HIP graph of {GRAPH_STEPS} steps, replayed",
+           "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes_per_step": step_bytes,
+           "timing": f"cold: {n_layers} layers' distinct caches ({n_layers * step_bytes / 2 ** 20:.0f} MiB touched "
+                     f"per pass, > 2x the 256 MiB Infinity Cache), one step per layer captured in one HIP graph "
+                     f"and replayed",
+           "warm": {"ms_per_step": round(ms_warm, 5), "tokens_per_s": round(B / ms_warm * 1e3, 1),
+                    "hbm_frac": round(step_bytes / ms_warm / 1e6 / HBM_PEAK_GBS, 4),
+                    "timing": f"one layer's inputs, HIP graph of {GRAPH_STEPS} steps replayed (caches stay warm)"},
+           "ms_per_step_eager_warm": round(ms_eager, 5),
            "step": "aekv_csa_decode_quant: score kernel + fused select/attention kernel",
-           "ms_per_step_separate_kernels": round(ms_sep, 5),
-           "separate_indexer_ms": round(ms_i, 5), "separate_attention_ms": round(ms_a, 5),
-           "bytes_per_step": step_bytes, "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    log(f"{name}: {ms * 1e3:.1f} us/step fused (graph replay; eager {ms_eager * 1e3:.1f}); separate kernels "
-        f"{ms_sep * 1e3:.1f} ({ms_i * 1e3:.1f} indexer + {ms_a * 1e3:.1f} attention) -> {res['tokens_per_s']:.0f} "
-        f"tok/s, {res['hbm_frac'] * 100:.1f}% of HBM peak")
-    if cpu_rows:
-        res["cpu_baseline"] = bench_cpu_csa(inp, cpu_rows, name, bits)
-    del inp
+           "ms_per_step_separate_kernels_warm": round(ms_sep, 5),
+           "separate_indexer_ms_warm": round(ms_i, 5), "separate_attention_ms_warm": round(ms_a, 5)}
+    log(f"{name}: cold {ms * 1e3:.1f} us/step ({n_layers} layers) -> {res['tokens_per_s']:.0f} tok/s, "
+        f"{res['hbm_frac'] * 100:.1f}% of HBM peak; warm {ms_warm * 1e3:.1f} (eager {ms_eager * 1e3:.1f}); separate "
+        f"kernels warm {ms_sep * 1e3:.1f} ({ms_i * 1e3:.1f} indexer + {ms_a * 1e3:.1f} attention)")
+    if cpu:
+        res["cpu_baseline"] = cpu
+    del inp, layers
     torch.cuda.empty_cache()
     return res
 
@@ -394,25 +489,41 @@ def bench_hca(args, dev):
     B, H, D, S, W = 32, 12, 128, 2048, 128
     log(f"cfg4: HCA decode B={B} S={S} 4-bit")
     pq = PolarQuant(4)
-    blocks = rope_interleaved(normal((B, S, D), 3, device=dev), torch.arange(S, device=dev) * 128 + 127)
-    codes, scale = pq.encode(blocks)
-    q = normal((B, 1, H, D), 4, device=dev)
-    win = normal((B, W, D), 5, device=dev)
-    sink = normal((H,), 6, dtype=torch.float32, device=dev)
     ws = attention_workspace(B, H, D, S, W, dev)
     out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
-    def step():
-        quant_sink_attention(q, codes, scale, None, win, sink, D ** -0.5, quant=pq, workspace=ws, out=out)
-
-    ms_eager = timed(step, args.steps, args.warmup)
-    ms = timed_graph(step, args.steps, args.warmup)
     flops = 2 * 2 * B * H * (S + W) * D
     step_bytes = B * (S * (D // 2 + 4) + W * D * 2 + H * D * 4)
+
+    def make_layer(seed):
+        # layer 0: seed 3 (blocks), 4 (q), 5 (window), 6 (sink); layer l > 0 the same seeds + 10007 l
+        blocks = rope_interleaved(normal((B, S, D), seed, device=dev), torch.arange(S, device=dev) * 128 + 127)
+        codes, scale = pq.encode(blocks)
+        return dict(codes=codes, scale=scale, q=normal((B, 1, H, D), seed + 1, device=dev),
+                    win=normal((B, W, D), seed + 2, device=dev),
+                    sink=normal((H,), seed + 3, dtype=torch.float32, device=dev))
+
+    def layer_step(x):
+        return lambda: quant_sink_attention(x["q"], x["codes"], x["scale"], None, x["win"], x["sink"], D ** -0.5,
+                                            quant=pq, workspace=ws, out=out)
+
+    n_layers = max(8, -(-2 * MALL_BYTES // step_bytes) + 1)
+    layers = [make_layer(3 + 10007 * l) for l in range(n_layers)]
+    step = layer_step(layers[0])
+    ms_eager = timed(step, args.steps, args.warmup)
+    ms_warm = timed_graph(step, args.steps, args.warmup)
+    ms = timed_graph_layers([layer_step(x) for x in layers], args.steps, args.warmup)
     res = {"B": B, "S": S, "bits": 4, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / ms * 1e3, 1),
-           "ms_per_step_eager": round(ms_eager, 5), "timing": f"HIP graph of {GRAPH_STEPS} steps, replayed",
+           "timing": f"cold: {n_layers} layers' distinct caches ({n_layers * step_bytes / 2 ** 20:.0f} MiB per pass), "
+                     f"one step per layer captured in one HIP graph and replayed",
            "tflops": round(flops / ms / 1e9, 3), "mfma_frac": round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 5),
-           "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    log(f"cfg4: {ms * 1e3:.1f} us/step (graph replay; eager {ms_eager * 1e3:.1f}) -> {res['tokens_per_s']:.0f} tok/s")
+           "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes_per_step": step_bytes,
+           "warm": {"ms_per_step": round(ms_warm, 5), "tokens_per_s": round(B / ms_warm * 1e3, 1),
+                    "timing": f"one layer's inputs, HIP graph of {GRAPH_STEPS} steps replayed (caches stay warm)"},
+           "ms_per_step_eager_warm": round(ms_eager, 5)}
+    log(f"cfg4: cold {ms * 1e3:.1f} us/step ({n_layers} layers) -> {res['tokens_per_s']:.0f} tok/s; warm "
+        f"{ms_warm * 1e3:.1f} (eager {ms_eager * 1e3:.1f})")
+    del layers
+    torch.cuda.empty_cache()
     return res
 
 
@@ -645,7 +756,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "encode", "csa", "hca", "prefill", "paging", "io", "sparse"],
+    ap.add_argument("--only", choices=["all", "encode", "codec", "csa", "hca", "prefill", "paging", "io", "sparse"],
                     default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -671,6 +782,8 @@ def main():
         if not args.no_cpu_baseline:
             cpu = bench_cpu_encode(res)
         torch.cuda.empty_cache()
+    if args.only in ("all", "codec"):
+        secondary["codec_shapes"] = bench_codec_shapes(args, dev)
     if args.only in ("all", "csa"):
         cpu_rows = (0, 0) if args.no_cpu_baseline else (8, 8)
         secondary["csa_decode_cfg5"] = bench_csa(args, dev, 64, 65536, 4, 4, True, "cfg5", cpu_rows[0])

@@ -24,6 +24,19 @@ from . import _lib
 from .turbo_quant import PolarQuant
 
 
+def _check_out(name: str, t: torch.Tensor, dtype: torch.dtype, numel: int, device) -> None:
+    """A caller-supplied output buffer goes to the kernels as a raw pointer: it must have the
+    dtype, element count and device the kernels write, and be contiguous."""
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.numel() != numel:
+        raise RuntimeError(f"{name} must hold {numel} elements, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    if t.device != torch.device(device):
+        raise RuntimeError(f"{name} must be on {device}, got {t.device}")
+
+
 def _scale_2d(scale: torch.Tensor, B: int, S: int) -> torch.Tensor:
     s = scale.to(torch.float32).contiguous()
     if s.numel() != B * S:
@@ -72,6 +85,8 @@ def csa_indexer_topk_quant(index_q: torch.Tensor, index_weight: torch.Tensor, ke
     L = _lib.lib()
     if out is None:
         out = torch.empty((B, k), dtype=torch.int64, device=index_q.device)
+    else:
+        _check_out("out", out, torch.int64, B * k, index_q.device)
     scores = torch.empty((B, k), dtype=torch.float32, device=index_q.device) if return_scores else None
     if workspace is None:
         workspace = indexer_workspace(B, S, k, index_q.device)
@@ -131,6 +146,8 @@ def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tens
         workspace = attention_workspace(B, H, D, n_comp, W, q.device)
     if out is None:
         out = torch.empty((B, H, D), dtype=torch.bfloat16, device=q.device)
+    else:
+        _check_out("out", out, torch.bfloat16, B * H * D, q.device)
     with torch.cuda.device(q.device):
         _lib.check(_lib.lib().aekv_quant_sink_attention(
             _lib.ptr(qc), _lib.ptr(cc), _lib.ptr(sc), _lib.ptr(s64), _lib.ptr(win), _lib.ptr(sk), _lib.ptr(diag), B, H,
@@ -203,9 +220,13 @@ def csa_decode_step(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.
     L = _lib.lib()
     if out_idx is None:
         out_idx = torch.empty((B, k), dtype=torch.int64, device=dev)
+    else:
+        _check_out("out_idx", out_idx, torch.int64, B * k, dev)
     scores = torch.empty((B, k), dtype=torch.float32, device=dev) if return_scores else None
     if out is None:
         out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
+    else:
+        _check_out("out", out, torch.bfloat16, B * H * D, dev)
     if workspace is None:
         workspace = decode_workspace(B, S, k, H, D, W, dev)
     with torch.cuda.device(dev):

@@ -7,11 +7,14 @@
 //
 // Two kernels instead of three: the wide score kernel (idx_mfma_device.h) writes every visible
 // key's order key and the 16-key slot maxima; then one workgroup per row selects the row's top-k
-// (select_row) and, in the same workgroup, attends the selected blocks and the window
-// (attend_main), reading the selection from LDS.  Fusing the two per-row stages removes a kernel
-// boundary and the global round trip of the selected indices between them, and lets the
-// attention's own loads and set-up run while the select waits on memory; both results are those
-// of the separate kernels, which the entry point falls back to outside the fused kernel's limits.
+// (select_row) and, in the same workgroup, attends the window and the selected blocks.  The window
+// does not depend on the selection: each wave requests its 16 window rows with the query in the
+// workgroup's first memory round and attends them while the select waits for its slot maxima, so
+// that after the select every wave has one group of 32 selected blocks left (k <= 256).  Fusing
+// the two per-row stages also removes a kernel boundary and the global round trip of the selected
+// indices between them; the selection is that of the separate kernels, and the attention that of
+// the separate attention kernel up to the order in which the sources are summed (the entry point
+// runs the separate kernels outside the fused kernel's limits).
 #include <mutex>
 
 #include "idx_mfma_device.h"
@@ -23,37 +26,67 @@ namespace {
 constexpr int kFusedThreads = 512;  // 8 waves: the select's 512-thread instance, the 8-wave attention body
 constexpr int kFusedCap = 1536;     // select candidates held in LDS
 constexpr int kFusedMaxK = 512;     // largest k the 512-thread select sorts outright
-constexpr int kFusedMaxW = 128;     // window rows staged in LDS
-using FusedLay = qattn::QLay<8, kFusedMaxW>;
+constexpr int kFusedMaxW = 128;     // window rows: 16 per wave
+using FusedLay = qattn::QLay<8>;
 
-// Work that does not depend on the selection is issued before it: the window rows go to LDS with
-// direct loads (global_load_lds_dwordx4, lane l -> 16 l bytes past the wave's base, the source
-// chunk chosen so that the rows land in the win_chunk layout) and the per-lane query and operand
-// constants are built, both overlapping the select's memory rounds.
 template <int KV_BITS>
 __global__ __launch_bounds__(kFusedThreads) void csa_decode_fused_kernel(idx::MfmaIdxArgs ia, qattn::QAttnMfmaArgs qa,
                                                                        int64_t* __restrict__ out_idx,
                                                                        float* __restrict__ out_score) {
+  constexpr int NW = kFusedThreads / 64;
   extern __shared__ __align__(16) unsigned char lds[];
-  unsigned char* win_lds = lds + FusedLay::win;
+  int32_t* sel_lds = reinterpret_cast<int32_t*>(lds + FusedLay::idx);
   const int b = blockIdx.x;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, c16 = lane & 15;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = static_cast<int>(qa.Wt);
-  // 4 rows (64 chunks of 16 bytes) per wave instruction
-  for (int i = wv; 4 * i < W; i += kFusedThreads / 64) {
-    const int r = 4 * i + (lane >> 4);
-    if (r < W) {
-      const uint16_t* src = qa.win + (static_cast<int64_t>(b) * qa.Wt + r) * qattn::kD + 8 * qattn::win_chunk(r, lane & 15);
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src),
-                                       (__attribute__((address_space(3))) void*)(win_lds + 1024 * i), 16, 0, 0);
-    }
+  // first memory round (with the select's count): the wave's window entries 16 wv .. 16 wv + 15 as
+  // block 0 of a group (lanes past W read entry 0 and are masked), and the query and diagonal
+  const bool has_win = 16 * wv < W;  // wave-uniform
+  const bool wok = 16 * wv + c16 < W;
+  qattn::GroupIn<KV_BITS> win_in;
+  if (has_win) {
+    qattn::SrcRef wsrc[2];
+    wsrc[0].kind = 2;
+    wsrc[0].at = wok ? 16 * wv + c16 : 0;
+    wsrc[1].kind = 0;
+    wsrc[1].at = -1;
+    qattn::group_fetch<KV_BITS>(qa, b, wsrc, nullptr, win_in);
   }
+  qattn::PrologueRaw praw;
+  qattn::prologue_loads(qa, b, praw);
   qattn::AttnFrags<KV_BITS> f;
-  qattn::attend_prologue<KV_BITS>(qa, b, f);
-  idx::select_row<kFusedThreads, kFusedCap>(ia, b, out_idx, out_score, reinterpret_cast<int32_t*>(lds + FusedLay::idx));
-  __builtin_amdgcn_s_waitcnt(0);  // the window's direct loads (vmcnt) before the barrier in attend_main
-  const qattn::RowSources rs = qattn::attend_sources<8>(qa, b, 0, nullptr);
-  qattn::attend_main<KV_BITS, 8>(qa, b, 0, lds, f, rs, win_lds);
+  qattn::AttnState st;
+  qattn::attn_state_init(st);
+  bool window_done = false;
+  auto window = [&]() {
+    qattn::prologue_build<KV_BITS>(qa, praw, f);
+    if (has_win) {
+      const bool okm[2] = {wok, false};
+      qattn::group_consume<KV_BITS>(qa, f, win_in, st, okm);
+    }
+    window_done = true;
+  };
+  const uint32_t kk = idx::select_row<kFusedThreads, kFusedCap>(ia, b, out_idx, out_score, sel_lds, window);
+  if (!window_done) window();  // a row with no visible block skips the select's memory rounds
+  __syncthreads();             // sel_lds
+  // the selected blocks, in the same state: wave w takes groups w, w + NW, ...
+  const int n_groups = static_cast<int>((kk + qattn::kGroup - 1) / qattn::kGroup);
+#pragma unroll 1
+  for (int G = wv; G < n_groups; G += NW) {
+    qattn::SrcRef src[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int si = G * qattn::kGroup + 16 * kb + c16;
+      const int32_t blk = si < static_cast<int>(kk) ? sel_lds[si] : -1;
+      src[kb].kind = blk >= 0 ? 1 : 0;
+      src[kb].at = blk;
+    }
+    qattn::GroupIn<KV_BITS, false> in;
+    qattn::group_fetch<KV_BITS, false>(qa, b, src, nullptr, in);
+    qattn::group_consume<KV_BITS, false>(qa, f, in, st);
+  }
+  qattn::attend_finish<NW>(qa, b, 0, lds, st);
 }
 
 }  // namespace

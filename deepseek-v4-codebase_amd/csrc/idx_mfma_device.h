@@ -325,7 +325,8 @@ __device__ __forceinline__ void query_loads(const MfmaIdxArgs& a, int b, QueryRa
   }
 }
 
-template <int BITS, int IC, int NRB>
+// NWV: waves in the workgroup; waves 4 and up take no heads (they only build their fragments).
+template <int BITS, int IC, int NRB, int NWV = 4>
 __device__ __forceinline__ void query_fragments(const MfmaIdxArgs& a, const QueryRaw<IC, NRB>& raw,
                                                 int8_t (*dig)[16][IC], float (*hf)[4], float (*hb)[2],
                                                 i32x4_t (&A)[NRB][IC / 64], float (&f)[NRB][4], float (&lo)[NRB],
@@ -336,6 +337,7 @@ __device__ __forceinline__ void query_fragments(const MfmaIdxArgs& a, const Quer
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
 #pragma unroll
   for (int i = 0; i < NRB; ++i) {
+    if (NWV > 4 && wv >= 4) break;  // wave-uniform
     const int h = wv + 4 * i;
     float v[EPL];
 #pragma unroll
@@ -690,10 +692,19 @@ __device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
 // 1024 / 4096 for few rows; 512 / 1536 (37 KB of LDS, 80 VGPRs: three rows per CU, where the
 // 1024-thread instance at 73 VGPRs fits one) for launches of many rows with k <= 512.
 // sel_lds (nullable): the row's output indices also go there as int32 (-1 padding), for a caller
-// that continues with them in the same workgroup.
-template <int NT, int CAP>
-__device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, int64_t* __restrict__ out_idx,
-                                           float* __restrict__ out_score, int32_t* __restrict__ sel_lds) {
+// that continues with them in the same workgroup.  during_wait: work of the caller's that needs no
+// result of the select, run once, with the first slot maxima requested and not yet used (every
+// thread of the workgroup calls it at the same point; rows with no visible block skip it).
+// Returns kk = min(k, visible count).
+struct NoHook {
+  __device__ void operator()() const {}
+};
+
+template <int NT, int CAP, typename Hook = NoHook>
+__device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b, int64_t* __restrict__ out_idx,
+                                               float* __restrict__ out_score, int32_t* __restrict__ sel_lds,
+                                               Hook&& during_wait = Hook{}) {
+  constexpr bool kHook = !std::is_same<std::decay_t<Hook>, NoHook>::value;
   constexpr int NW = NT / 64;
   __shared__ uint64_t cbuf[CAP];  // candidates: keys ck[] then indices ci[], or sort words
   __shared__ __align__(16) uint32_t h[kHistBins];
@@ -707,12 +718,19 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
   const uint32_t kk = static_cast<uint32_t>(min<int64_t>(k, nv));
   int64_t* orow = out_idx + static_cast<int64_t>(b) * k;
   float* srow = out_score ? out_score + static_cast<int64_t>(b) * k : nullptr;
-  for (int i = static_cast<int>(kk) + tid; i < k; i += NT) {
-    orow[i] = -1;
-    if (srow) srow[i] = -__builtin_inff();
-    if (sel_lds) sel_lds[i] = -1;
+  // the -1 padding past kk, written last (a store loop ahead of the loads below would make every
+  // later wait for them wait for all of the workgroup's requests)
+  auto pad = [&]() {
+    for (int i = static_cast<int>(kk) + tid; i < k; i += NT) {
+      orow[i] = -1;
+      if (srow) srow[i] = -__builtin_inff();
+      if (sel_lds) sel_lds[i] = -1;
+    }
+  };
+  if (kk == 0) {
+    pad();
+    return 0u;
   }
-  if (kk == 0) return;
   const uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.ks;
   const uint4* krow4 = reinterpret_cast<const uint4*>(krow);
   const uint32_t* mrow = a.smax + static_cast<int64_t>(b) * a.ms;
@@ -730,16 +748,24 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
   }
   uint32_t mx[kSlotPer];
   auto load_max = [&](int64_t c0) {
+    // branch-free: slots past the row read slot 0 and count as 0, so the wait counts stay exact
+    uint32_t v[kSlotPer];
 #pragma unroll
     for (int r = 0; r < kSlotPer; ++r) {
       const int64_t sl = c0 + tid + static_cast<int64_t>(r) * NT;
-      mx[r] = sl < n_slots ? mrow[sl] : 0u;
+      v[r] = mrow[sl < n_slots ? sl : 0];
     }
+#pragma unroll
+    for (int r = 0; r < kSlotPer; ++r) mx[r] = c0 + tid + static_cast<int64_t>(r) * NT < n_slots ? v[r] : 0u;
   };
   // the row's largest slot max anchors the histogram
   uint32_t mloc = 0u;
   for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
     load_max(c0);
+    if (kHook && c0 == 0) {
+      __builtin_amdgcn_sched_barrier(0);  // the maxima are requested before the caller's work
+      during_wait();
+    }
 #pragma unroll
     for (int r = 0; r < kSlotPer; ++r) mloc = mloc > mx[r] ? mloc : mx[r];  // mx is 0 past the end
   }
@@ -895,7 +921,8 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
         if (sel_lds) sel_lds[pos] = static_cast<int32_t>(w & 0xffffffffu);
       }
     }
-    return;
+    pad();
+    return kk;
   }
 
   // ---- 2. three radix levels down to the kk-th largest key T ----
@@ -1011,6 +1038,8 @@ __device__ __forceinline__ void select_row(const MfmaIdxArgs& a, const int b, in
       if (sel_lds) sel_lds[r] = static_cast<int32_t>(w & 0xffffffffu);
     }
   }
+  pad();
+  return kk;
 }
 
 // The 512-thread instance serves launches of many rows: bounded to 80 VGPRs (six waves per SIMD),

@@ -176,25 +176,35 @@ struct AttnFrags {
   bf16x8_t esel[2];
 };
 
-template <int BITS>
-__device__ __forceinline__ void attend_prologue(const QAttnMfmaArgs& a, const int64_t b, AttnFrags<BITS>& f) {
+// The prologue's loads: the diagonal at the lane's 32 dims and the query row of its head.
+struct PrologueRaw {
+  float4 dg[4][2];
+  uint2 lo[4], hi[4];
+};
+
+__device__ __forceinline__ void prologue_loads(const QAttnMfmaArgs& a, const int64_t b, PrologueRaw& r) {
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-  const int H = a.H;
   // The lane's 32 dims, for every key it holds: element j of k-step ks (bf16x8) is dim
   // 16*(2ks + (j >> 2)) + 4g + (j & 3).  Every load (the diagonal at those dims, the query row of
   // head c16) is issued before any is used: one memory round.  Lanes past the heads read head 0's
   // row and use zeros.
-  const bool has_head = c16 < H;
-  const uint16_t* qr = a.q + (b * H + (has_head ? c16 : 0)) * kD + 4 * g;
-  float4 dg[4][2];
-  uint2 lo[4], hi[4];
+  const uint16_t* qr = a.q + (b * a.H + (c16 < a.H ? c16 : 0)) * kD + 4 * g;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-    for (int hv = 0; hv < 2; ++hv) dg[ks][hv] = *reinterpret_cast<const float4*>(a.diag + 16 * (2 * ks + hv) + 4 * g);
-    lo[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks));
-    hi[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks + 1));
+    for (int hv = 0; hv < 2; ++hv) r.dg[ks][hv] = *reinterpret_cast<const float4*>(a.diag + 16 * (2 * ks + hv) + 4 * g);
+    r.lo[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks));
+    r.hi[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks + 1));
   }
+}
+
+template <int BITS>
+__device__ __forceinline__ void prologue_build(const QAttnMfmaArgs& a, const PrologueRaw& r, AttnFrags<BITS>& f) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+  const bool has_head = c16 < a.H;
+  const float4 (&dg)[4][2] = r.dg;
+  const uint2 (&lo)[4] = r.lo;
+  const uint2 (&hi)[4] = r.hi;
   // dsign: the diagonal's sign bits for the lane's dims, per packed bf16 pair (dword e of k-step ks)
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
@@ -243,252 +253,251 @@ __device__ __forceinline__ void attend_prologue(const QAttnMfmaArgs& a, const in
   }
 }
 
-// The row's attention over its sources (after attend_sources and attend_prologue).  win_lds
-// (nullable): the cache row's window entries 0 .. Wt-1 staged in LDS (win_chunk layout) instead of
-// read from global memory.  PIPE: a wave requests its next group's rows before decoding the
-// current one (the 4-wave prefill instance, whose register budget has room for them).
-template <int BITS, int NW, bool PIPE = false>
-__device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_t b, const int split,
-                                            unsigned char* lds, const AttnFrags<BITS>& f, const RowSources& rs,
-                                            const unsigned char* win_lds) {
+template <int BITS>
+__device__ __forceinline__ void attend_prologue(const QAttnMfmaArgs& a, const int64_t b, AttnFrags<BITS>& f) {
+  PrologueRaw r;
+  prologue_loads(a, b, r);
+  prologue_build<BITS>(a, r, f);
+}
+
+// ---- one 32-source group of a wave: its rows requested, then decoded and attended -------------
+// A group is two blocks of 16 keys; lane (key c16 of block kb) holds its source's row: a code row
+// (kind 1, block id blk of cache row cb), a window row (kind 2, entry wrow) or nothing (kind 0).
+// WIN: the group may hold window rows (kind 2); without, it holds code rows only.
+template <int BITS, bool WIN = true>
+struct GroupIn {
+  int kind[2];
+  uint32_t cw[2][2][BITS == 8 ? 4 : 2];
+  float sraw[2];
+  uint2 wv2[WIN ? 2 : 1][4][2];
+};
+
+// The lane's source of block kb: kind and block id (kind 1) or window entry (kind 2).
+struct SrcRef {
+  int kind;
+  int64_t at;
+};
+
+// Requests the rows of both blocks (every load issued before any is used).  win_lds (nullable):
+// the cache row's window entries staged in LDS (win_chunk layout) instead of global memory.
+template <int BITS, bool WIN = true>
+__device__ __forceinline__ void group_fetch(const QAttnMfmaArgs& a, const int64_t cb, const SrcRef (&src)[2],
+                                            const unsigned char* win_lds, GroupIn<BITS, WIN>& in) {
+  constexpr int RB = BITS == 8 ? kD : kD / 2;   // code bytes per row
+  constexpr int HB = RB / 2;                    // code bytes per 64-code half
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    in.kind[kb] = src[kb].kind;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int e = 0; e < (BITS == 8 ? 4 : 2); ++e) in.cw[kb][hh][e] = 0u;
+    in.sraw[kb] = 0.0f;
+    if (src[kb].kind == 1) {
+      const int64_t blk = src[kb].at;
+      const uint8_t* row = a.codes + (cb * a.S + blk) * RB;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        if constexpr (BITS == 8) {
+          const uint4 v = *reinterpret_cast<const uint4*>(row + HB * hh + 16 * g);
+          in.cw[kb][hh][0] = v.x;
+          in.cw[kb][hh][1] = v.y;
+          in.cw[kb][hh][2] = v.z;
+          in.cw[kb][hh][3] = v.w;
+        } else {
+          const uint2 v = *reinterpret_cast<const uint2*>(row + HB * hh + 8 * g);
+          in.cw[kb][hh][0] = v.x;
+          in.cw[kb][hh][1] = v.y;
+        }
+      }
+      in.sraw[kb] = a.scale[cb * a.S + blk];
+    }
+    if (WIN && src[kb].kind == 2) {
+      const int64_t wrow = src[kb].at;
+      if (win_lds) {
+        // dims 32ks + 4g (+16): chunk 4ks + g/2 (+2), bytes 8(g & 1) .. +8 of it
+        const int r = static_cast<int>(wrow);
+        const unsigned char* rp = win_lds + 2 * kD * r + 8 * (g & 1);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          in.wv2[WIN ? kb : 0][ks][0] = *reinterpret_cast<const uint2*>(rp + 16 * win_chunk(r, 4 * ks + (g >> 1)));
+          in.wv2[WIN ? kb : 0][ks][1] = *reinterpret_cast<const uint2*>(rp + 16 * win_chunk(r, 4 * ks + 2 + (g >> 1)));
+        }
+      } else {
+        const uint16_t* wr = a.win + (cb * a.Wt + wrow) * kD + 4 * g;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          in.wv2[WIN ? kb : 0][ks][0] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks));
+          in.wv2[WIN ? kb : 0][ks][1] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks + 1));
+        }
+      }
+    }
+  }
+}
+
+// Online-softmax state and output of head c16 (replicated over the four lane groups).
+struct AttnState {
+  float m_run, l_run;
+  f32x4_t O[8];
+};
+
+__device__ __forceinline__ void attn_state_init(AttnState& s) {
+  s.m_run = kNegInf;
+  s.l_run = 0.0f;
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) s.O[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+// Decodes the group's rows and folds its 32 sources into the state.
+// ok_mask (per block kb, nullable): a per-lane validity on top of the row kinds, e.g. whether the
+// lane's candidate made the selection.
+template <int BITS, bool WIN = true>
+__device__ __forceinline__ void group_consume(const QAttnMfmaArgs& a, const AttnFrags<BITS>& f,
+                                              const GroupIn<BITS, WIN>& in, AttnState& s,
+                                              const bool* ok_mask = nullptr) {
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  const uint32_t (&dsign)[4][4] = f.dsign;
+  const bf16x8_t (&qb)[4] = f.qb;
+  const i32x4_t (&hA)[4] = f.hA;
+  const bf16x8_t (&esel)[2] = f.esel;
+  const int (&kind)[2] = in.kind;
+  const auto& cw = in.cw;
+  const float (&sraw)[2] = in.sraw;
+  const auto& wv2 = in.wv2;
+  const float kscale_unit = (BITS == 4 ? 1.0f / 16.0f : 1.0f) * a.wscale;
+  bf16x8_t kf[2][4];
+  bool okk[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    okk[kb] = kind[kb] != 0 && (!ok_mask || ok_mask[kb]);
+    const float fk = sraw[kb] * kscale_unit;
+    // y = H64 codes per half (all lanes take part; lanes without a code row supply zeros)
+    i32x4_t P[2][4];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      i32x4_t Bop;
+      if constexpr (BITS == 8) {
+        Bop = i32x4_t{static_cast<int>(cw[kb][hh][0]), static_cast<int>(cw[kb][hh][1]),
+                      static_cast<int>(cw[kb][hh][2]), static_cast<int>(cw[kb][hh][3])};
+      } else {
+        const uint32_t x = cw[kb][hh][0], y = cw[kb][hh][1];
+        Bop = i32x4_t{static_cast<int>((x << 4) & 0xF0F0F0F0u), static_cast<int>(x & 0xF0F0F0F0u),
+                      static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
+      }
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4)
+        P[hh][a4] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hA[a4], Bop, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+    }
+    // P[hh][a4][i] = (H64 codes_half_hh)[16*a4 + 4g + i]; dims 16*blk + 4g + i of the full
+    // transform: blk < 4 -> P[0] + P[1], blk >= 4 -> P[0] - P[1]
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      uint32_t w4[4];
+      if (WIN && kind[kb] == 2) {
+        constexpr int kw = 0;  // (wv2 has one block without window rows)
+        const int wb = WIN ? kb : kw;
+        w4[0] = wv2[wb][ks][0].x ^ dsign[ks][0];
+        w4[1] = wv2[wb][ks][0].y ^ dsign[ks][1];
+        w4[2] = wv2[wb][ks][1].x ^ dsign[ks][2];
+        w4[3] = wv2[wb][ks][1].y ^ dsign[ks][3];
+      } else {
+        float v[8];
+#pragma unroll
+        for (int hv = 0; hv < 2; ++hv) {
+          const int blk8 = 2 * ks + hv;
+          const int a4 = blk8 & 3;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int y = blk8 < 4 ? P[0][a4][i] + P[1][a4][i] : P[0][a4][i] - P[1][a4][i];
+            v[4 * hv + i] = static_cast<float>(y) * fk;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w4[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+      }
+      kf[kb][ks] = __builtin_bit_cast(bf16x8_t, make_uint4(w4[0], w4[1], w4[2], w4[3]));
+    }
+  }
+
+  // st[kb][i] = S[head c16][key 16kb + 4g + i of the group]
+  f32x4_t st[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    st[kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb][ks], qb[ks], st[kb], 0, 0, 0);
+  }
+  float pr[2][4];
+  {
+    float lg[2][4];
+    float tm = kNegInf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      // okk[kb] belongs to key c16, so bit 4g+i of its ballot is the validity of row 4g+i
+      const uint64_t okm = __builtin_amdgcn_ballot_w64(okk[kb]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = (okm >> (4 * g + i)) & 1u;
+        lg[kb][i] = ok ? st[kb][i] * a.sm_scale : kNegInf;
+        tm = fmaxf(tm, lg[kb][i]);
+      }
+    }
+    tm = fmaxf(tm, xor_lane<16>(tm));
+    tm = fmaxf(tm, xor_lane<32>(tm));
+    const float mnew = fmaxf(s.m_run, tm);
+    const float corr = s.m_run == kNegInf ? 0.0f : __expf(s.m_run - mnew);
+    float ps = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[kb][i] = lg[kb][i] == kNegInf ? 0.0f : __expf(lg[kb][i] - mnew);
+        ps += pr[kb][i];
+      }
+    ps += xor_lane<16>(ps);
+    ps += xor_lane<32>(ps);
+    s.l_run = s.l_run * corr + ps;
+    s.m_run = mnew;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) s.O[nb] *= corr;
+  }
+  // B = P^T: lane (head c16), element 4kb + i <-> key 16kb + 4g + i
+  const bf16x8_t pb = __builtin_bit_cast(
+      bf16x8_t, make_uint4(pack_bf16x2(pr[0][0], pr[0][1]), pack_bf16x2(pr[0][2], pr[0][3]),
+                           pack_bf16x2(pr[1][0], pr[1][1]), pack_bf16x2(pr[1][2], pr[1][3])));
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    // V columns 16nb .. 16nb+15 of the 32 keys: K fragments times a 0/1 selector (exact)
+    const f32x4_t v0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[0][nb >> 1], esel[nb & 1], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    const f32x4_t v1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[1][nb >> 1], esel[nb & 1], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    // A = V^T: lane (dim 16nb + c16), element 4kb + i <-> key 16kb + 4g + i (same order as pb)
+    const bf16x8_t va = __builtin_bit_cast(
+        bf16x8_t, make_uint4(pack_bf16x2(v0[0], v0[1]), pack_bf16x2(v0[2], v0[3]), pack_bf16x2(v1[0], v1[1]),
+                             pack_bf16x2(v1[2], v1[3])));
+    // O^T[nb][i] = O[head c16][dim 16nb + 4g + i] (times diag, removed at the end)
+    s.O[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, s.O[nb], 0, 0, 0);
+  }
+}
+
+// Merges the NW waves' states (and the sink, unless this is one split of several) and writes the
+// row's output, or its split result (max, sum, O) for the combine.
+template <int NW>
+__device__ __forceinline__ void attend_finish(const QAttnMfmaArgs& a, const int64_t b, const int split,
+                                              unsigned char* lds, const AttnState& s) {
   constexpr int kW = NW, kT = 64 * NW;
   using L = QLay<NW>;
   float* Ob = reinterpret_cast<float*>(lds + L::ob);    // [wave][head][kObStride]
   float* stat = reinterpret_cast<float*>(lds + L::st);  // [wave][head][m, l]
   float* inv = reinterpret_cast<float*>(lds + L::inv);  // [head]
-  const int32_t* sidx = reinterpret_cast<const int32_t*>(lds + L::idx);
-  constexpr int RB = BITS == 8 ? kD : kD / 2;   // code bytes per row
-  constexpr int HB = RB / 2;                    // code bytes per 64-code half
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4, c16 = lane & 15;
   const int H = a.H;
-  const int64_t cb = rs.cb, n_comp = rs.n_comp, w0 = rs.w0, src0 = rs.src0, src1 = rs.src1;
-  const uint32_t (&dsign)[4][4] = f.dsign;
-  const bf16x8_t (&qb)[4] = f.qb;
-  const i32x4_t (&hA)[4] = f.hA;
-  const bf16x8_t (&esel)[2] = f.esel;
-  __syncthreads();  // sidx
-
-  // softmax state and output of head c16 (replicated over the four lane groups)
-  float m_run = kNegInf, l_run = 0.0f;
-  f32x4_t O[8];
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const float kscale_unit = (BITS == 4 ? 1.0f / 16.0f : 1.0f) * a.wscale;
-
-  const int n_groups = src1 > src0 ? static_cast<int>((src1 - src0 + kGroup - 1) / kGroup) : 0;
-  // group G's sources (32 per group): both blocks' rows are requested before either is decoded
-  struct GroupIn {
-    int kind[2];  // 0 empty, 1 code row, 2 window row
-    uint32_t cw[2][2][BITS == 8 ? 4 : 2];
-    float sraw[2];
-    uint2 wv2[2][4][2];
-  };
-  auto fetch = [&](const int G, GroupIn& in) {
-    int (&kind)[2] = in.kind;
-    auto& cw = in.cw;
-    float (&sraw)[2] = in.sraw;
-    auto& wv2 = in.wv2;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      // lane (key c16 of block kb): its source, code bytes (two halves) or window dims
-      const int64_t si = src0 + static_cast<int64_t>(G) * kGroup + 16 * kb + c16;
-      kind[kb] = 0;
-      int64_t blk = -1;
-      if (si < n_comp) {
-        blk = a.sel ? sidx[si - src0] : si;
-        kind[kb] = blk >= 0 ? 1 : 0;
-      } else if (si < src1) {
-        kind[kb] = 2;
-      }
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int e = 0; e < (BITS == 8 ? 4 : 2); ++e) cw[kb][hh][e] = 0u;
-      sraw[kb] = 0.0f;
-      if (kind[kb] == 1) {
-        const uint8_t* row = a.codes + (cb * a.S + blk) * RB;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          if constexpr (BITS == 8) {
-            const uint4 v = *reinterpret_cast<const uint4*>(row + HB * hh + 16 * g);
-            cw[kb][hh][0] = v.x;
-            cw[kb][hh][1] = v.y;
-            cw[kb][hh][2] = v.z;
-            cw[kb][hh][3] = v.w;
-          } else {
-            const uint2 v = *reinterpret_cast<const uint2*>(row + HB * hh + 8 * g);
-            cw[kb][hh][0] = v.x;
-            cw[kb][hh][1] = v.y;
-          }
-        }
-        sraw[kb] = a.scale[cb * a.S + blk];
-      }
-      if (kind[kb] == 2) {
-        const int64_t wrow = w0 + (si - n_comp);
-        if (win_lds) {
-          // dims 32ks + 4g (+16): chunk 4ks + g/2 (+2), bytes 8(g & 1) .. +8 of it
-          const int r = static_cast<int>(wrow);
-          const unsigned char* rp = win_lds + 2 * kD * r + 8 * (g & 1);
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) {
-            wv2[kb][ks][0] = *reinterpret_cast<const uint2*>(rp + 16 * win_chunk(r, 4 * ks + (g >> 1)));
-            wv2[kb][ks][1] = *reinterpret_cast<const uint2*>(rp + 16 * win_chunk(r, 4 * ks + 2 + (g >> 1)));
-          }
-        } else {
-          const uint16_t* wr = a.win + (cb * a.Wt + wrow) * kD + 4 * g;
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) {
-            wv2[kb][ks][0] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks));
-            wv2[kb][ks][1] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks + 1));
-          }
-        }
-      }
-    }
-
-  };
-  auto consume = [&](const int G, const GroupIn& in) {
-    const int (&kind)[2] = in.kind;
-    const auto& cw = in.cw;
-    const float (&sraw)[2] = in.sraw;
-    const auto& wv2 = in.wv2;
-    bf16x8_t kf[2][4];
-    bool okk[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      okk[kb] = kind[kb] != 0;
-      const float fk = sraw[kb] * kscale_unit;
-      // y = H64 codes per half (all lanes take part; lanes without a code row supply zeros)
-      i32x4_t P[2][4];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        i32x4_t Bop;
-        if constexpr (BITS == 8) {
-          Bop = i32x4_t{static_cast<int>(cw[kb][hh][0]), static_cast<int>(cw[kb][hh][1]),
-                        static_cast<int>(cw[kb][hh][2]), static_cast<int>(cw[kb][hh][3])};
-        } else {
-          const uint32_t x = cw[kb][hh][0], y = cw[kb][hh][1];
-          Bop = i32x4_t{static_cast<int>((x << 4) & 0xF0F0F0F0u), static_cast<int>(x & 0xF0F0F0F0u),
-                        static_cast<int>((y << 4) & 0xF0F0F0F0u), static_cast<int>(y & 0xF0F0F0F0u)};
-        }
-#pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4)
-          P[hh][a4] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hA[a4], Bop, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
-      }
-      // P[hh][a4][i] = (H64 codes_half_hh)[16*a4 + 4g + i]; dims 16*blk + 4g + i of the full
-      // transform: blk < 4 -> P[0] + P[1], blk >= 4 -> P[0] - P[1]
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        uint32_t w4[4];
-        if (kind[kb] == 2) {
-          w4[0] = wv2[kb][ks][0].x ^ dsign[ks][0];
-          w4[1] = wv2[kb][ks][0].y ^ dsign[ks][1];
-          w4[2] = wv2[kb][ks][1].x ^ dsign[ks][2];
-          w4[3] = wv2[kb][ks][1].y ^ dsign[ks][3];
-        } else {
-          float v[8];
-#pragma unroll
-          for (int hv = 0; hv < 2; ++hv) {
-            const int blk8 = 2 * ks + hv;
-            const int a4 = blk8 & 3;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int y = blk8 < 4 ? P[0][a4][i] + P[1][a4][i] : P[0][a4][i] - P[1][a4][i];
-              v[4 * hv + i] = static_cast<float>(y) * fk;
-            }
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) w4[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-        }
-        kf[kb][ks] = __builtin_bit_cast(bf16x8_t, make_uint4(w4[0], w4[1], w4[2], w4[3]));
-      }
-    }
-
-    // st[kb][i] = S[head c16][key 16kb + 4g + i of the group]
-    f32x4_t st[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      st[kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb][ks], qb[ks], st[kb], 0, 0, 0);
-    }
-    float pr[2][4];
-    {
-      float lg[2][4];
-      float tm = kNegInf;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        // okk[kb] belongs to key c16, so bit 4g+i of its ballot is the validity of row 4g+i
-        const uint64_t okm = __builtin_amdgcn_ballot_w64(okk[kb]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const bool ok = (okm >> (4 * g + i)) & 1u;
-          lg[kb][i] = ok ? st[kb][i] * a.sm_scale : kNegInf;
-          tm = fmaxf(tm, lg[kb][i]);
-        }
-      }
-      tm = fmaxf(tm, xor_lane<16>(tm));
-      tm = fmaxf(tm, xor_lane<32>(tm));
-      const float mnew = fmaxf(m_run, tm);
-      const float corr = m_run == kNegInf ? 0.0f : __expf(m_run - mnew);
-      float ps = 0.0f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pr[kb][i] = lg[kb][i] == kNegInf ? 0.0f : __expf(lg[kb][i] - mnew);
-          ps += pr[kb][i];
-        }
-      ps += xor_lane<16>(ps);
-      ps += xor_lane<32>(ps);
-      l_run = l_run * corr + ps;
-      m_run = mnew;
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) O[nb] *= corr;
-    }
-    // B = P^T: lane (head c16), element 4kb + i <-> key 16kb + 4g + i
-    const bf16x8_t pb = __builtin_bit_cast(
-        bf16x8_t, make_uint4(pack_bf16x2(pr[0][0], pr[0][1]), pack_bf16x2(pr[0][2], pr[0][3]),
-                             pack_bf16x2(pr[1][0], pr[1][1]), pack_bf16x2(pr[1][2], pr[1][3])));
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      // V columns 16nb .. 16nb+15 of the 32 keys: K fragments times a 0/1 selector (exact)
-      const f32x4_t v0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[0][nb >> 1], esel[nb & 1], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-      const f32x4_t v1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[1][nb >> 1], esel[nb & 1], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-      // A = V^T: lane (dim 16nb + c16), element 4kb + i <-> key 16kb + 4g + i (same order as pb)
-      const bf16x8_t va = __builtin_bit_cast(
-          bf16x8_t, make_uint4(pack_bf16x2(v0[0], v0[1]), pack_bf16x2(v0[2], v0[3]), pack_bf16x2(v1[0], v1[1]),
-                               pack_bf16x2(v1[2], v1[3])));
-      // O^T[nb][i] = O[head c16][dim 16nb + 4g + i] (times diag, removed at the end)
-      O[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, O[nb], 0, 0, 0);
-    }
-  };
-  if constexpr (PIPE) {
-    // the next group's rows are requested before this group is decoded
-    GroupIn cur, nxt;
-    if (wv < n_groups) fetch(wv, cur);
-#pragma unroll 1
-    for (int G = wv; G < n_groups; G += kW) {
-      const bool more = G + kW < n_groups;  // wave-uniform
-      if (more) fetch(G + kW, nxt);
-      consume(G, cur);
-      if (more) cur = nxt;
-    }
-  } else {
-#pragma unroll 1
-    for (int G = wv; G < n_groups; G += kW) {
-      GroupIn in;
-      fetch(G, in);
-      consume(G, in);
-    }
-  }
-
-  // ---- merge the waves (and the sink, unless this is one split of several) ----
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb)
-    *reinterpret_cast<f32x4_t*>(Ob + (wv * 16 + c16) * kObStride + 16 * nb + 4 * g) = O[nb];
+    *reinterpret_cast<f32x4_t*>(Ob + (wv * 16 + c16) * kObStride + 16 * nb + 4 * g) = s.O[nb];
   if (g == 0) {
-    stat[(wv * 16 + c16) * 2] = m_run;
-    stat[(wv * 16 + c16) * 2 + 1] = l_run;
+    stat[(wv * 16 + c16) * 2] = s.m_run;
+    stat[(wv * 16 + c16) * 2 + 1] = s.l_run;
   }
   __syncthreads();
   // per head (one thread each): M = max(sink, wave maxima), the waves' factors e^{m_w - M}, and
@@ -498,20 +507,20 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
     float M = a.n_split == 1 ? a.sink[h] : kNegInf;
 #pragma unroll
     for (int w = 0; w < kW; ++w) M = fmaxf(M, stat[(w * 16 + h) * 2]);
-    float L = a.n_split == 1 ? __expf(a.sink[h] - M) : 0.0f;
+    float Lsum = a.n_split == 1 ? __expf(a.sink[h] - M) : 0.0f;
 #pragma unroll
     for (int w = 0; w < kW; ++w) {
       const float mw = stat[(w * 16 + h) * 2];
       const float f = mw == kNegInf ? 0.0f : __expf(mw - M);
-      L = fmaf(f, stat[(w * 16 + h) * 2 + 1], L);
+      Lsum = fmaf(f, stat[(w * 16 + h) * 2 + 1], Lsum);
       stat[(w * 16 + h) * 2] = f;
     }
     if (a.n_split == 1) {
-      inv[h] = 1.0f / L;
+      inv[h] = 1.0f / Lsum;
     } else {
       float* dst = a.part + ((b * a.n_split + split) * H + h) * kPartStride;
       dst[0] = M;
-      dst[1] = L;
+      dst[1] = Lsum;
     }
   }
   __syncthreads();
@@ -535,6 +544,67 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
       *reinterpret_cast<f32x4_t*>(a.part + ((b * a.n_split + split) * H + h) * kPartStride + 4 + d4) = acc;
     }
   }
+}
+
+// The row's attention over its sources (after attend_sources and attend_prologue).  win_lds
+// (nullable): the cache row's window entries 0 .. Wt-1 staged in LDS (win_chunk layout) instead of
+// read from global memory.  PIPE: a wave requests its next group's rows before decoding the
+// current one (the 4-wave prefill instance, whose register budget has room for them).
+template <int BITS, int NW, bool PIPE = false>
+__device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_t b, const int split,
+                                            unsigned char* lds, const AttnFrags<BITS>& f, const RowSources& rs,
+                                            const unsigned char* win_lds) {
+  constexpr int kW = NW;
+  using L = QLay<NW>;
+  const int32_t* sidx = reinterpret_cast<const int32_t*>(lds + L::idx);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c16 = lane & 15;
+  const int64_t cb = rs.cb, n_comp = rs.n_comp, w0 = rs.w0, src0 = rs.src0, src1 = rs.src1;
+  __syncthreads();  // sidx
+
+  AttnState s;
+  attn_state_init(s);
+  const int n_groups = src1 > src0 ? static_cast<int>((src1 - src0 + kGroup - 1) / kGroup) : 0;
+  // group G's sources (32 per group): both blocks' rows are requested before either is decoded
+  auto fetch = [&](const int G, GroupIn<BITS>& in) {
+    SrcRef src[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      // lane (key c16 of block kb): its source, code bytes (two halves) or window dims
+      const int64_t si = src0 + static_cast<int64_t>(G) * kGroup + 16 * kb + c16;
+      src[kb].kind = 0;
+      src[kb].at = -1;
+      if (si < n_comp) {
+        const int64_t blk = a.sel ? sidx[si - src0] : si;
+        src[kb].kind = blk >= 0 ? 1 : 0;
+        src[kb].at = blk;
+      } else if (si < src1) {
+        src[kb].kind = 2;
+        src[kb].at = w0 + (si - n_comp);
+      }
+    }
+    group_fetch<BITS>(a, cb, src, win_lds, in);
+  };
+  if constexpr (PIPE) {
+    // the next group's rows are requested before this group is decoded
+    GroupIn<BITS> cur, nxt;
+    if (wv < n_groups) fetch(wv, cur);
+#pragma unroll 1
+    for (int G = wv; G < n_groups; G += kW) {
+      const bool more = G + kW < n_groups;  // wave-uniform
+      if (more) fetch(G + kW, nxt);
+      group_consume<BITS>(a, f, cur, s);
+      if (more) cur = nxt;
+    }
+  } else {
+#pragma unroll 1
+    for (int G = wv; G < n_groups; G += kW) {
+      GroupIn<BITS> in;
+      fetch(G, in);
+      group_consume<BITS>(a, f, in, s);
+    }
+  }
+  // ---- merge the waves (and the sink, unless this is one split of several) ----
+  attend_finish<NW>(a, b, split, lds, s);
 }
 
 

@@ -272,13 +272,6 @@ int aekv_emit_block(const void* c, const void* z, const void* z_bias, int64_t B,
  * normalised with norm_weight[d] bf16 and eps (NULL: none); out [rows, heads, d] bf16 (may alias
  * x).  Rounding points as the reference's bf16 torch ops (bf16 cos/sin and RoPE terms, fp32
  * RMSNorm).  d = 128 or 256. */
-/* Measurement utility, no counterpart in the reference: moves the bytes of a 4-bit D = 128 bf16
- * encode of n_vec vectors (x [n_vec, 128] bf16 in; codes [n_vec, 64] bytes and scale [n_vec] out)
- * with the encode kernel's access pattern and non-temporal stores but no transform (the outputs are
- * xor folds of the inputs).  bench.py times it beside the encode as the practical streaming
- * ceiling of that traffic.  x and codes 16-byte aligned. */
-int aekv_stream_probe(const void* x, int64_t n_vec, void* codes, float* scale, void* stream);
-
 int aekv_rope_rmsnorm(const void* x, int64_t rows, int32_t heads, int32_t d, const int64_t* positions,
                       int32_t pos_sign, const float* inv_freq, int32_t rope_dim, const void* norm_weight,
                       float eps, void* out, void* stream);
@@ -294,6 +287,14 @@ int aekv_tiled_prefill_attention_ws(const void* q, const void* kv, const void* s
                                     int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t D, int64_t S,
                                     float softmax_scale, int32_t tile_size, void* ws, size_t ws_bytes, void* out,
                                     void* stream);
+
+/* ---- measurement utilities (no counterpart in the reference; not used by any entry above) ---- */
+/* Measurement utility, no counterpart in the reference: moves the bytes of a 4-bit D = 128 bf16
+ * encode of n_vec vectors (x [n_vec, 128] bf16 in; codes [n_vec, 64] bytes and scale [n_vec] out)
+ * with the encode kernel's access pattern and non-temporal stores but no transform (the outputs are
+ * xor folds of the inputs).  bench.py times it beside the encode as the practical streaming
+ * ceiling of that traffic.  x and codes 16-byte aligned. */
+int aekv_stream_probe(const void* x, int64_t n_vec, void* codes, float* scale, void* stream);
 
 #ifdef __cplusplus
 }

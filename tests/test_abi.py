@@ -209,3 +209,20 @@ def test_loader_returns_kernel_namespace():
     ext = aetherkv.load_aether_cuda_kernels()
     for n in ("sparse_sink_attention", "tiled_prefill_attention", "csa_indexer_topk", "hca_compress"):
         assert callable(getattr(ext, n))
+
+
+def test_caller_output_buffers_are_checked_before_the_kernels():
+    # out= / out_idx= buffers reach the kernels as raw pointers, so a wrong dtype, size or layout
+    # must be refused on the host (the kernels would write B*k int64 / B*H*D bf16 past them)
+    from aetherkv.decode import _check_out
+
+    dev = torch.device("cpu")
+    _check_out("out_idx", torch.empty(4, 8, dtype=torch.int64), torch.int64, 32, dev)  # accepted
+    with pytest.raises(RuntimeError, match="out_idx must be torch.int64"):
+        _check_out("out_idx", torch.empty(4, 8, dtype=torch.int32), torch.int64, 32, dev)
+    with pytest.raises(RuntimeError, match="must hold 32 elements"):
+        _check_out("out_idx", torch.empty(4, 7, dtype=torch.int64), torch.int64, 32, dev)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        _check_out("out", torch.empty(8, 4, dtype=torch.bfloat16).t(), torch.bfloat16, 32, dev)
+    with pytest.raises(RuntimeError, match="must be on"):
+        _check_out("out", torch.empty(32, dtype=torch.bfloat16), torch.bfloat16, 32, torch.device("cuda:0"))

@@ -3,9 +3,10 @@
 Where its fused kernel applies, the selection and the attention of a row run in one workgroup; the
 results must be those of the two separate entry points (aekv_csa_indexer_topk_quant, then
 aekv_quant_sink_attention over its selection): the selection and its scores bit for bit, and the
-attention bit for bit where the separate kernel runs the row in one piece (at most 512 sources),
-within the attention tolerance of it otherwise.  Outside the fused kernel's limits the entry point
-runs the two separate entry points itself.  The oracle checks of the same step are in
+attention within the attention tolerance (the fused kernel attends the window first, while the
+select runs, so its sources are summed in another order), and within the tolerance of the oracle.
+Outside the fused kernel's limits the entry point runs the two separate entry points itself, with
+identical results.  The oracle checks of the same step are in
 test_gpu_attention.py (cfg3, cfg5) and test_gpu_cache.py.
 """
 from __future__ import annotations
@@ -44,6 +45,8 @@ def _inputs(dev, B, S, H, IH, IC, W, kv_bits, ix_bits, seed, outliers=False):
     (4, 3000, 16, 4, 64, 0, 64, 8, 4, "raw", [3000, 70, 64, 2]),                # no window, mixed widths
     (3, 4000, 1, 8, 128, 37, 100, 4, 8, "relu_w", None),                        # one head, IC 128, 8 index heads
     (2, 20000, 12, 16, 64, 128, 384, 4, 4, "softplus", None),                   # 16 index heads, 512 sources
+    (3, 9000, 12, 4, 64, 5, 256, 8, 8, "softplus", [9000, 0, 300]),             # window of 5, an empty row
+    (2, 70000, 12, 4, 64, 127, 512, 4, 4, "softplus", None),                    # 16 selected groups, W = 127
 ])
 def test_decode_step_equals_separate_entry_points(dev, B, S, H, IH, IC, W, k, kv_bits, ix_bits, mode, valid):
     x = _inputs(dev, B, S, H, IH, IC, W, kv_bits, ix_bits, 200 + S % 97, outliers=kv_bits == 4)
@@ -59,10 +62,7 @@ def test_decode_step_equals_separate_entry_points(dev, B, S, H, IH, IC, W, k, kv
     torch.cuda.synchronize()
     assert torch.equal(idx, idx1)
     assert torch.equal(sc, sc1)
-    if k + W <= 512:
-        assert torch.equal(out, out1)
-    else:
-        np.testing.assert_allclose(to_np_f32(out), to_np_f32(out1), rtol=1e-2, atol=2e-3)
+    np.testing.assert_allclose(to_np_f32(out), to_np_f32(out1), rtol=1e-2, atol=2e-3)
     # and the attention against the oracle on the returned selection
     want = O.quant_attention(to_np_f32(x["q"]).reshape(B, H, 128), x["kv_codes"].cpu().numpy(),
                              x["kv_scale"].cpu().numpy(), idx.cpu().numpy(),
@@ -108,7 +108,7 @@ def test_decode_step_exact_ties(dev, ix_bits, n_special, S):
     out1 = quant_sink_attention(q, kv_codes, kv_scale, idx1, win, sink, sm, quant=kvq)
     torch.cuda.synchronize()
     assert torch.equal(idx, idx1) and torch.equal(sc, sc1)
-    assert torch.equal(out, out1)
+    np.testing.assert_allclose(to_np_f32(out), to_np_f32(out1), rtol=1e-2, atol=2e-3)
 
 
 @pytest.mark.parametrize("k,W", [(600, 128), (512, 600)])
