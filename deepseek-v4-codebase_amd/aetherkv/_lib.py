@@ -112,6 +112,26 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+_hot: dict = {}
+
+
+def hot(name: str):
+    """The entry point `name` for calls made once per token: the CPython fast-call function of
+    aetherkv._fastcall when that module is built (same arguments as plain ints / floats / None),
+    else the ctypes function.  The library is loaded through ctypes first, so both use one copy."""
+    fn = _hot.get(name)
+    if fn is None:
+        L = lib()
+        try:
+            from . import _fastcall  # noqa: WPS433 (built next to libaetherkv.so)
+
+            fn = getattr(_fastcall, name)
+        except (ImportError, AttributeError):
+            fn = getattr(L, name)
+        _hot[name] = fn
+    return fn
+
+
 def check(rc: int, what: str) -> None:
     if rc == OK:
         return
@@ -127,6 +147,54 @@ def ptr(t: Optional[torch.Tensor]):
 
 def stream_of(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def raw_stream(device: torch.device) -> int:
+    """The current HIP stream of `device` as an integer handle (no Stream object is built)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class _Nothing:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NOTHING = _Nothing()
+
+
+def on_device(device: torch.device):
+    """Context making `device` current: nothing to do when it already is (the common case)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _NOTHING
+    return torch.cuda.device(device)
+
+
+# Split workspaces of the drop-in attention calls, one per (device, stream): calls on one stream run
+# in order, so each reuses the previous call's buffer.  Not grown while a graph is being captured
+# (the buffer would come from the graph's private pool): such calls get a buffer of their own.
+_ws_cache: dict = {}
+
+
+def workspace(nbytes: int, device: torch.device, stream: int) -> Optional[torch.Tensor]:
+    if nbytes <= 0:
+        return None
+    key = (device.index, stream)
+    buf = _ws_cache.get(key)
+    if buf is not None and buf.numel() >= nbytes:
+        return buf
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    buf = torch.empty(max(nbytes, 2 * buf.numel() if buf is not None else 0), dtype=torch.uint8, device=device)
+    _ws_cache[key] = buf
+    return buf
 
 
 def require_device(name: str, *tensors: Optional[torch.Tensor]) -> None:

@@ -10,6 +10,10 @@ Flags that matter for parity:
   -mllvm -amdgpu-mfma-vgpr-form                  matrix-instruction results in ordinary VGPRs: otherwise
                                                  the compiler keeps some accumulators in AGPRs and copies
                                                  every result to VGPRs for the VALU that consumes it
+
+Beside it, gcc builds ``aetherkv/_fastcall*.so`` from ``aetherkv/_fastcall.c``: CPython fast-call
+functions over the same C ABI for the entry points called once per token (linked against
+libaetherkv.so through $ORIGIN, so both share one loaded library).
 """
 from __future__ import annotations
 
@@ -17,6 +21,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -70,14 +75,32 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     with ThreadPoolExecutor(max_workers=min(jobs, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libaetherkv.so", *map(str, objs), "-o",
+           str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    build_fastcall()
     if verbose:
         print(f"built {LIB}", file=sys.stderr)
     return LIB
+
+
+FASTCALL_SRC = PKG / "_fastcall.c"
+FASTCALL_LIB = PKG / ("_fastcall" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+
+
+def build_fastcall() -> Path:
+    """gcc the CPython fast-call module over libaetherkv.so (next to it)."""
+    tmp = FASTCALL_LIB.with_name(FASTCALL_LIB.name + ".tmp")
+    cmd = ["gcc", "-shared", "-fPIC", "-O2", "-Wall", f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}",
+           str(FASTCALL_SRC), f"-L{PKG}", "-laetherkv", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"fast-call module build failed:\n{res.stderr}")
+    os.replace(tmp, FASTCALL_LIB)
+    return FASTCALL_LIB
 
 
 if __name__ == "__main__":

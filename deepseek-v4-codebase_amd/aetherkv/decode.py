@@ -37,6 +37,11 @@ def _check_out(name: str, t: torch.Tensor, dtype: torch.dtype, numel: int, devic
         raise RuntimeError(f"{name} must be on {device}, got {t.device}")
 
 
+def _iptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    """Device address as a plain int (None stays None), for the entry points called per token."""
+    return None if t is None else t.data_ptr()
+
+
 def _scale_2d(scale: torch.Tensor, B: int, S: int) -> torch.Tensor:
     s = scale.to(torch.float32).contiguous()
     if s.numel() != B * S:
@@ -148,11 +153,13 @@ def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tens
         out = torch.empty((B, H, D), dtype=torch.bfloat16, device=q.device)
     else:
         _check_out("out", out, torch.bfloat16, B * H * D, q.device)
-    with torch.cuda.device(q.device):
-        _lib.check(_lib.lib().aekv_quant_sink_attention(
-            _lib.ptr(qc), _lib.ptr(cc), _lib.ptr(sc), _lib.ptr(s64), _lib.ptr(win), _lib.ptr(sk), _lib.ptr(diag), B, H,
-            D, S, K, W, bits, float(softmax_scale), _lib.ptr(workspace), workspace.numel(), _lib.ptr(out),
-            _lib.stream_of(q)), "aekv_quant_sink_attention")
+    dev = q.device
+    with _lib.on_device(dev):
+        rc = _lib.hot("aekv_quant_sink_attention")(
+            qc.data_ptr(), cc.data_ptr(), sc.data_ptr(), _iptr(s64), _iptr(win), sk.data_ptr(), diag.data_ptr(), B, H,
+            D, S, K, W, bits, float(softmax_scale), workspace.data_ptr(), workspace.numel(), out.data_ptr(),
+            _lib.raw_stream(dev))
+    _lib.check(rc, "aekv_quant_sink_attention")
     return out.view(B, 1, H, D) if squeeze else out
 
 
@@ -229,13 +236,13 @@ def csa_decode_step(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.
         _check_out("out", out, torch.bfloat16, B * H * D, dev)
     if workspace is None:
         workspace = decode_workspace(B, S, k, H, D, W, dev)
-    with torch.cuda.device(dev):
-        _lib.check(L.aekv_csa_decode_quant(
-            _lib.ptr(iq), _lib.ptr(iw), _lib.ptr(ic), _lib.ptr(isc), _lib.ptr(idiag), _lib.ptr(v), B, S, IH, IC,
-            index_quant.bits, int(k), _lib.INDEX_MODES[mode], _lib.ptr(q3), _lib.ptr(kc), _lib.ptr(ksc), _lib.ptr(win),
-            _lib.ptr(sk), _lib.ptr(kdiag), H, D, W, kv_quant.bits, float(softmax_scale), _lib.ptr(workspace),
-            workspace.numel(), _lib.ptr(out_idx), _lib.ptr(scores), _lib.ptr(out), _lib.stream_of(q)),
-            "aekv_csa_decode_quant")
+    with _lib.on_device(dev):
+        rc = _lib.hot("aekv_csa_decode_quant")(
+            iq.data_ptr(), iw.data_ptr(), ic.data_ptr(), isc.data_ptr(), idiag.data_ptr(), _iptr(v), B, S, IH, IC,
+            index_quant.bits, int(k), _lib.INDEX_MODES[mode], q3.data_ptr(), kc.data_ptr(), ksc.data_ptr(), _iptr(win),
+            sk.data_ptr(), kdiag.data_ptr(), H, D, W, kv_quant.bits, float(softmax_scale), workspace.data_ptr(),
+            workspace.numel(), out_idx.data_ptr(), _iptr(scores), out.data_ptr(), _lib.raw_stream(dev))
+    _lib.check(rc, "aekv_csa_decode_quant")
     o = out.view(B, 1, H, D) if squeeze else out
     return (o, out_idx, scores) if return_scores else (o, out_idx)
 

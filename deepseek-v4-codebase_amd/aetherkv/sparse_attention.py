@@ -9,10 +9,16 @@ Reference: aether_kernels/sparse_attention.py:8-83 (wrappers) and aether_kernels
 * ``hca_compress(buffer_c, buffer_z)``
 
 Outputs are freshly allocated tensors on the inputs' device; kernels run on the current stream.  The
-attention calls also take a split workspace from torch's caching allocator when the matrix-core
-launch would leave most CUs idle (few targets, many sources).
+attention calls also take a split workspace when the matrix-core launch would leave most CUs idle
+(few targets, many sources): one buffer per (device, stream), reused by the calls on that stream.
+The host-side cost per call is kept small because the reference's callers make one call per target
+token (modeling.py:322,534): pointers go to the library as plain integers, the stream handle is read
+without building a Stream object, the device is switched only when it is not already current, and
+workspace sizes are memoised per shape.
 """
 from __future__ import annotations
+
+import functools
 
 import torch
 
@@ -31,13 +37,49 @@ def _check_sink(sink: torch.Tensor, heads: int) -> None:
         raise RuntimeError("sink must be a scalar or a [num_heads] tensor")
 
 
-def _workspace(nbytes: int, device):
-    """Split workspace for the matrix-core attention (torch's caching allocator; None: no split)."""
-    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
+@functools.lru_cache(maxsize=256)
+def _ws_bytes(dt: int, B: int, T: int, H: int, D: int, S: int, K: int) -> int:
+    return int(_lib.lib().aekv_sink_attention_workspace_size(dt, B, T, H, D, S, K))
+
+
+_IDX_DTYPES = (torch.int64, torch.int32)
+
+
+def _sparse_ok(q, kv, topk_indices, sink) -> bool:
+    """Every check of _sparse_checks passes (one expression: the checks' cost counts per call)."""
+    qs, ks, ts = q.shape, kv.shape, topk_indices.shape
+    return (q.is_cuda and kv.is_cuda and topk_indices.is_cuda and sink.is_cuda and q.is_contiguous()
+            and kv.is_contiguous() and topk_indices.is_contiguous() and sink.is_contiguous() and len(qs) == 4
+            and len(ks) == 4 and ks[2] == 2 and len(ts) == 3 and qs[0] == ks[0] == ts[0] and qs[1] == ts[1]
+            and qs[3] == ks[3] and topk_indices.dtype in _IDX_DTYPES
+            and (sink.numel() == 1 or (sink.dim() == 1 and sink.size(0) == qs[2])) and kv.dtype == q.dtype
+            and sink.dtype == q.dtype)
 
 
 def _ext_sparse_sink_attention(q, kv, topk_indices, sink, softmax_scale):
     """bindings.cpp:21-46 checks, then aekv_sparse_sink_attention."""
+    if not _sparse_ok(q, kv, topk_indices, sink):
+        _sparse_checks(q, kv, topk_indices, sink)
+    B, T, H, D = q.shape
+    S, K = kv.size(1), topk_indices.size(2)
+    out = torch.empty_like(q)
+    dev = q.device
+    dt = _lib.TORCH_TO_AEKV.get(q.dtype)
+    if dt is None:
+        raise RuntimeError(f"unsupported dtype {q.dtype}")
+    st = _lib.raw_stream(dev)
+    ws = _lib.workspace(_ws_bytes(dt, B, T, H, D, S, K), dev, st)
+    with _lib.on_device(dev):
+        rc = _lib.hot("aekv_sparse_sink_attention_ws")(
+            q.data_ptr(), kv.data_ptr(), topk_indices.data_ptr(), _lib.I64 if topk_indices.dtype == torch.int64
+            else _lib.I32, sink.data_ptr(), sink.numel(), dt, B, T, H, D, S, K, float(softmax_scale),
+            None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), out.data_ptr(), st)
+    _lib.check(rc, "aekv_sparse_sink_attention")
+    return out
+
+
+def _sparse_checks(q, kv, topk_indices, sink) -> None:
+    """The reference's checks in its order, each with its message (raises on the first failure)."""
     for n, t in (("q", q), ("kv", kv), ("topk_indices", topk_indices), ("sink", sink)):
         _check_input(n, t)
     if q.dim() != 4:
@@ -61,22 +103,40 @@ def _ext_sparse_sink_attention(q, kv, topk_indices, sink, softmax_scale):
     _check_sink(sink, q.size(2))
     if kv.dtype != q.dtype or sink.dtype != q.dtype:
         raise RuntimeError("q, kv and sink must share one floating dtype")
-    B, T, H, D = q.shape
-    out = torch.empty_like(q)
-    L = _lib.lib()
-    K = topk_indices.size(2)
-    ws = _workspace(L.aekv_sink_attention_workspace_size(_lib.dtype_code(q), B, T, H, D, kv.size(1), K), q.device)
-    with torch.cuda.device(q.device):
-        _lib.check(L.aekv_sparse_sink_attention_ws(
-            _lib.ptr(q), _lib.ptr(kv), _lib.ptr(topk_indices), _lib.dtype_code(topk_indices), _lib.ptr(sink),
-            sink.numel(), _lib.dtype_code(q), B, T, H, D, kv.size(1), K, float(softmax_scale),
-            _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(out), _lib.stream_of(q)),
-            "aekv_sparse_sink_attention")
-    return out
+
+
+def _tiled_ok(q, kv, sink, tile_size) -> bool:
+    """Every check of _tiled_checks passes."""
+    qs, ks = q.shape, kv.shape
+    return (q.is_cuda and kv.is_cuda and sink.is_cuda and q.is_contiguous() and kv.is_contiguous()
+            and sink.is_contiguous() and len(qs) == 4 and len(ks) == 4 and ks[2] == 2 and qs[0] == ks[0]
+            and qs[3] == ks[3] and tile_size > 0 and (sink.numel() == 1 or (sink.dim() == 1 and sink.size(0) == qs[2]))
+            and kv.dtype == q.dtype and sink.dtype == q.dtype)
 
 
 def _ext_tiled_prefill_attention(q, kv, sink, softmax_scale, tile_size):
     """bindings.cpp:58-77 checks, then aekv_tiled_prefill_attention (sink counted once)."""
+    if not _tiled_ok(q, kv, sink, tile_size):
+        _tiled_checks(q, kv, sink, tile_size)
+    B, T, H, D = q.shape
+    S = kv.size(1)
+    out = torch.empty_like(q)
+    dev = q.device
+    dt = _lib.TORCH_TO_AEKV.get(q.dtype)
+    if dt is None:
+        raise RuntimeError(f"unsupported dtype {q.dtype}")
+    st = _lib.raw_stream(dev)
+    ws = _lib.workspace(_ws_bytes(dt, B, T, H, D, S, -1), dev, st)
+    with _lib.on_device(dev):
+        rc = _lib.hot("aekv_tiled_prefill_attention_ws")(
+            q.data_ptr(), kv.data_ptr(), sink.data_ptr(), sink.numel(), dt, B, T, H, D, S, float(softmax_scale),
+            int(tile_size), None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), out.data_ptr(), st)
+    _lib.check(rc, "aekv_tiled_prefill_attention")
+    return out
+
+
+def _tiled_checks(q, kv, sink, tile_size) -> None:
+    """The reference's checks in its order, each with its message (raises on the first failure)."""
     for n, t in (("q", q), ("kv", kv), ("sink", sink)):
         _check_input(n, t)
     if q.dim() != 4:
@@ -94,16 +154,6 @@ def _ext_tiled_prefill_attention(q, kv, sink, softmax_scale, tile_size):
     _check_sink(sink, q.size(2))
     if kv.dtype != q.dtype or sink.dtype != q.dtype:
         raise RuntimeError("q, kv and sink must share one floating dtype")
-    B, T, H, D = q.shape
-    out = torch.empty_like(q)
-    L = _lib.lib()
-    ws = _workspace(L.aekv_sink_attention_workspace_size(_lib.dtype_code(q), B, T, H, D, kv.size(1), -1), q.device)
-    with torch.cuda.device(q.device):
-        _lib.check(L.aekv_tiled_prefill_attention_ws(
-            _lib.ptr(q), _lib.ptr(kv), _lib.ptr(sink), sink.numel(), _lib.dtype_code(q), B, T, H, D, kv.size(1),
-            float(softmax_scale), int(tile_size), _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(out),
-            _lib.stream_of(q)), "aekv_tiled_prefill_attention")
-    return out
 
 
 def _ext_csa_indexer_topk(index_q, index_kv, index_weight, k, mode="relu_w"):
@@ -170,6 +220,7 @@ def tiled_prefill_attention(q: torch.Tensor, kv: torch.Tensor, sink: torch.Tenso
                             tile_size: int = 256) -> torch.Tensor:
     """Sink attention of every target over all S sources; the sink enters the normaliser once
     (aether_2b/modeling.py:158-178 semantics)."""
+    # (.contiguous() as the reference wrapper, sparse_attention.py:37-39; a no-op on contiguous views)
     return _ext_tiled_prefill_attention(q.contiguous(), kv.contiguous(), sink.contiguous(), float(softmax_scale),
                                         int(tile_size))
 

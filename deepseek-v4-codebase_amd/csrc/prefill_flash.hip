@@ -512,7 +512,7 @@ flash_sink_attn_kernel(FlashArgs a) {
   const float mf = fmaxf(m_run, sk);
   const float fo = m_run == kFNegInf ? 0.0f : exp2f(m_run - mf);
   const float L = fmaf(lsum, fo, exp2f(sk - mf));
-  const float rs = fo / L;
+  const float rs = mf == kFNegInf ? 0.0f : fo / L;  // no source and sink -inf: 0
   uint16_t* orow = a.out + (static_cast<int64_t>(b) * RT + r) * kFD;  // r < RT here
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)

@@ -516,7 +516,7 @@ __device__ __forceinline__ void attend_finish(const QAttnMfmaArgs& a, const int6
       stat[(w * 16 + h) * 2] = f;
     }
     if (a.n_split == 1) {
-      inv[h] = 1.0f / Lsum;
+      inv[h] = M == kNegInf ? 0.0f : 1.0f / Lsum;  // no source and sink -inf: 0
     } else {
       float* dst = a.part + ((b * a.n_split + split) * H + h) * kPartStride;
       dst[0] = M;

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kThreads) void sparse_attn_kernel(const void* __res
   const float M = fmaxf(m, sk);
   const float cm = (m == kNegInf) ? 0.0f : __expf(m - M);
   const float den = l * cm + __expf(sk - M);
-  const float f = cm / den;
+  const float f = M == kNegInf ? 0.0f : cm / den;  // no valid source and sink -inf: 0
 #pragma unroll
   for (int i = 0; i < kMaxDPL; ++i) {
     const int d = lane + 64 * i;
@@ -273,7 +273,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_combine_kernel(QAttnArgs 
       fac[t * H + h] = f;
       L += f * part[(t * H + h) * (D + 2) + 1];
     }
-    den[h] = L;
+    den[h] = M == kNegInf ? 1.0f : L;  // no source and sink -inf: every factor is 0, so 0
   }
   __syncthreads();
   for (int p = threadIdx.x; p < H * D; p += kThreads) {

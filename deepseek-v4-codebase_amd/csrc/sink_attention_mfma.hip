@@ -240,7 +240,8 @@ __global__ __launch_bounds__(64 * NW) void gather_attn_kernel(GatherArgs a) {
       L.st[(w * 16 + h) * 2] = f;
     }
     if (whole) {
-      L.inv[h] = 1.0f / den;
+      // no valid source and sink -inf: 0, as the reference kernel (its sum skips every index)
+      L.inv[h] = M == kNegInf ? 0.0f : 1.0f / den;
     } else {
       float* dst = a.part + ((bt * a.H + h0 + h) * a.n_split + split) * kPartStride;
       dst[0] = M;

@@ -349,6 +349,8 @@ int aekvo_topk(const double* scores, const int32_t* valid, int64_t B, int64_t S,
 /* outside [0,S) contributes nothing).                                                          */
 /*   l_j = scale * q.K[idx_j];  M = max(max_j l_j, sink_h)                                       */
 /*   out = sum_j e^{l_j-M} V[idx_j] / (sum_j e^{l_j-M} + e^{sink_h-M})   (duplicates counted)    */
+/* A target with no index in range gets 0 whatever its sink (the kernel's weighted sum visits    */
+/* only in-range indices, :102-113, so with the sink at -inf its NaN normaliser is never used).  */
 /* q [B,T,H,D], kv [B,S,2,D], idx [B,T,K] (int64), sink [sink_numel] fp32; out fp32.            */
 /* ------------------------------------------------------------------------------------------ */
 int aekvo_sink_attention(const float* q, const float* kv, const int64_t* idx, const float* sink,
@@ -377,17 +379,19 @@ int aekvo_sink_attention(const float* q, const float* kv, const int64_t* idx, co
           if (l[j] > M) M = l[j];
         }
         double den = exp(sk - M);
+        int64_t n_in = 0;
         for (int64_t d = 0; d < D; ++d) acc[d] = 0.0;
         for (int64_t j = 0; j < K; ++j) {
           const int64_t s = ip[j];
           if (s < 0 || s >= S) continue;
           const double e = exp(l[j] - M);
           den += e;
+          ++n_in;
           const float* vp = kv + ((b * S + s) * 2 + 1) * D;
           for (int64_t d = 0; d < D; ++d) acc[d] += e * (double)vp[d];
         }
         float* op = out + (bt * H + h) * D;
-        for (int64_t d = 0; d < D; ++d) op[d] = (float)(acc[d] / den);
+        for (int64_t d = 0; d < D; ++d) op[d] = n_in ? (float)(acc[d] / den) : 0.0f;
       }
     }
     free(l);
@@ -446,14 +450,17 @@ int aekvo_quant_attention(const float* q, const uint8_t* codes, const float* sca
           if (l[j] > M) M = l[j];
         }
         double den = exp(sk - M);
+        int64_t n_in = 0;
         for (int64_t d = 0; d < D; ++d) acc[d] = 0.0;
         for (int64_t j = 0; j < n; ++j) {
           if (!ok[j]) continue;
           const double e = exp(l[j] - M);
           den += e;
+          ++n_in;
           for (int64_t d = 0; d < D; ++d) acc[d] += e * (double)src[j * D + d];
         }
-        for (int64_t d = 0; d < D; ++d) out[(b * H + h) * D + d] = (float)(acc[d] / den);
+        /* no source: 0, as the engine's empty-source step (aether_2b/serving.py:451-452) */
+        for (int64_t d = 0; d < D; ++d) out[(b * H + h) * D + d] = n_in ? (float)(acc[d] / den) : 0.0f;
       }
     }
     free(src);

@@ -226,3 +226,29 @@ def test_caller_output_buffers_are_checked_before_the_kernels():
         _check_out("out", torch.empty(8, 4, dtype=torch.bfloat16).t(), torch.bfloat16, 32, dev)
     with pytest.raises(RuntimeError, match="must be on"):
         _check_out("out", torch.empty(32, dtype=torch.bfloat16), torch.bfloat16, 32, torch.device("cuda:0"))
+
+
+def test_fast_call_module_shares_the_library_and_its_checks(lib):
+    # the CPython fast-call functions call the same loaded libaetherkv (one thread-local error
+    # message: a failure through the fast call is read back through ctypes) and take the ctypes
+    # calls' arguments as plain ints / floats / None
+    from aetherkv import _fastcall
+
+    fake = 0x10000
+    rc = _fastcall.aekv_sparse_sink_attention_ws(fake, fake, fake, L.F32, fake, 1, L.BF16, 1, 1, 4, 128, 8, 4, 0.1,
+                                                 None, 0, fake, None)
+    assert rc == L.ERR_DTYPE and "int32 or int64" in _err(lib)
+    rc = _fastcall.aekv_tiled_prefill_attention_ws(fake, fake, fake, 1, L.BF16, 1, 1, 4, 128, 8, 0.1, 0, None, 0,
+                                                   fake, None)
+    assert rc == L.ERR_VALUE
+    need = lib.aekv_quant_attention_workspace_size(64, 12, 128, 256, 128)
+    rc = _fastcall.aekv_quant_sink_attention(fake, fake, fake, fake, fake, fake, fake, 64, 12, 128, 65536, 256, 128, 4,
+                                             0.1, fake, need - 1, fake, None)
+    assert rc == L.ERR_WORKSPACE
+    rc = _fastcall.aekv_csa_decode_quant(fake, fake, fake, fake, fake, None, 2, 100, 4, 64, 3, 16, 0, fake, fake,
+                                         fake, fake, fake, fake, 12, 128, 16, 8, 0.1, fake, 1 << 30, fake, None, fake,
+                                         None)
+    assert rc == L.ERR_VALUE and "bits" in _err(lib)
+    with pytest.raises(TypeError):
+        _fastcall.aekv_quant_sink_attention(fake)
+    assert L.hot("aekv_sparse_sink_attention_ws") is _fastcall.aekv_sparse_sink_attention_ws

@@ -211,3 +211,59 @@ def test_split_calls_in_a_graph(dev):
         torch.cuda.synchronize()
         assert torch.equal(out_d, want_d) and torch.equal(out_s, want_s)
         tiled_prefill_attention(qs, kvs, sink, 0.2)  # eager work between replays
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_no_valid_source_with_sink_minus_inf_is_zero_split_or_not(dev, dtype):
+    # A target whose indices are all out of range, with the sink at -inf: the reference kernel's
+    # weighted sum skips every index and writes 0 (sparse_sink_attention_cuda.cu:102-114), so every
+    # route gives 0 — the split launch (the wrapper's workspace) and the unsplit C entry point —
+    # while the other targets match the oracle.
+    B, T, H, S, K = 1, 2, 16, 640, 640
+    g = torch.Generator().manual_seed(47)
+    q = torch.randn(B, T, H, 128, generator=g).to(dtype)
+    kv = torch.randn(B, S, 2, 128, generator=g).to(dtype)
+    topk = torch.randint(0, S, (B, T, K), generator=g, dtype=torch.int32)
+    topk[0, 1] = -1                                  # target 1: no valid source
+    sink = torch.full((H,), float("-inf")).to(dtype)
+    want = O.sink_attention(to_np_f32(q), to_np_f32(kv), topk.numpy(), to_np_f32(sink), 128 ** -0.5)
+    assert not np.abs(want[0, 1]).sum() and np.isfinite(want).all()
+    qd, kvd, td, sd = q.to(dev), kv.to(dev), topk.to(dev), sink.to(dev)
+    split = sparse_sink_attention(qd, kvd, td, sd, 128 ** -0.5)
+    unsplit = torch.empty_like(qd)
+    with torch.cuda.device(dev):
+        L.check(L.lib().aekv_sparse_sink_attention(L.ptr(qd), L.ptr(kvd), L.ptr(td), L.I32, L.ptr(sd), H,
+                                                   L.dtype_code(qd), B, T, H, 128, S, K, 128 ** -0.5, L.ptr(unsplit),
+                                                   L.stream_of(qd)), "sparse")
+    torch.cuda.synchronize()
+    tol = 1e-4 if dtype == torch.float32 else TOL
+    for got in (split, unsplit):
+        assert torch.isfinite(got.float()).all()
+        np.testing.assert_allclose(to_np_f32(got), want, rtol=tol, atol=tol)
+        assert not bool(got[0, 1].float().abs().sum())
+
+
+def test_quant_attention_without_sources_and_sink_minus_inf_is_zero(dev):
+    # the quantised decode attention (the engine returns zeros when a step has no source,
+    # aether_2b/serving.py:451-452): every selected index skipped, no window, sink -inf -> 0, in
+    # one piece and split over pieces (a row of 3000 selected blocks)
+    from aetherkv import PolarQuant
+    from aetherkv.decode import quant_sink_attention
+
+    pq = PolarQuant(4)
+    B, H, S = 2, 12, 4000
+    g = torch.Generator().manual_seed(49)
+    codes, scale = pq.encode(torch.randn(B, S, 128, generator=g).to(torch.bfloat16).to(dev))
+    q = torch.randn(B, 1, H, 128, generator=g).to(torch.bfloat16).to(dev)
+    sink = torch.full((H,), float("-inf"), device=dev)
+    for K in (100, 3000):
+        sel = torch.full((B, K), -1, dtype=torch.int64, device=dev)
+        sel[0] = torch.randint(0, S, (K,), generator=g).to(dev)     # row 0 has sources, row 1 none
+        out = quant_sink_attention(q, codes, scale, sel, None, sink, 128 ** -0.5, quant=pq)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out.float()).all(), K
+        assert not bool(out[1].float().abs().sum()), K
+        want = O.quant_attention(to_np_f32(q).reshape(B, H, 128), codes.cpu().numpy(), scale.cpu().numpy(),
+                                 sel.cpu().numpy(), np.zeros((B, 0, 128), np.float32), to_np_f32(sink),
+                                 O.diag(42, 128), 4, 128 ** -0.5)
+        np.testing.assert_allclose(to_np_f32(out).reshape(B, H, 128), want, rtol=1e-2, atol=2e-3)

@@ -357,6 +357,30 @@ def test_sink_attention_no_valid_index_gives_zero():
     assert not got.any()
 
 
+def test_sink_attention_no_valid_index_and_sink_minus_inf_gives_zero_not_nan():
+    # sparse_sink_attention_cuda.cu:102-113 sums weight * V over in-range indices only: with none
+    # the output is 0 even though its normaliser e^{sink - max} is NaN at sink = max = -inf.  A
+    # target with a valid index is unaffected (plain softmax, checked against brute force).
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((1, 2, 2, 8)).astype(np.float32)
+    kv = rng.standard_normal((1, 4, 2, 8)).astype(np.float32)
+    idx = np.array([[[-1, 9, 4], [0, 2, -3]]])
+    sink = np.array([-np.inf, -np.inf], np.float32)
+    got = O.sink_attention(q, kv, idx, sink, 0.5)
+    assert np.isfinite(got).all() and not got[0, 0].any()
+    np.testing.assert_allclose(got[0, 1], _brute_attention(q[:, 1:], kv, idx[:, 1:], sink, 0.5)[0, 0],
+                               rtol=1e-6, atol=1e-7)
+    # the quantised decode attention: a row with no selected block and no window is 0 as well
+    B, H, D, S = 2, 2, 16, 6
+    dg = O.diag(42, D)
+    codes, scale = O.encode(O.f32_to_bf16(rng.standard_normal((B, S, D)).astype(np.float32)), "bf16", 8, dg)
+    qq = O.bf16_to_f32(O.f32_to_bf16(rng.standard_normal((B, H, D)).astype(np.float32)))
+    sel = np.array([[0, 3], [-1, -1]])
+    out = O.quant_attention(qq, codes, scale, sel, np.zeros((B, 0, D), np.float32), np.full(H, -np.inf, np.float32),
+                            dg, 8, 0.25)
+    assert np.isfinite(out).all() and not out[1].any() and out[0].any()
+
+
 @pytest.mark.parametrize("bits", [8, 4])
 def test_quant_attention_equals_decode_gather_concat_attend(bits):
     # aether_2b/serving.py:597-625 composed from oracle pieces: decode to bf16, gather, concat window,
