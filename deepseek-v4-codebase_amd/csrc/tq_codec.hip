@@ -229,6 +229,9 @@ extern "C" int aekv_tq_encode(const void* x, int32_t x_dtype, int64_t n_vec, int
   if (bits == 4 && d == 128 && x_dtype == AEKV_BF16 && use_specialised_codec() &&
       launch_encode4_d128_bf16(x, n_vec, diag, wht_scale(d), codes, scale, as_stream(stream)))
     return check_launch("aekv_tq_encode");
+  if (x_dtype == AEKV_BF16 && use_specialised_codec() &&
+      launch_encode_fast_bf16(x, n_vec, bits, d, diag, wht_scale(d), codes, scale, as_stream(stream)))
+    return check_launch("aekv_tq_encode");
   fwd_fn fn = bits == 8 ? pick_fwd_dt<kModeEnc8>(x_dtype, d) : pick_fwd_dt<kModeEnc4>(x_dtype, d);
   hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(grid_for(n_vec, d))), dim3(kThreads), 0, as_stream(stream), x,
                      n_vec, diag, wht_scale(d), codes, scale);

@@ -1,4 +1,5 @@
-// Fast TurboQuant 4-bit encode and decode for the production shape: D = 128, bf16 (gfx950).
+// Fast TurboQuant encode and decode for the production shapes (gfx950): the 4-bit D = 128 bf16 KV
+// layer (encode and decode), and the encode of 8-bit D = 128 blocks and of the D = 64 index keys.
 //
 // ENCODE
 // Same result, bit for bit, as tq_forward_kernel<BF16, 128, ENC4> and as
@@ -278,6 +279,218 @@ __global__ __launch_bounds__(kEncThreads, kEncMinWaves) void tq_encode4_d128_bf1
   encode_group(ta, x, grp, n_vec, v, g, dm, s32, s64, sigma, diag, c, c7, codes, scale);
 }
 
+// ---- encode of the engine's other shapes: 8-bit D = 128, 4- and 8-bit D = 64 (bf16 in) ---------
+// The 4-bit D = 128 design with two changes.
+// * Layout: 32 elements per lane as above, LPV = D / 32 lanes per vector (4 at D = 128: stages h =
+//   32, 64 across the quad; 2 at D = 64: stage h = 32 across the lane pair), 64 / LPV vectors per
+//   wave.  A wave reads 4 KiB and writes 64 / LPV vectors' codes (1 or 2 KiB), contiguous.
+// * Quantiser factor in fp64.  With Q = 127 the rounding grid is 18x finer than at Q = 7, so the
+//   4-bit kernel's interval K(1 +- 2^-20) would straddle a rounding boundary in a large share of
+//   waves.  Here K = Q c / m is computed in fp64 (error ~2^-52) once per vector and widened to
+//   K- = fp32(K (1 - 4 2^-24)) <= K (1 - 3 2^-24) and K+ = fp32(K (1 + 4 2^-24)) >= K (1 + 3 2^-24)
+//   (each fp32 rounding moves it by at most 2^-24 relative).  The reference's three roundings keep
+//   t = RN(RN(RN(raw c) / m) Q) within 3 2^-24 of raw c Q / m, so t lies between raw K- and raw K+
+//   and, rne being monotonic, equal roundings of the two decide rne(t).  A wave with any element
+//   undecided (within ~8 2^-24 |t| of a half-integer: ~3% of 8-bit D = 128 waves on Gaussian
+//   data, a few per mille at 4 bits) re-encodes its vectors with the reference's exact sequence.
+// * 8-bit codes: RN(p + 1.5 2^23 + 128) = 1.5 2^23 + 128 + rne(p) for |p| <= 2^22, whose low
+//   byte is rne(p) + 128; xor 0x80 gives the two's-complement int8.
+constexpr float kMagic128 = 12583040.0f;  // 1.5 * 2^23 + 128
+
+template <int BITS, int D>
+struct FastEnc {
+  static constexpr int LPV = D / 32;               // lanes per vector
+  static constexpr int VPW = 64 / LPV;             // vectors per wave (one group)
+  static constexpr int RB = BITS == 8 ? D : D / 2; // code bytes per vector
+  static constexpr int LB = RB / LPV;              // code bytes per lane (16 or 32)
+  static constexpr float Q = BITS == 8 ? 127.0f : 7.0f;
+};
+
+// Stage h = 32 alone (lane ^ 1 through DPP quad_perm [1,0,3,2]) on eight registers, as in
+// quad_stages8.
+__device__ __forceinline__ void pair_stage8(float& a0, float& a1, float& a2, float& a3, float& a4, float& a5,
+                                            float& a6, float& a7, float s32) {
+  asm("s_nop 1\n"
+      "v_fmac_f32_dpp %0, %0, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %1, %1, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %2, %2, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %3, %3, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %4, %4, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %5, %5, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %6, %6, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n"
+      "v_fmac_f32_dpp %7, %7, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf"
+      : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(a4), "+v"(a5), "+v"(a6), "+v"(a7)
+      : "v"(s32));
+}
+
+// The reference's exact sequence for the group's vectors, re-read from x (the generic kernel's
+// per-lane code: 8 elements per lane, D / 8 lanes per vector).
+template <int BITS, int D>
+__device__ __forceinline__ void encode_group_exact_g(const uint16_t* __restrict__ x, int64_t grp, int64_t n_vec,
+                                                     const float* __restrict__ diag, float c,
+                                                     uint8_t* __restrict__ codes, float* __restrict__ scale) {
+  using F = FastEnc<BITS, D>;
+  constexpr int EPL = 8, LPV8 = D / EPL, VPP = 64 / LPV8, NB = BITS == 8 ? EPL : EPL / 2;
+  const int lane = threadIdx.x & 63;
+  const int sub = lane % LPV8, slot = lane / LPV8;
+  float dg[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) dg[e] = diag[sub * EPL + e];
+#pragma unroll 1
+  for (int pass = 0; pass < F::VPW / VPP; ++pass) {
+    const int64_t v = grp * F::VPW + pass * VPP + slot;
+    const bool ok = v < n_vec;
+    float a[EPL];
+    load_elems<AEKV_BF16, EPL>(x, v * D + sub * EPL, ok, a);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) a[e] = a[e] * dg[e];
+    float m;
+    const Bytes<NB> w = encode_lane<BITS, D, false>(a, sub, c, &m);
+    if (ok) {
+      if (sub == 0) scale[v] = m / F::Q;
+      *reinterpret_cast<Bytes<NB>*>(codes + v * F::RB + sub * NB) = w;
+    }
+  }
+}
+
+template <int BITS, int D>
+__global__ __launch_bounds__(kEncThreads, kEncMinWaves) void tq_encode_fast_bf16_kernel(
+    const uint16_t* __restrict__ x, int64_t n_vec, const float* __restrict__ diag, float c,
+    uint8_t* __restrict__ codes, float* __restrict__ scale) {
+  using F = FastEnc<BITS, D>;
+  constexpr int LPV = F::LPV, VPW = F::VPW;
+  const int lane = threadIdx.x & 63;
+  const int v = lane / LPV, g = lane % LPV;
+  // diag sign masks of the lane part's 16 packed words (bit 15: low element, bit 31: high)
+  __shared__ uint4 dm_tab[LPV][4];
+  if (threadIdx.x < 16 * LPV) {
+    const int gg = threadIdx.x >> 4, k = threadIdx.x & 15;
+    reinterpret_cast<uint32_t*>(dm_tab[gg])[k] = (diag[32 * gg + 2 * k] < 0.0f ? 0x8000u : 0u) |
+                                                (diag[32 * gg + 2 * k + 1] < 0.0f ? 0x80000000u : 0u);
+  }
+  __syncthreads();
+  const int64_t n_groups = (n_vec + VPW - 1) / VPW;
+  const int64_t grp = static_cast<int64_t>(blockIdx.x) * (kEncThreads / 64) +
+                      __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  if (grp >= n_groups) return;
+  // the lane's 64 bytes (lanes past a partial last group re-read its last vector, never stored)
+  uint32_t w[16];
+  {
+    const char* base = reinterpret_cast<const char*>(x + grp * VPW * D);
+    const int64_t rem = n_vec - grp * VPW;
+    const uint32_t vv = static_cast<uint32_t>(v < rem ? v : rem - 1);
+    const uint32_t off = vv * (2u * D) + static_cast<uint32_t>(g) * 64u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 t = *reinterpret_cast<const uint4*>(base + (off + 16u * i));
+      w[4 * i] = t.x;
+      w[4 * i + 1] = t.y;
+      w[4 * i + 2] = t.z;
+      w[4 * i + 3] = t.w;
+    }
+  }
+  uint32_t dm[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 d = dm_tab[g][i];
+    dm[4 * i] = d.x;
+    dm[4 * i + 1] = d.y;
+    dm[4 * i + 2] = d.z;
+    dm[4 * i + 3] = d.w;
+  }
+  float a[32];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    // stage h = 1 on x * diag: lo + hi, lo - hi
+    const float lo = __builtin_bit_cast(float, (w[k] + dm[k]) << 16);
+    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_bitop3_b32(w[k], 0xFFFF0000u, dm[k], 0x48));
+    a[2 * k] = lo + hi;
+    a[2 * k + 1] = lo - hi;
+  }
+#pragma unroll
+  for (int h = 2; h < 32; h <<= 1) {
+#pragma unroll
+    for (int blk = 0; blk < 32; blk += 2 * h) {
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const float p = a[blk + i], q = a[blk + h + i];
+        a[blk + i] = p + q;
+        a[blk + h + i] = p - q;
+      }
+    }
+  }
+  const float s32 = (g & 1) ? -1.0f : 1.0f;
+  float sigma = s32;
+  if constexpr (LPV == 4) {
+    const float s64 = (g & 2) ? -1.0f : 1.0f;
+    sigma = s32 * s64;
+#pragma unroll
+    for (int r = 0; r < 32; r += 8)
+      quad_stages8(a[r], a[r + 1], a[r + 2], a[r + 3], a[r + 4], a[r + 5], a[r + 6], a[r + 7], s32, s64);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 32; r += 8)
+      pair_stage8(a[r], a[r + 1], a[r + 2], a[r + 3], a[r + 4], a[r + 5], a[r + 6], a[r + 7], s32);
+  }
+  // m = max(RN(c max|raw|), 1e-8) over the LPV lanes of the vector
+  float mr = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 32; r += 2) mr = max3_abs(mr, a[r], a[r + 1]);
+  mr = fmaxf(mr, xor_lane<1>(mr));
+  if constexpr (LPV == 4) mr = fmaxf(mr, xor_lane<2>(mr));
+  const float m = fmaxf(mr * c, 1e-8f);
+  const double kd = static_cast<double>(c) * static_cast<double>(F::Q) / static_cast<double>(m);
+  const float klo = static_cast<float>(kd * (1.0 - 0x1p-22)) * sigma;
+  const float khi = static_cast<float>(kd * (1.0 + 0x1p-22)) * sigma;
+  constexpr float kMag = BITS == 8 ? kMagic128 : kMagic8;
+  constexpr int NW = F::LB / 4;  // code dwords per lane
+  uint32_t o[NW];
+  uint32_t diff = 0u;
+#pragma unroll
+  for (int dw = 0; dw < NW; ++dw) {
+    constexpr int EPW = BITS == 8 ? 4 : 8;  // elements per code dword
+    uint32_t b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (BITS == 8) {
+        const float x0 = a[EPW * dw + j];
+        const uint32_t u0 = __builtin_bit_cast(uint32_t, fmaf(x0, klo, kMag));
+        diff = __builtin_amdgcn_bitop3_b32(diff, u0, __builtin_bit_cast(uint32_t, fmaf(x0, khi, kMag)), 0xF6);
+        b[j] = u0;
+      } else {
+        const float x0 = a[EPW * dw + 2 * j], x1 = a[EPW * dw + 2 * j + 1];
+        const uint32_t u0 = __builtin_bit_cast(uint32_t, fmaf(x0, klo, kMag));
+        const uint32_t u1 = __builtin_bit_cast(uint32_t, fmaf(x1, klo, kMag));
+        diff = __builtin_amdgcn_bitop3_b32(diff, u0, __builtin_bit_cast(uint32_t, fmaf(x0, khi, kMag)), 0xF6);
+        diff = __builtin_amdgcn_bitop3_b32(diff, u1, __builtin_bit_cast(uint32_t, fmaf(x1, khi, kMag)), 0xF6);
+        b[j] = nib_pair(u0, u1);
+      }
+    }
+    if constexpr (BITS == 8) {
+      const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u);  // [b0.0, b1.0, 0, 0]
+      const uint32_t hi = __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu);  // [0, 0, b2.0, b3.0]
+      o[dw] = (lo | hi) ^ 0x80808080u;
+    } else {
+      o[dw] = pack4(b[0], b[1], b[2], b[3]);
+    }
+  }
+  if (__builtin_amdgcn_ballot_w64(diff != 0u) != 0) {  // a rounding the interval cannot decide
+    encode_group_exact_g<BITS, D>(x, grp, n_vec, diag, c, codes, scale);
+    return;
+  }
+  if (v < n_vec - grp * VPW) {  // streaming stores: the outputs are not read again by this kernel
+    if (g == 0)
+      __builtin_nontemporal_store(m / F::Q, reinterpret_cast<float*>(reinterpret_cast<char*>(scale + grp * VPW) +
+                                                                      4u * static_cast<uint32_t>(v)));
+    char* cb = reinterpret_cast<char*>(codes + grp * VPW * F::RB) + static_cast<uint32_t>(lane) * F::LB;
+#pragma unroll
+    for (int i = 0; i < NW / 4; ++i) {
+      const u32x4_t ov = {o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+      __builtin_nontemporal_store(ov, reinterpret_cast<u32x4_t*>(cb + 16 * i));
+    }
+  }
+}
+
 // ---- decode: 4-bit codes -> bf16, D = 128 ------------------------------------------------------
 // Same result, bit for bit, as tq_decode_kernel<4, 128, BF16> and aether_2b/turbo_quant.py:187-211
 // (rot = code * scale; x = _wht(rot) * diag; bf16 RNE).
@@ -502,6 +715,33 @@ bool launch_encode4_d128_bf16(const void* x, int64_t n_vec, const float* diag, f
   return true;
 }
 
+
+// Launches the fast encode of 8-bit D = 128 or 4- / 8-bit D = 64 (bf16 in); false when the shape or
+// the alignment is not one of those.
+bool launch_encode_fast_bf16(const void* x, int64_t n_vec, int bits, int d, const float* diag, float c, void* codes,
+                             float* scale, hipStream_t st) {
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(codes) & 15)) return false;
+  void (*kern)(const uint16_t*, int64_t, const float*, float, uint8_t*, float*) = nullptr;
+  int vpw = 0;
+  if (bits == 8 && d == 128) {
+    kern = tq_encode_fast_bf16_kernel<8, 128>;
+    vpw = FastEnc<8, 128>::VPW;
+  } else if (bits == 8 && d == 64) {
+    kern = tq_encode_fast_bf16_kernel<8, 64>;
+    vpw = FastEnc<8, 64>::VPW;
+  } else if (bits == 4 && d == 64) {
+    kern = tq_encode_fast_bf16_kernel<4, 64>;
+    vpw = FastEnc<4, 64>::VPW;
+  } else {
+    return false;
+  }
+  if (n_vec <= 0) return true;
+  const int64_t blocks = ceil_div(ceil_div(n_vec, vpw), kEncThreads / 64);
+  if (blocks > 0x7fffffff) return false;
+  hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(blocks)), dim3(kEncThreads), 0, st,
+                     static_cast<const uint16_t*>(x), n_vec, diag, c, static_cast<uint8_t*>(codes), scale);
+  return true;
+}
 
 // Launches the specialised decode; returns false when the shape or alignment is not the specialised one.
 bool launch_decode4_d128_bf16(const void* codes, const float* scale, int64_t n_vec, const float* diag, float c,

@@ -189,5 +189,8 @@ bool launch_encode4_d128_bf16(const void* x, int64_t n_vec, const float* diag, f
                               hipStream_t st);
 bool launch_decode4_d128_bf16(const void* codes, const float* scale, int64_t n_vec, const float* diag, float c,
                               void* out, hipStream_t st);
+// 8-bit D = 128 and 4- / 8-bit D = 64 encode, bf16 in.
+bool launch_encode_fast_bf16(const void* x, int64_t n_vec, int bits, int d, const float* diag, float c, void* codes,
+                             float* scale, hipStream_t st);
 
 }  // namespace aekv

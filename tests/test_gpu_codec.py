@@ -123,41 +123,44 @@ def test_config2_4bit_full_layer_properties(dev):
     assert float(cos.mean()) > 0.99
 
 
-def near_tie_rows(n: int, seed: int) -> torch.Tensor:
+def near_tie_rows(n: int, seed: int, d: int = 128) -> torch.Tensor:
     """bf16 rows whose rotated values sit on or next to quantiser ties: x*diag = a*e_0 + b*e_j gives
-    raw butterflies a +- b, so raw/max*7 hits k + 1/2 for (a+b, a-b) = (14, 1), (14, 3), (254, 1) ..."""
+    raw butterflies a +- b, so raw/max*Q hits k + 1/2 for (a+b, a-b) = (14, 1), (14, 3) at Q = 7 and
+    (254, 1), (254, 3), (254, 5) at Q = 127 ..."""
     g = torch.Generator().manual_seed(seed)
-    dg = torch.from_numpy(O.diag(42, 128))
-    x = torch.zeros(n, 128)
-    pairs = [(7.5, 6.5), (8.5, 5.5), (9.5, 4.5), (127.5, 126.5), (3.5, 3.0), (1.0, 0.0), (0.75, 0.25)]
+    dg = torch.from_numpy(O.diag(42, d))
+    x = torch.zeros(n, d)
+    pairs = [(7.5, 6.5), (8.5, 5.5), (9.5, 4.5), (127.5, 126.5), (3.5, 3.0), (1.0, 0.0), (0.75, 0.25), (128.5, 125.5),
+             (129.5, 124.5)]
     for i in range(n):
         a, b = pairs[i % len(pairs)]
-        j = int(torch.randint(1, 128, (1,), generator=g))
+        j = int(torch.randint(1, d, (1,), generator=g))
         s = float(torch.randn(1, generator=g).sign())
         x[i, 0] = a * s
         x[i, j] = b * s * (1 if i % 2 else -1)
         if i % 3 == 0:
-            x[i, (j + 5) % 127 + 1] += 0.5
+            x[i, (j + 5) % (d - 1) + 1] += 0.5
     return (x * dg).to(torch.bfloat16)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-def test_encode_near_tie_rows_bit_exact(dev, bits):
-    x = near_tie_rows(4001, 17)
-    want_c, want_s = O.encode(bf16_bits(x), "bf16", bits, O.diag(42, 128))
+@pytest.mark.parametrize("d", [64, 128])
+def test_encode_near_tie_rows_bit_exact(dev, bits, d):
+    x = near_tie_rows(4001, 17, d)
+    want_c, want_s = O.encode(bf16_bits(x), "bf16", bits, O.diag(42, d))
     pq = PolarQuant(bits)
     codes, scale = pq.encode(x.to(dev))
     np.testing.assert_array_equal(codes.cpu().numpy(), want_c)
     np.testing.assert_array_equal(scale.cpu().numpy(), want_s)
 
 
-def wide_pair_rows(n: int, seed: int) -> torch.Tensor:
+def wide_pair_rows(n: int, seed: int, d: int = 128) -> torch.Tensor:
     """bf16 rows whose only nonzero elements are one pair (2k, 2k+1) with magnitudes 2^9 .. 2^30
     apart: the first butterfly stage a +- b is then inexact in fp32 (ties included) and its rounding
     reaches the row maximum, i.e. the scale."""
     g = torch.Generator().manual_seed(seed)
-    x = torch.zeros(n, 128)
-    k = torch.randint(0, 64, (n,), generator=g)
+    x = torch.zeros(n, d)
+    k = torch.randint(0, d // 2, (n,), generator=g)
     ma = 1 + torch.randint(0, 128, (n,), generator=g) / 128.0
     mb = 1 + torch.randint(0, 128, (n,), generator=g) / 128.0
     gap = torch.randint(9, 31, (n,), generator=g).float()
@@ -171,19 +174,26 @@ def wide_pair_rows(n: int, seed: int) -> torch.Tensor:
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-def test_encode_inexact_first_stage_bit_exact(dev, bits):
-    x = wide_pair_rows(4096, 23)
-    want_c, want_s = O.encode(bf16_bits(x), "bf16", bits, O.diag(42, 128))
+@pytest.mark.parametrize("d", [64, 128])
+def test_encode_inexact_first_stage_bit_exact(dev, bits, d):
+    x = wide_pair_rows(4096, 23, d)
+    want_c, want_s = O.encode(bf16_bits(x), "bf16", bits, O.diag(42, d))
     codes, scale = PolarQuant(bits).encode(x.to(dev))
     np.testing.assert_array_equal(scale.cpu().numpy(), want_s)
     np.testing.assert_array_equal(codes.cpu().numpy(), want_c)
 
 
-def test_specialised_and_generic_encode_agree(dev):
+@pytest.mark.parametrize("bits,d,n", [(4, 128, 3001), (8, 128, 3001), (4, 64, 3001), (8, 64, 3001),
+                                      (8, 128, 200003), (4, 64, 400003), (8, 64, 400003)])
+def test_specialised_and_generic_encode_agree(dev, bits, d, n):
+    # the production-shape kernels (4-bit D=128; 8-bit D=128 and 4/8-bit D=64 with the fp64
+    # quantiser factor and the exact fallback for undecided waves) against the generic kernel and the
+    # oracle; n not a multiple of a wave's vectors, the large n over thousands of waves (some of which
+    # take the fallback)
     import aetherkv._lib as L
 
-    x = normal_with_outliers((3001, 128), 5, trailing_dims=1).to(dev)
-    pq = PolarQuant(4)
+    x = normal_with_outliers((n, d), 5 + d + bits, trailing_dims=1).to(dev)
+    pq = PolarQuant(bits)
     prev = L.lib().aekv_set_generic_kernels(1)
     try:
         cg, sg = pq.encode(x)
@@ -191,8 +201,9 @@ def test_specialised_and_generic_encode_agree(dev):
         L.lib().aekv_set_generic_kernels(prev)
     cs, ss = pq.encode(x)
     assert torch.equal(cg, cs) and torch.equal(sg, ss)
-    want_c, want_s = O.encode(bf16_bits(x), "bf16", 4, O.diag(42, 128))
+    want_c, want_s = O.encode(bf16_bits(x), "bf16", bits, O.diag(42, d))
     np.testing.assert_array_equal(cs.cpu().numpy(), want_c)
+    np.testing.assert_array_equal(ss.cpu().numpy(), want_s)
 
 
 @pytest.mark.parametrize("n", [1, 15, 16, 4097, 262147])
