@@ -440,11 +440,14 @@ def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
                         inp["kv_scale"], inp["win"], inp["sink"], D ** -0.5, k, kv_quant=pq, index_quant=pq,
                         workspace=ws_s, out_idx=idx, out=out)
 
-    ms_eager = timed(step, args.steps, args.warmup)
-    ms_warm = timed_graph(step, args.steps, args.warmup)
-    ms_sep = timed_graph(step_separate, args.steps, args.warmup)
-    ms_i = timed_graph(index_only, args.steps, args.warmup)
-    ms_a = timed_graph(attn_only, args.steps, args.warmup)
+    if args.cold_only:  # (profiling the cold step alone)
+        ms_eager = ms_warm = ms_sep = ms_i = ms_a = float("nan")
+    else:
+        ms_eager = timed(step, args.steps, args.warmup)
+        ms_warm = timed_graph(step, args.steps, args.warmup)
+        ms_sep = timed_graph(step_separate, args.steps, args.warmup)
+        ms_i = timed_graph(index_only, args.steps, args.warmup)
+        ms_a = timed_graph(attn_only, args.steps, args.warmup)
     cpu = bench_cpu_csa(inp, cpu_rows, name, bits) if cpu_rows else None
 
     # cold: L layers' caches (layer 0 = the inputs above, layer l > 0 seeded seed + 10007 l), one step
@@ -509,8 +512,11 @@ def bench_hca(args, dev):
     n_layers = max(8, -(-2 * MALL_BYTES // step_bytes) + 1)
     layers = [make_layer(3 + 10007 * l) for l in range(n_layers)]
     step = layer_step(layers[0])
-    ms_eager = timed(step, args.steps, args.warmup)
-    ms_warm = timed_graph(step, args.steps, args.warmup)
+    if args.cold_only:  # (profiling the cold step alone)
+        ms_eager = ms_warm = float("nan")
+    else:
+        ms_eager = timed(step, args.steps, args.warmup)
+        ms_warm = timed_graph(step, args.steps, args.warmup)
     ms = timed_graph_layers([layer_step(x) for x in layers], args.steps, args.warmup)
     res = {"B": B, "S": S, "bits": 4, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / ms * 1e3, 1),
            "timing": f"cold: {n_layers} layers' distinct caches ({n_layers * step_bytes / 2 ** 20:.0f} MiB per pass), "
@@ -759,6 +765,8 @@ def main():
     ap.add_argument("--only", choices=["all", "encode", "codec", "csa", "hca", "prefill", "paging", "io", "sparse"],
                     default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cold-only", action="store_true",
+                    help="decode lines: time only the cold layer rotation (for profiling it alone)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (sharding is a "
