@@ -189,6 +189,27 @@ def rope_inv_freq(rope_dim: int, theta: float, device=None) -> torch.Tensor:
     return (1.0 / (theta ** (freqs / rope_dim))).to(device)
 
 
+def block_rope_position(block, m: int, convention: str = "end"):
+    """RoPE position of compressed block `block` (int or integer tensor) of m tokens.
+
+    "end" (the default): block·m + m − 1, the block's last token.  This is the position the
+    reference uses everywhere but one place: HCA emission in the engine (serving.py:534 passes
+    token_count − 1 to _hca_emit, :498) and in the model (modeling.py:285), CSA blocks in the model
+    (modeling.py:476-480) and in the engine's batched prefill, which builds its cache with
+    _compress_main (serving.py:1146).  At the first query that sees block i (position (i+1)·m) the
+    relative RoPE distance is then 1.
+
+    "start": block·m, what the engine's step-by-step CSA emission uses (serving.py:564:
+    absolute_token − (m − 1) with absolute_token = token_count − 1, :640).  A cache extended this
+    way after a batched prefill mixes the two conventions; pass "start" only to reproduce that
+    engine's decode outputs bit for bit."""
+    if convention == "end":
+        return block * m + (m - 1)
+    if convention == "start":
+        return block * m
+    raise ValueError(f"block_rope_position: convention must be 'end' or 'start', got {convention!r}")
+
+
 def emit_block(quant: PolarQuant, c: torch.Tensor, z: torch.Tensor, *, bias: Optional[torch.Tensor] = None,
                rope_dim: int = 0, positions=None, inv_freq: Optional[torch.Tensor] = None,
                norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,

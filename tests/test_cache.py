@@ -11,7 +11,8 @@ import torch
 
 import oracle as O
 from aetherkv.cache import (CodeRing, CSAServingState, DequantMemo, HCAServingState, append_seq,
-                            compressed_to_bf16_for_paging, quant_append, read_compressed)
+                            block_rope_position, compressed_to_bf16_for_paging, quant_append, read_compressed,
+                            rope_inv_freq)
 from conftest import bf16_bits
 
 HCA_FIELDS = ["token_count", "loaded_prefix_tokens", "compressed", "compressed_scale", "window", "buffer_c",
@@ -129,3 +130,40 @@ def test_code_ring_rejects_bad_shapes():
         ring.append(torch.zeros(2, 1, 8))
     with pytest.raises(ValueError):
         CodeRing(OracleQuant(8), 0, 16, device=torch.device("cpu"))
+
+
+def test_block_rope_position_conventions():
+    m = 128
+    blocks = torch.arange(6)
+    # the engine emits block i when token_count reaches (i + 1) m and passes token_count - 1
+    # (serving.py:534, :640); HCA rotates at it (:498), the step-by-step CSA emission at it - (m - 1) (:564)
+    emitted_at = (blocks + 1) * m - 1
+    assert torch.equal(block_rope_position(blocks, m), emitted_at)
+    assert torch.equal(block_rope_position(blocks, m, "start"), emitted_at - (m - 1))
+    # the model's and the batched prefill's CSA blocks: arange(n) * m + (m - 1) (modeling.py:480)
+    assert torch.equal(block_rope_position(blocks, m), torch.arange(6) * m + (m - 1))
+    assert block_rope_position(3, 4) == 15 and block_rope_position(3, 4, "start") == 12
+    with pytest.raises(ValueError):
+        block_rope_position(1, m, "middle")
+
+
+@pytest.mark.parametrize("block", [0, 5, 300])
+def test_end_position_puts_a_new_block_at_distance_one(block):
+    """RoPE scores depend on the position difference only: the query at (i + 1) m, the first that
+    sees block i, scores that block's key as a key at distance 1 under "end" and m under "start"
+    (the distance the reference's modeling.py:476-478 comment names)."""
+    m, D, rd = 128, 128, 64
+    rng = np.random.default_rng(11 + block)
+    q = O.f32_to_bf16(rng.standard_normal((1, 1, D)).astype(np.float32))
+    k = O.f32_to_bf16(rng.standard_normal((1, 1, D)).astype(np.float32))
+    inv = rope_inv_freq(rd, 10000.0).numpy()
+    f32 = lambda u: O.bf16_to_f32(u).astype(np.float64).ravel()
+    tol = 0.02 * np.linalg.norm(f32(q)) * np.linalg.norm(f32(k))
+    t = (block + 1) * m
+    qt = f32(O.rope_rmsnorm(q, np.array([t]), inv, rd))
+    for conv, dist, other in (("end", 1, m), ("start", m, 1)):
+        kp = f32(O.rope_rmsnorm(k, np.array([block_rope_position(block, m, conv)]), inv, rd))
+        score = qt @ kp
+        at = lambda d: f32(O.rope_rmsnorm(q, np.array([d]), inv, rd)) @ f32(k)
+        assert abs(score - at(dist)) <= tol
+        assert abs(score - at(other)) > tol  # and the two conventions are told apart
