@@ -425,7 +425,7 @@ def csa_decode_ring(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.
 def hca_decode_ring(q: torch.Tensor, kv_ring: CodeRing, window: Optional[torch.Tensor], sink: torch.Tensor,
                     softmax_scale: float, *, workspace: Optional[torch.Tensor] = None,
                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """One HCA decode step (aether_2b/serving.py:507-522) over a ring: every valid block + window."""
-    codes, scale = kv_ring.storage
-    return quant_sink_attention(q, codes, scale, kv_ring.all_indices(), window, sink, softmax_scale,
+    """One HCA decode step (aether_2b/serving.py:507-522) over a ring: every valid block + window.
+    The ring's data / scale views are read in place (the first n blocks of each storage row)."""
+    return quant_sink_attention(q, kv_ring.data, kv_ring.scale, None, window, sink, softmax_scale,
                                 quant=kv_ring.quant, workspace=workspace, out=out)

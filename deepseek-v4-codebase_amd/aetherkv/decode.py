@@ -49,6 +49,23 @@ def _scale_2d(scale: torch.Tensor, B: int, S: int) -> torch.Tensor:
     return s
 
 
+def _prefix_rows(codes: torch.Tensor, scale: torch.Tensor) -> Optional[int]:
+    """Row stride S when codes [B, n, rb] and scale fp32 [B, n] / [B, n, 1] are the first n rows of
+    [B, S, ·] storages (a CodeRing's data / scale views): the kernels then read them in place, as
+    the first n blocks of rows S apart.  None when they are laid out otherwise."""
+    if codes.dim() != 3 or scale.dtype != torch.float32 or scale.dim() not in (2, 3):
+        return None
+    B, n, rb = codes.shape
+    if codes.stride(2) != 1 or codes.stride(1) != rb or codes.stride(0) % rb:
+        return None
+    S = codes.stride(0) // rb
+    if scale.size(0) != B or scale.size(1) != n or (scale.dim() == 3 and scale.size(2) != 1):
+        return None
+    if scale.stride(0) != S or (n > 1 and scale.stride(1) != 1) or S < n:
+        return None
+    return S
+
+
 def indexer_workspace(B: int, S: int, k: int, device) -> torch.Tensor:
     return torch.empty(_lib.lib().aekv_csa_indexer_workspace_size(B, S, k), dtype=torch.uint8, device=device)
 
@@ -129,10 +146,14 @@ def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tens
     if codes.size(-1) * (1 if bits == 8 else 2) != D or codes.size(0) != B:
         raise RuntimeError(f"codes shape {tuple(codes.shape)} does not match q {tuple(q.shape)}")
     qc = q3.contiguous()
-    cc = codes.contiguous()
-    sc = _scale_2d(scale, B, S)
     s64 = None if sel is None else sel.to(torch.int64).contiguous()
     K = -1 if s64 is None else s64.size(1)  # n_sel < 0: every block (HCA)
+    stride = _prefix_rows(codes, scale) if s64 is None and not codes.is_contiguous() else None
+    if stride is not None:
+        # every block of row prefixes (e.g. a ring's valid blocks): read in place, rows `stride` apart
+        cc, sc, K = codes, scale, S
+    else:
+        cc, sc = codes.contiguous(), _scale_2d(scale, B, S)
     if window is not None and window.numel() > 0:
         if window.dtype != torch.bfloat16 or window.dim() != 3 or window.size(0) != B or window.size(2) != D:
             raise RuntimeError(f"window must be bf16 [B, W, D], got {window.dtype} {tuple(window.shape)}")
@@ -157,8 +178,8 @@ def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tens
     with _lib.on_device(dev):
         rc = _lib.hot("aekv_quant_sink_attention")(
             qc.data_ptr(), cc.data_ptr(), sc.data_ptr(), _iptr(s64), _iptr(win), sk.data_ptr(), diag.data_ptr(), B, H,
-            D, S, K, W, bits, float(softmax_scale), workspace.data_ptr(), workspace.numel(), out.data_ptr(),
-            _lib.raw_stream(dev))
+            D, S if stride is None else stride, K, W, bits, float(softmax_scale), workspace.data_ptr(),
+            workspace.numel(), out.data_ptr(), _lib.raw_stream(dev))
     _lib.check(rc, "aekv_quant_sink_attention")
     return out.view(B, 1, H, D) if squeeze else out
 

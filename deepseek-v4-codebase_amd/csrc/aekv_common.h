@@ -67,6 +67,8 @@ int launch_dense_flash_attention(const void* q, const void* kv, const void* sink
                                  int64_t B, int64_t T, int64_t H, int64_t S, float softmax_scale, int n_split,
                                  float* part, void* out, hipStream_t st, const char* who);
 size_t quant_attn_mfma_workspace(int64_t B, int64_t H, int64_t n_src);
+// K: the selection's length (sel [rows or B, K]), or with all_blocks the number of blocks taken in
+// order, 0 .. K-1, of each row of S (the row stride of codes and scale).
 int launch_quant_attn_mfma(const void* q, const void* codes, const float* scale, const int64_t* sel,
                            const void* window, const float* sink, const float* diag, int64_t B, int64_t H, int64_t S,
                            int64_t K, bool all_blocks, int64_t W, int bits, float softmax_scale, void* ws,

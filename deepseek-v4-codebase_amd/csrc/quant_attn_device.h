@@ -371,7 +371,7 @@ __device__ __forceinline__ void group_consume(const QAttnMfmaArgs& a, const Attn
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     okk[kb] = kind[kb] != 0 && (!ok_mask || ok_mask[kb]);
-    const float fk = sraw[kb] * kscale_unit;
+    const float fk = sraw[kb] * kscale_unit;  // 0 for lanes without a code row (no scale loaded)
     // y = H64 codes per half (all lanes take part; lanes without a code row supply zeros)
     i32x4_t P[2][4];
 #pragma unroll
@@ -458,9 +458,13 @@ __device__ __forceinline__ void group_consume(const QAttnMfmaArgs& a, const Attn
     ps += xor_lane<16>(ps);
     ps += xor_lane<32>(ps);
     s.l_run = s.l_run * corr + ps;
-    s.m_run = mnew;
+    // O is rescaled only when some head's running max moved (corr is exactly 1 otherwise, and O is
+    // still 0 while the max is -inf): most groups skip the 32 multiplies
+    if (__builtin_amdgcn_ballot_w64(mnew != s.m_run && s.m_run != kNegInf) != 0) {
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) s.O[nb] *= corr;
+      for (int nb = 0; nb < 8; ++nb) s.O[nb] *= corr;
+    }
+    s.m_run = mnew;
   }
   // B = P^T: lane (head c16), element 4kb + i <-> key 16kb + 4g + i
   const bf16x8_t pb = __builtin_bit_cast(
@@ -621,6 +625,132 @@ __device__ __forceinline__ void attend_row(const QAttnMfmaArgs& a, const int64_t
   attend_main<BITS, NW, NW == 4>(a, b, split, lds, f, rs, nullptr);
 }
 
+// ---- rows that attend every block, without per-row counts (the decode step's HCA call) ----
+// Buffer resources over one cache row's codes, scales and window entries: the hardware checks each
+// load's offset against the range and returns zeros past it, so a lane without such a source loads
+// at an offset past the range instead of branching.  The loads are buffer intrinsics, which the
+// compiler leaves where they are written (it may merge or move plain loads that feed a loop
+// variable down to their first use, which undoes a prefetch).
+constexpr uint32_t kBufWord3 = 0x00020000u;  // 32-bit data, raw (unswizzled) addressing
+constexpr uint32_t kPastRange = 0x80000000u; // an offset past every range (ranges are < 2^31 bytes)
+
+struct DenseRsrc {
+  __amdgpu_buffer_rsrc_t codes, scale, win;
+};
+
+template <int BITS>
+__device__ __forceinline__ DenseRsrc dense_rsrc(const QAttnMfmaArgs& a, const int64_t b) {
+  constexpr int RB = BITS == 8 ? kD : kD / 2;
+  DenseRsrc r;
+  r.codes = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.codes + b * a.S * RB), 0,
+                                              static_cast<int>(a.S * RB), kBufWord3);
+  r.scale = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.scale + b * a.S), 0, static_cast<int>(a.S * 4),
+                                              kBufWord3);
+  r.win = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.win + b * a.Wt * kD), 0,
+                                            static_cast<int>(a.Wt * kD * 2), kBufWord3);
+  return r;
+}
+
+// A group's rows: every lane issues the same loads (a code row's two halves, its scale and, WIN,
+// a window row), at offsets past the range for the sources it does not have, which read as zeros
+// (a zero scale, as group_consume expects of a lane without a code row).
+template <int BITS, bool WIN>
+__device__ __forceinline__ void dense_fetch(const QAttnMfmaArgs& a, const DenseRsrc& rs, const int64_t src0,
+                                            const int64_t src1, const int G, GroupIn<BITS, WIN>& in) {
+  constexpr int RB = BITS == 8 ? kD : kD / 2;
+  constexpr int HB = RB / 2;
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+  const int64_t n_comp = a.n_comp;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int64_t si = src0 + static_cast<int64_t>(G) * kGroup + 16 * kb + c16;
+    const bool is_code = si < n_comp && si < src1;
+    const bool is_win = WIN && !is_code && si < src1;
+    in.kind[kb] = is_code ? 1 : (is_win ? 2 : 0);
+    const uint32_t co = is_code ? static_cast<uint32_t>(si) * RB : kPastRange;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      if constexpr (BITS == 8) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs.codes, co + HB * hh + 16 * g, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) in.cw[kb][hh][e] = v[e];
+      } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs.codes, co + HB * hh + 8 * g, 0, 0);
+        in.cw[kb][hh][0] = v[0];
+        in.cw[kb][hh][1] = v[1];
+      }
+    }
+    in.sraw[kb] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                rs.scale, is_code ? static_cast<uint32_t>(si) * 4 : kPastRange, 0, 0));
+    if constexpr (WIN) {
+      const uint32_t wo = is_win ? static_cast<uint32_t>(si - n_comp) * (2 * kD) + 8 * g : kPastRange;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const auto w0 = __builtin_amdgcn_raw_buffer_load_b64(rs.win, wo + 64 * ks, 0, 0);
+        const auto w1 = __builtin_amdgcn_raw_buffer_load_b64(rs.win, wo + 64 * ks + 32, 0, 0);
+        in.wv2[kb][ks][0] = make_uint2(w0[0], w0[1]);
+        in.wv2[kb][ks][1] = make_uint2(w1[0], w1[1]);
+      }
+    }
+  }
+}
+
+// One split [src0, src1) of decode row b over every block then every window entry (T = 1, no
+// selection, no counts).  The query's and the wave's first group's rows are requested together.
+// Without window entries in the split (!WIN), the second group's rows are requested once the query
+// fragments are built (their registers are free then) and each group is decoded while the group
+// after next is requested (two buffers, no copies).  A split with window entries (WIN: 64 more
+// bytes per lane and block) keeps one buffer: a group's successor is requested after it is decoded.
+template <int BITS, int NW, bool WIN>
+__device__ __forceinline__ void attend_dense(const QAttnMfmaArgs& a, const int64_t b, const int split,
+                                             unsigned char* lds) {
+  constexpr int kW = NW;
+  const int wv = threadIdx.x >> 6;
+  const int64_t src0 = static_cast<int64_t>(split) * a.split_src;
+  const int64_t src1 = min<int64_t>(a.n_comp + a.Wt, src0 + a.split_src);
+  const int n_groups = src1 > src0 ? static_cast<int>((src1 - src0 + kGroup - 1) / kGroup) : 0;
+  // (the scheduling barriers keep each request batch in program order: a wait counts requests in
+  // issue order, so a batch moved behind a later one would make its wait include that one too)
+  const DenseRsrc rs = dense_rsrc<BITS>(a, b);
+  PrologueRaw praw;
+  prologue_loads(a, b, praw);
+  __builtin_amdgcn_sched_barrier(0);
+  GroupIn<BITS, WIN> in0;
+  dense_fetch<BITS, WIN>(a, rs, src0, src1, wv, in0);
+  __builtin_amdgcn_sched_barrier(0);
+  AttnFrags<BITS> f;
+  prologue_build<BITS>(a, praw, f);
+  AttnState s;
+  attn_state_init(s);
+  if constexpr (WIN) {
+#pragma unroll 1
+    for (int G = wv; G < n_groups; G += kW) {  // wave-uniform
+      group_consume<BITS, WIN>(a, f, in0, s);
+      dense_fetch<BITS, WIN>(a, rs, src0, src1, G + kW, in0);
+    }
+  } else {
+    GroupIn<BITS, WIN> in1;
+    __builtin_amdgcn_sched_barrier(0);
+    dense_fetch<BITS, WIN>(a, rs, src0, src1, wv + kW, in1);
+    __builtin_amdgcn_sched_barrier(0);
+    // Both buffers are decoded on every pass, so that no load is used only under a branch (the
+    // compiler would move it there, after the wait it was meant to overlap).  A group past the split
+    // has no sources and changes nothing (all keys masked: the state's factor is exactly 1).
+#pragma unroll 1
+    for (int G = wv; G < n_groups; G += 2 * kW) {  // wave-uniform
+      group_consume<BITS, WIN>(a, f, in0, s);
+      __builtin_amdgcn_sched_barrier(0);
+      dense_fetch<BITS, WIN>(a, rs, src0, src1, G + 2 * kW, in0);
+      __builtin_amdgcn_sched_barrier(0);
+      group_consume<BITS, WIN>(a, f, in1, s);
+      __builtin_amdgcn_sched_barrier(0);
+      dense_fetch<BITS, WIN>(a, rs, src0, src1, G + 3 * kW, in1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  attend_finish<NW>(a, b, split, lds, s);
+}
+
 // One row (or one split of a long row) per workgroup of 64 * NW threads.
 //
 // Workgroups are dispatched round-robin over the 8 XCDs (linear id L on XCD L % 8), each with its
@@ -639,6 +769,20 @@ __global__ __launch_bounds__(64 * NW) void quant_attn_mfma_kernel(QAttnMfmaArgs 
     split = w % nx;
   }
   attend_row<BITS, NW>(a, row, static_cast<int>(split), lds);
+}
+
+// Decode rows over every block (T = 1, no selection, no counts): attend_dense, one workgroup of
+// 512 threads per (split, row).
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void quant_attn_dense_kernel(QAttnMfmaArgs a) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int64_t row = blockIdx.y;
+  const int split = static_cast<int>(blockIdx.x);
+  const bool has_win = static_cast<int64_t>(split + 1) * a.split_src > a.n_comp && a.Wt > 0;  // workgroup-uniform
+  if (has_win)
+    attend_dense<BITS, kWaves, true>(a, row, split, lds);
+  else
+    attend_dense<BITS, kWaves, false>(a, row, split, lds);
 }
 
 }  // namespace qattn

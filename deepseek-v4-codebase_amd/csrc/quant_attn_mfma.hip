@@ -106,9 +106,13 @@ int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* s
   a.Wt = Wt;
   a.S = S;
   a.K = K;
-  a.n_comp = all_blocks ? S : K;
+  a.n_comp = all_blocks ? std::min(K, S) : K;
   a.n_src = a.n_comp + Wt;  // an upper bound of every row's sources
   a.H = static_cast<int>(H);
+  // decode rows over every block without counts take the dense kernel (its buffer ranges, one cache
+  // row's codes and window entries, must stay below 2^31 bytes)
+  const bool dense = T == 1 && all_blocks && !vis && !wstart && !wlen &&
+                     S * (bits == 8 ? kD : kD / 2) < (int64_t{1} << 31) && Wt * kD * 2 < (int64_t{1} << 31);
   a.split_src = static_cast<int>(split_sources(rows, a.n_src));
   const int64_t n_split = a.n_src > 0 ? ceil_div(a.n_src, static_cast<int64_t>(a.split_src)) : 1;
   if (n_split > kMaxCombineSplits || rows > 65535)
@@ -122,12 +126,13 @@ int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* s
   a.part = static_cast<float*>(ws);
   a.out = static_cast<uint16_t*>(out);
   // 4 waves per workgroup once the launch has >= 1024 workgroups (prefill rows), else 8
-  const bool narrow = rows * n_split >= 1024;
-  auto fn = narrow ? (bits == 8 ? quant_attn_mfma_kernel<8, 4> : quant_attn_mfma_kernel<4, 4>)
+  const bool narrow = !dense && rows * n_split >= 1024;
+  auto fn = dense ? (bits == 8 ? quant_attn_dense_kernel<8> : quant_attn_dense_kernel<4>)
+          : narrow ? (bits == 8 ? quant_attn_mfma_kernel<8, 4> : quant_attn_mfma_kernel<4, 4>)
                    : (bits == 8 ? quant_attn_mfma_kernel<8, 8> : quant_attn_mfma_kernel<4, 8>);
   const size_t lds = narrow ? QLay<4>::bytes : QLay<8>::bytes;
-  static std::once_flag once[4];
-  std::call_once(once[(bits == 8 ? 2 : 0) + (narrow ? 1 : 0)], [&] {
+  static std::once_flag once[6];
+  std::call_once(once[(bits == 8 ? 3 : 0) + (dense ? 2 : narrow ? 1 : 0)], [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                               static_cast<int>(lds));
   });

@@ -167,7 +167,7 @@ __global__ __launch_bounds__(kThreads) void quant_attn_partial_kernel(QAttnArgs 
   const int64_t b = blockIdx.y;
   const int tile = blockIdx.x;
   const bool comp = tile < a.n_comp_tiles;
-  const int64_t n_src = comp ? (a.sel ? a.K : a.S) : a.W;
+  const int64_t n_src = comp ? a.K : a.W;  // (without sel: blocks 0 .. K-1 in order)
   const int64_t j0 = static_cast<int64_t>(comp ? tile : tile - a.n_comp_tiles) * ts;
   const int nt = static_cast<int>(min<int64_t>(ts, n_src - j0));
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -456,13 +456,13 @@ extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const
   if (B < 0 || H <= 0 || S < 0 || W < 0) return fail(AEKV_ERR_SHAPE, "%s: bad sizes", who);
   if (H * D > 4096) return fail(AEKV_ERR_UNSUPPORTED, "%s: H*D=%lld exceeds 4096", who, (long long)(H * D));
   if (B > 65535) return fail(AEKV_ERR_UNSUPPORTED, "%s: B exceeds 65535", who);
-  const bool all_blocks = n_sel < 0;  // HCA: every block in order
+  // in order: every block (n_sel < 0, HCA) or, without sel, the first n_sel blocks of each row
+  const bool all_blocks = n_sel < 0 || !sel;
   const int64_t K = all_blocks ? 0 : n_sel;
-  const int64_t n_comp = all_blocks ? S : K;
+  const int64_t n_comp = n_sel < 0 ? S : (all_blocks ? std::min(n_sel, S) : K);
   const QLayout l = qlayout(B, H, D, n_comp, W);
   if (B == 0) return AEKV_OK;
-  if (!q || !sink || !diag || !out || (n_comp > 0 && (!codes || !scale)) || (W > 0 && !window) ||
-      (K > 0 && !sel))
+  if (!q || !sink || !diag || !out || (n_comp > 0 && (!codes || !scale)) || (W > 0 && !window))
     return fail(AEKV_ERR_VALUE, "%s: null pointer", who);
   if (l.n_tiles == 0) {
     // no sources: every weight is zero -> out = 0 (serving.py:451-452)
@@ -476,8 +476,8 @@ extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const
   if (quant_attn_mfma_supported(H, D) && quant_attn_mfma_fits(B, n_comp + W) && use_specialised_codec() &&
       is_aligned(q, 16) && is_aligned(out, 8) && is_aligned(ws, 16) &&
       is_aligned(diag, 16) && (n_comp == 0 || is_aligned(codes, 16)) && (W == 0 || is_aligned(window, 16)))
-    return launch_quant_attn_mfma(q, codes, scale, sel, window, sink, diag, B, H, S, K, all_blocks, W, bits,
-                                  softmax_scale, ws, out, as_stream(stream), who);
+    return launch_quant_attn_mfma(q, codes, scale, sel, window, sink, diag, B, H, S, all_blocks ? n_comp : K,
+                                  all_blocks, W, bits, softmax_scale, ws, out, as_stream(stream), who);
   if (l.n_tiles > 65535) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many source tiles", who);
   QAttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
@@ -488,7 +488,7 @@ extern "C" int aekv_quant_sink_attention(const void* q, const void* codes, const
   a.sink = sink;
   a.diag = diag;
   a.S = S;
-  a.K = K;
+  a.K = all_blocks ? n_comp : K;
   a.W = W;
   a.H = static_cast<int>(H);
   a.ts = l.ts;
@@ -565,7 +565,8 @@ extern "C" int aekv_quant_prefill_attention(const void* q, const void* codes, co
     return fail(AEKV_ERR_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", who, need, ws_bytes);
   // without per-target window slices every target sees the whole [0, Wt) window
   return launch_quant_attn_mfma_rows(q, codes, scale, sel, visible, window, win_start, win_len, sink, diag, B * T, T,
-                                     H, S, K, all_blocks, Wt, bits, softmax_scale, ws, out, as_stream(stream), who);
+                                     H, S, n_comp, all_blocks, Wt, bits, softmax_scale, ws, out, as_stream(stream),
+                                     who);
 }
 
 extern "C" int aekv_hca_compress(const void* c, const void* z, int32_t dtype, int64_t B, int64_t M, int64_t D, void* out,

@@ -191,7 +191,9 @@ size_t aekv_sink_attention_workspace_size(int32_t dtype, int64_t B, int64_t T, i
  * a bf16 sliding window (the serving engine's decode step, dequantise + gather + concat + attend
  * fused):
  *   q [B,H,D] bf16; codes [B,S,D or D/2] + scale [B,S]; sel [B,n_sel] int64 block indices
- *   (n_sel < 0: all S blocks in order, i.e. HCA, sel ignored; entries outside [0,S) are skipped);
+ *   (n_sel < 0: all S blocks in order, i.e. HCA, sel ignored; sel NULL with n_sel >= 0: the first
+ *   min(n_sel, S) blocks of each row in order, S then being the row stride of codes and scale, e.g. a
+ *   ring's storage holding n_sel valid blocks; entries outside [0,S) are skipped);
  *   window [B,W,D] bf16 (W may be 0); sink fp32 [H]; out [B,H,D] bf16.
  *   Sources = [dequant(blocks[sel]), window]; K = V = source (aether_2b/serving.py:52-53).
  * Gathered code rows are dequantised on load to the bf16 values the engine attends (its bf16

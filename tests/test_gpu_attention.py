@@ -203,6 +203,30 @@ def test_split_rows_odd_row_head_count(dev, B, H):
     _close(got.view(B, H, D), _oracle_quant(pq, codes, scale, None, q, win, sink, sm), QUANT_RTOL, QUANT_ATOL)
 
 
+@pytest.mark.parametrize("S,W,bits", [
+    (0, 5, 4),      # window only
+    (37, 0, 8),     # blocks only, one partial group
+    (70, 3, 8),     # one piece holding blocks, then window rows, in one group
+    (1000, 40, 4),  # two pieces, the second holding the last blocks and the window
+    (1023, 1, 4),   # the one window row alone in the second piece's last group
+    (600, 200, 8),  # window rows spread over several groups and waves
+])
+def test_every_block_decode_rows_edges(dev, S, W, bits):
+    # decode rows over every block with no per-row counts take the dense kernel: every lane issues
+    # its loads whatever its source, reading past the buffer ranges (zeros) where it has none
+    B, H, D = 3, 12, 128
+    pq, codes, scale, q, win, sink = _quant_inputs(dev, B, H, D, max(S, 1), max(W, 1), bits, 300 + S + W)
+    codes, scale = codes[:, :S].contiguous(), scale[:, :S].contiguous()
+    win = win[:, :W].contiguous() if W else None
+    sm = D ** -0.5
+    print(f"every-block decode S={S} W={W} bits={bits}", flush=True)
+    got = quant_sink_attention(q, codes, scale, None, win, sink, sm, quant=pq)
+    want = O.quant_attention(to_np_f32(q).reshape(B, H, D), codes.cpu().numpy(), scale.cpu().numpy(), None,
+                             np.zeros((B, 0, D), np.float32) if win is None else to_np_f32(win), to_np_f32(sink),
+                             O.diag(42, D), bits, sm)
+    _close(got.view(B, H, D), want, QUANT_RTOL, QUANT_ATOL)
+
+
 @pytest.mark.parametrize("S", [130400, 130900])
 def test_quant_attention_most_pieces(dev, S):
     # one row, S blocks + 128 window rows in pieces of 512: 255 pieces, and 256 (the launch limit);
