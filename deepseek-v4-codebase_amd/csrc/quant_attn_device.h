@@ -365,6 +365,8 @@ __device__ __forceinline__ void group_consume(const QAttnMfmaArgs& a, const Attn
   const auto& cw = in.cw;
   const float (&sraw)[2] = in.sraw;
   const auto& wv2 = in.wv2;
+  // a group with no source at all (past the end of a piece) changes nothing
+  if (__builtin_amdgcn_ballot_w64(kind[0] != 0 || kind[1] != 0) == 0) return;
   const float kscale_unit = (BITS == 4 ? 1.0f / 16.0f : 1.0f) * a.wscale;
   bf16x8_t kf[2][4];
   bool okk[2];
