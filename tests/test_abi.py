@@ -252,3 +252,30 @@ def test_fast_call_module_shares_the_library_and_its_checks(lib):
     with pytest.raises(TypeError):
         _fastcall.aekv_quant_sink_attention(fake)
     assert L.hot("aekv_sparse_sink_attention_ws") is _fastcall.aekv_sparse_sink_attention_ws
+
+
+def test_ring_prefix_views_are_recognised_and_others_are_not():
+    """quant_sink_attention reads codes / scales in place when they are the first n rows of
+    [B, S, .] storages (a CodeRing's data / scale views): the row stride S goes to the library with
+    n_sel = n and no selection.  Anything else is copied to a compact tensor first."""
+    from aetherkv.decode import _prefix_rows
+
+    B, cap, rb = 3, 40, 64
+    codes = torch.zeros(B, cap, rb, dtype=torch.uint8)
+    scale3 = torch.zeros(B, cap, 1, dtype=torch.float32)
+    scale2 = torch.zeros(B, cap, dtype=torch.float32)
+    assert _prefix_rows(codes[:, :25], scale3[:, :25]) == cap
+    assert _prefix_rows(codes[:, :25], scale2[:, :25]) == cap
+    assert _prefix_rows(codes[:, :1], scale3[:, :1]) == cap
+    assert _prefix_rows(codes, scale3) == cap  # the whole storage (contiguous callers copy nothing anyway)
+    # rows 5..29 of every storage row work the same way: the pointers are those of row 5
+    assert _prefix_rows(codes[:, 5:30], scale3[:, 5:30]) == cap
+    # scales of another stride, a column slice, wrong dtype or mismatched lengths are refused
+    assert _prefix_rows(codes[:, :25], torch.zeros(B, 2 * cap, 1)[:, :25]) is None
+    assert _prefix_rows(codes[:, :25, :32], scale3[:, :25]) is None
+    assert _prefix_rows(codes[:, :25], scale3[:, :25].to(torch.float64)) is None
+    assert _prefix_rows(codes[:, :25], scale3[:, :24]) is None
+    assert _prefix_rows(codes[:, ::2], scale3[:, ::2]) is None
+    # batch-strided views whose row stride is not a multiple of the row are refused
+    odd = torch.zeros(B * (cap * rb + 8), dtype=torch.uint8).as_strided((B, 25, rb), (cap * rb + 8, rb, 1))
+    assert _prefix_rows(odd, scale3[:, :25]) is None
