@@ -487,3 +487,22 @@ def test_emit_block_pooling_reduces_to_hca_compress_and_plain_values():
     np.testing.assert_allclose(gf, exact, rtol=2e-2, atol=2e-3)
     one = O.emit_block(_bits16(c[:, :1]), _bits16(z[:, :1]))
     np.testing.assert_array_equal(one, _bits16(c[:, 0]))
+
+
+def test_diag_signs_match_the_committed_fixture():
+    """The d = 64 and d = 128 diagonals of the engine's seed, frozen in tests/golden (written by
+    tests/golden/make_diag_signs.py from torch's CPU generator, as turbo_quant.py:111-121 draws them):
+    the oracle's MT19937 restatement and the library's host generator both reproduce them."""
+    import json
+    import ctypes
+    from pathlib import Path
+
+    import aetherkv._lib as L
+
+    fx = json.loads((Path(__file__).parent / "golden" / "diag_signs_seed42.json").read_text())
+    for d in (64, 128):
+        want = np.array([1.0 if c == "+" else -1.0 for c in fx["signs"][str(d)]], np.float32)
+        np.testing.assert_array_equal(O.diag(fx["seed"], d), want)
+        host = np.empty(d, np.float32)
+        assert L.lib().aekv_tq_diag(fx["seed"], d, host.ctypes.data_as(ctypes.c_void_p)) == L.OK
+        np.testing.assert_array_equal(host, want)
