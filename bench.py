@@ -29,6 +29,7 @@ sequence of the step, on the first 8 rows of the config.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -186,8 +187,14 @@ def bench_encode(args, dev, out):
     c2, s2 = torch.empty_like(codes), torch.empty_like(scale)
     c2p, s2p = L.ptr(c2), L.ptr(s2)
 
+    plib = ctypes.CDLL(str(Path(L.__file__).with_name("libaetherkv_probe.so")))
+    plib.aekv_stream_probe.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+    plib.aekv_stream_probe.restype = ctypes.c_int
+
     def probe():
-        L.check(lib.aekv_stream_probe(xp, N_VEC2, c2p, s2p, stream), "stream probe")
+        if plib.aekv_stream_probe(xp, N_VEC2, c2p, s2p, stream) != 0:
+            raise RuntimeError("aekv_stream_probe rejected its arguments or failed to launch")
 
     ms_p = timed(probe, args.steps, args.warmup)
     out["stream_ceiling_gbs"] = ENC_BYTES / ms_p / 1e6

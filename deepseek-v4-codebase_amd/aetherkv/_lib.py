@@ -35,7 +35,7 @@ SYMBOLS = (
     "aekv_set_flash_rows", "aekv_emit_block", "aekv_csa_prefill_indexer_topk_quant", "aekv_quant_prefill_workspace_size",
     "aekv_quant_prefill_attention", "aekv_rope_rmsnorm", "aekv_csa_indexer_topk_quant_noalloc",
     "aekv_csa_decode_workspace_size", "aekv_csa_decode_quant", "aekv_sparse_sink_attention_ws",
-    "aekv_tiled_prefill_attention_ws", "aekv_sink_attention_workspace_size", "aekv_stream_probe",
+    "aekv_tiled_prefill_attention_ws", "aekv_sink_attention_workspace_size",
 )
 
 # size of the static device scratch behind aekv_csa_indexer_topk_quant_noalloc (AEKV_STATIC_SCRATCH_BYTES)
@@ -102,7 +102,6 @@ def lib() -> ctypes.CDLL:
         "aekv_tiled_prefill_attention_ws": (
             [P, P, P, I64_, I32_, I64_, I64_, I64_, I64_, I64_, F, I32_, P, SZ, P, P], ctypes.c_int),
         "aekv_sink_attention_workspace_size": ([I32_, I64_, I64_, I64_, I64_, I64_, I64_], SZ),
-        "aekv_stream_probe": ([P, I64_, P, P, P], ctypes.c_int),
     }
     for name, (argtypes, restype) in sig.items():
         fn = getattr(L, name)

@@ -13,7 +13,9 @@ Flags that matter for parity:
 
 Beside it, gcc builds ``aetherkv/_fastcall*.so`` from ``aetherkv/_fastcall.c``: CPython fast-call
 functions over the same C ABI for the entry points called once per token (linked against
-libaetherkv.so through $ORIGIN, so both share one loaded library).
+libaetherkv.so through $ORIGIN, so both share one loaded library), and hipcc builds
+``aetherkv/libaetherkv_probe.so`` from ``probe/stream_probe.hip``: bench.py's streaming probe, kept
+out of the product library.
 """
 from __future__ import annotations
 
@@ -82,9 +84,25 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
     build_fastcall()
+    build_probe()
     if verbose:
         print(f"built {LIB}", file=sys.stderr)
     return LIB
+
+
+PROBE_SRC = ROOT / "probe" / "stream_probe.hip"
+PROBE_LIB = PKG / "libaetherkv_probe.so"
+
+
+def build_probe() -> Path:
+    """hipcc the measurement probe into its own library (bench.py loads it; the product does not)."""
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *COMMON_FLAGS, "-shared", "-x", "hip", str(PROBE_SRC), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"probe build failed:\n{res.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 FASTCALL_SRC = PKG / "_fastcall.c"

@@ -1,5 +1,6 @@
-// Streaming ceiling for the cfg2 encode's traffic shape (a measurement utility for bench.py; no
-// counterpart in the reference).
+// Streaming ceiling for the cfg2 encode's traffic shape: a measurement utility for bench.py with
+// no counterpart in the reference, built into its own library (libaetherkv_probe.so, declared in
+// include/aetherkv_probe.h) so that the product library exports only the path's entry points.
 //
 // stream_probe_kernel moves exactly the encode's bytes with the encode's access pattern and
 // almost no arithmetic: one wave per group of 16 vectors of 128 bf16 (lane 4v + g reads the 64
@@ -7,9 +8,12 @@
 // vector) and 4 bytes per vector (the scale), both with non-temporal stores.  The outputs are xor
 // folds of the inputs, so no load can be dropped.  Its time is the box's practical HBM ceiling
 // for this stream, beside the 8 TB/s datasheet peak.
-#include "aekv_common.h"
+#include <hip/hip_runtime.h>
 
-namespace aekv {
+#include <cstdint>
+
+#include "aetherkv_probe.h"
+
 namespace {
 
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
@@ -37,20 +41,17 @@ __global__ __launch_bounds__(256) void stream_probe_kernel(const uint4* __restri
 }
 
 }  // namespace
-}  // namespace aekv
-
-using namespace aekv;
 
 extern "C" int aekv_stream_probe(const void* x, int64_t n_vec, void* codes, float* scale, void* stream) {
-  const char* who = "aekv_stream_probe";
-  if (n_vec < 0) return fail(AEKV_ERR_SHAPE, "%s: negative size", who);
-  if (n_vec == 0) return AEKV_OK;
-  if (!x || !codes || !scale) return fail(AEKV_ERR_VALUE, "%s: null pointer", who);
-  if (!is_aligned(x, 16) || !is_aligned(codes, 16) || !is_aligned(scale, 4))
-    return fail(AEKV_ERR_ALIGN, "%s: misaligned pointer", who);
-  const int64_t blocks = ceil_div(ceil_div(n_vec, 16), 4);
-  if (blocks > 0x7fffffff) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many vectors", who);
-  hipLaunchKernelGGL(stream_probe_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, as_stream(stream),
-                     static_cast<const uint4*>(x), n_vec, static_cast<uint4*>(codes), scale);
-  return check_launch(who);
+  auto aligned = [](const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; };
+  if (n_vec < 0) return AEKV_PROBE_ERR_ARGS;
+  if (n_vec == 0) return AEKV_PROBE_OK;
+  if (!x || !codes || !scale || !aligned(x, 16) || !aligned(codes, 16) || !aligned(scale, 4))
+    return AEKV_PROBE_ERR_ARGS;
+  const int64_t blocks = ((n_vec + 15) / 16 + 3) / 4;
+  if (blocks > 0x7fffffff) return AEKV_PROBE_ERR_ARGS;
+  hipLaunchKernelGGL(stream_probe_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint4*>(x), n_vec,
+                     static_cast<uint4*>(codes), scale);
+  return hipGetLastError() == hipSuccess ? AEKV_PROBE_OK : AEKV_PROBE_ERR_LAUNCH;
 }

@@ -290,14 +290,6 @@ int aekv_tiled_prefill_attention_ws(const void* q, const void* kv, const void* s
                                     float softmax_scale, int32_t tile_size, void* ws, size_t ws_bytes, void* out,
                                     void* stream);
 
-/* ---- measurement utilities (no counterpart in the reference; not used by any entry above) ---- */
-/* Measurement utility, no counterpart in the reference: moves the bytes of a 4-bit D = 128 bf16
- * encode of n_vec vectors (x [n_vec, 128] bf16 in; codes [n_vec, 64] bytes and scale [n_vec] out)
- * with the encode kernel's access pattern and non-temporal stores but no transform (the outputs are
- * xor folds of the inputs).  bench.py times it beside the encode as the practical streaming
- * ceiling of that traffic.  x and codes 16-byte aligned. */
-int aekv_stream_probe(const void* x, int64_t n_vec, void* codes, float* scale, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,27 @@ def test_every_declared_symbol_is_exported(lib):
     assert set(names) == set(L.SYMBOLS)
 
 
+def test_probe_library_exports_its_header_and_nothing_leaks_into_the_product():
+    """bench.py's streaming probe lives in libaetherkv_probe.so (include/aetherkv_probe.h), not in
+    the product library, and rejects bad arguments before enqueuing anything."""
+    text = (ROOT / "include" / "aetherkv_probe.h").read_text()
+    names = sorted(set(re.findall(r"^\s*int\s+(aekv_\w+)\(", text, flags=re.M)))
+    assert names == ["aekv_stream_probe"]
+    path = L.LIB_PATH.with_name("libaetherkv_probe.so")
+    if not path.exists():
+        pytest.fail("libaetherkv_probe.so is not built (run __graft_entry__.build())")
+    plib = ctypes.CDLL(str(path))
+    for n in names:
+        assert hasattr(plib, n), n
+    assert "aekv_stream_probe" not in L.SYMBOLS
+    plib.aekv_stream_probe.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+    assert plib.aekv_stream_probe(None, -1, None, None, None) == 1
+    assert plib.aekv_stream_probe(None, 0, None, None, None) == 0
+    assert plib.aekv_stream_probe(None, 16, None, None, None) == 1
+    assert plib.aekv_stream_probe(ctypes.c_void_p(0x10008), 16, FAKE, FAKE, None) == 1  # x not 16-byte aligned
+
+
 def test_version_and_limits(lib):
     assert b"gfx950" in lib.aekv_version()
     assert lib.aekv_max_head_dim() == 512
