@@ -833,6 +833,9 @@ def main():
                        "bytes_per_step": ENC_BYTES},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                         "traffic_from": "profiles/tq_encode_cfg2_traffic.json: rocprofv3 --pmc FETCH_SIZE and "
+                                         "WRITE_SIZE passes over this kernel at this workload, scaled by the factors "
+                                         "that make a copy kernel's counters read its size (not measured in this run)",
                          "kernel": "tq_encode4_d128_bf16_kernel"},
         })
         secondary["tq_decode_cfg2"] = {"ms": round(res["decode_ms"], 5),
