@@ -82,6 +82,22 @@ int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* s
                                 void* out, hipStream_t st, const char* who);
 
 // ---- device helpers ------------------------------------------------------------------------
+// Requests every 64-byte line of the kernel's argument block in one scalar-memory round.  The
+// compiler loads an argument where it is first needed, often behind a branch on an argument loaded
+// before it, and each such load is a memory round trip of its own while the argument block is not
+// cached (a graph replayed over more data than the caches hold); after this call they hit the
+// scalar cache.  NBYTES: the size of the kernel's arguments.
+template <int NBYTES>
+__device__ __forceinline__ void touch_kernargs() {
+  typedef const __attribute__((address_space(4))) uint32_t karg_u32;
+  karg_u32* p = (karg_u32*)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t v[(NBYTES + 63) / 64];
+#pragma unroll
+  for (int i = 0; i < (NBYTES + 63) / 64; ++i) v[i] = p[16 * i];
+#pragma unroll
+  for (int i = 0; i < (NBYTES + 63) / 64; ++i) asm volatile("" ::"s"(v[i]));
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __builtin_bit_cast(float, bits16 << 16); }
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));

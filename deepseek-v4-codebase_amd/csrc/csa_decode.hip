@@ -34,6 +34,7 @@ __global__ __launch_bounds__(kFusedThreads) void csa_decode_fused_kernel(idx::Mf
                                                                        int64_t* __restrict__ out_idx,
                                                                        float* __restrict__ out_score) {
   constexpr int NW = kFusedThreads / 64;
+  touch_kernargs<sizeof(ia) + sizeof(qa) + 2 * sizeof(void*)>();
   extern __shared__ __align__(16) unsigned char lds[];
   int32_t* sel_lds = reinterpret_cast<int32_t*>(lds + FusedLay::idx);
   const int b = blockIdx.x;
@@ -58,20 +59,25 @@ __global__ __launch_bounds__(kFusedThreads) void csa_decode_fused_kernel(idx::Mf
   qattn::AttnFrags<KV_BITS> f;
   qattn::AttnState st;
   qattn::attn_state_init(st);
-  bool window_done = false;
-  auto window = [&]() {
+  // the query fragments are built while the select waits for its slot maxima (they arrive with the
+  // query); the window rows, which arrive then too, are attended after the select, while the
+  // wave's first group of selected rows is requested, so that the select starts as soon as its
+  // maxima are in
+  bool built = false;
+  auto build = [&]() {
     qattn::prologue_build<KV_BITS>(qa, praw, f);
-    if (has_win) {
-      const bool okm[2] = {wok, false};
-      qattn::group_consume<KV_BITS>(qa, f, win_in, st, okm);
-    }
-    window_done = true;
+    built = true;
   };
-  const uint32_t kk = idx::select_row<kFusedThreads, kFusedCap>(ia, b, out_idx, out_score, sel_lds, window);
-  if (!window_done) window();  // a row with no visible block skips the select's memory rounds
-  __syncthreads();             // sel_lds
+  const uint32_t kk = idx::select_row<kFusedThreads, kFusedCap>(ia, b, out_idx, out_score, sel_lds, build);
+  if (!built) build();  // a row with no visible block skips the select's memory rounds
+  __syncthreads();      // sel_lds
+  auto window = [&]() {
+    const bool okm[2] = {wok, false};
+    qattn::group_consume<KV_BITS>(qa, f, win_in, st, okm);
+  };
   // the selected blocks, in the same state: wave w takes groups w, w + NW, ...
   const int n_groups = static_cast<int>((kk + qattn::kGroup - 1) / qattn::kGroup);
+  bool win_pending = has_win;  // wave-uniform
 #pragma unroll 1
   for (int G = wv; G < n_groups; G += NW) {
     qattn::SrcRef src[2];
@@ -84,9 +90,14 @@ __global__ __launch_bounds__(kFusedThreads) void csa_decode_fused_kernel(idx::Mf
     }
     qattn::GroupIn<KV_BITS, false> in;
     qattn::group_fetch<KV_BITS, false>(qa, b, src, nullptr, in);
+    if (win_pending) {
+      window();
+      win_pending = false;
+    }
     qattn::group_consume<KV_BITS, false>(qa, f, in, st);
   }
-  qattn::attend_finish<NW>(qa, b, 0, lds, st);
+  if (win_pending) window();  // a wave without a selected group
+  qattn::attend_finish<NW>(qa, b, 0, lds, st, f.sink);
 }
 
 }  // namespace

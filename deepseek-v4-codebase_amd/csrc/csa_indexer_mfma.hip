@@ -56,10 +56,9 @@ int launch_mfma_score(MfmaIdxArgs& a, const float* q, const float* w, const void
   if (!score) return fail(AEKV_ERR_UNSUPPORTED, "%s: no matrix-core indexer for IH=%d IC=%d", who, IH, IC);
   // workgroup rows: one per row, or one per kScoreTT targets of a key row
   const int64_t n_y = tt == 1 ? B : (B / T) * ceil_div(T, static_cast<int64_t>(tt));
-  // slot-group size of the score kernel (must match SPW there) and groups per wave: enough
-  // workgroups to fill the chip (~2048), at most 16 groups per wave
-  const int rb_bytes = bits == 8 ? IC : IC / 2;
-  const int64_t group_keys = 64 * (rb_bytes <= 32 ? 4 : (rb_bytes <= 64 ? 2 : 1));
+  // slot-group size of the score kernel and groups per wave: enough workgroups to fill the chip
+  // (~2048), at most 16 groups per wave
+  const int64_t group_keys = 64 * score_spw(bits, IC, tt);
   const int64_t groups_per_row = ceil_div(S, group_keys);
   int64_t gpw = (n_y * groups_per_row) / (4 * kScoreTargetWG);
   gpw = std::min<int64_t>(16, std::max<int64_t>(1, gpw));

@@ -53,6 +53,15 @@ constexpr int64_t kMaxKeys = int64_t(1) << 24;  // byte offsets within a key row
 constexpr int kScoreTT = 4;          // prefill rows sharing each key group in the score kernel
 constexpr int64_t kScoreTargetWG = 2048;  // score workgroups the launch aims for
 
+// Slots of 64 keys per score group (one group's codes per wave in registers): 256 keys of up to
+// 32 code bytes, 128 of 64, 64 of 128.  Decode rows (TT = 1) keep two groups in flight, of half
+// that size, so that the registers stay within eight waves per SIMD.
+__host__ __device__ constexpr int score_spw(int bits, int ic, int tt) {
+  const int rb = bits == 8 ? ic : ic / 2;
+  const int spw = rb <= 32 ? 4 : (rb <= 64 ? 2 : 1);
+  return tt == 1 && spw > 1 ? spw / 2 : spw;
+}
+
 typedef __attribute__((ext_vector_type(4))) int i32x4_t;
 
 __device__ __forceinline__ float softplus_f32(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
@@ -512,11 +521,13 @@ __device__ __forceinline__ float lane_score(const i32x4_t (&A)[NRB][KS], const i
 template <int BITS, int IC, int NRB, int TT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void
 idx_mfma_score_kernel(MfmaIdxArgs a) {
+  touch_kernargs<sizeof(a)>();
   constexpr int KS = IC / 64;
   constexpr int RB = BITS == 8 ? IC : IC / 2;        // code bytes per key
-  constexpr int SPW = RB <= 32 ? 4 : (RB <= 64 ? 2 : 1);
+  constexpr int SPW = score_spw(BITS, IC, TT);
   constexpr int LW = BITS == 8 ? 4 : 2;               // dwords per lane per k-step
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4;
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int64_t S = a.S;
 
   // this workgroup's rows: TT targets of key row kr (rows past the sequence's T are not scored)
@@ -596,16 +607,47 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
       gr.scl[s] = *reinterpret_cast<const float*>(srow + (!CLAMP || jo < lim ? static_cast<uint32_t>(jo) * 4u : 0u));
     }
   };
+  // Decode rows (TT == 1) read their codes and scales through buffer resources whose ranges end at
+  // the wave's last key (of the S stored, so that the first request does not wait for the row's
+  // count): a load past it returns zeros without touching memory, so the next group is requested
+  // unconditionally, while the current one is scored.
+  const int64_t wkeys = max<int64_t>(0, min<int64_t>(wave_base + static_cast<int64_t>(a.gpw) * kGroupKeys, S) - wave_base);
+  const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(crow + (wkeys > 0 ? wave_base * RB : 0)), 0, static_cast<int>(wkeys * RB), 0x00020000);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(srow + (wkeys > 0 ? wave_base * 4 : 0)), 0, static_cast<int>(wkeys * 4), 0x00020000);
+  auto fetch = [&](const int gi, GroupRaw& gr) {  // group gi of the wave (TT == 1)
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+#pragma unroll
+      for (int tq = 0; tq < 4; ++tq) {
+        const uint32_t j = static_cast<uint32_t>(gi * kGroupKeys + 64 * s + 16 * tq + (lane & 15));
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          if constexpr (BITS == 8) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(crs, j * RB + 64 * ks + 16 * g, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) gr.raw[s][tq][ks][e] = v[e];
+          } else {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(crs, j * RB + 32 * ks + 8 * g, 0, 0);
+            gr.raw[s][tq][ks][0] = v[0];
+            gr.raw[s][tq][ks][1] = v[1];
+          }
+        }
+      }
+      gr.scl[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                srs, static_cast<uint32_t>(gi * kGroupKeys + 64 * s + lane) * 4u, 0, 0));
+    }
+  };
   // The first memory round: the rows' counts (above), their queries and, for single-target rows, the
   // wave's first key group, which does not depend on the query (keys past S read key 0; those past
   // a row's count are dropped when scored).
-  const bool preload = TT == 1 && a.gpw > 1;  // wave-uniform
-  GroupRaw g0;
+  GroupRaw b0, b1;  // (TT == 1) the groups in flight
   {
     QueryRaw<IC, NRB> raw[TT];
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) query_loads<IC, NRB>(a, static_cast<int>(row[tt]), raw[tt]);
-    if (preload && wave_base < S) load_group(static_cast<int>(wave_base), std::true_type{}, static_cast<int>(S), g0);
+    if constexpr (TT == 1) fetch(0, b0);
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
       if (tt > 0) __syncthreads();  // the previous row's fragments have been read out of LDS
@@ -639,31 +681,51 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
       }
     }
   };
-  auto group = [&](const int kb, auto full_c) {
-    GroupRaw gr;
-    // keys past a row's count read key 0 (nv_max >= 1 here) and are dropped
-    load_group(kb, std::integral_constant<bool, !decltype(full_c)::value>{}, nv_maxi, gr);
-    score_group(kb, full_c, gr);
-  };
+  if constexpr (TT == 1) {
+    // two groups in flight: group gi + 2 is requested as soon as group gi is scored (the
+    // scheduling barriers keep each request batch in program order)
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    auto consume = [&](const int gi, const GroupRaw& gr) {
+      const int64_t kb64 = wave_base + static_cast<int64_t>(gi) * kGroupKeys;
+      if (gi >= a.gpw || kb64 >= nv_max) return;  // wave-uniform; past gpw are the next wave's keys
+      if (kb64 + kGroupKeys <= nv_mini) score_group(static_cast<int>(kb64), std::true_type{}, gr);
+      else score_group(static_cast<int>(kb64), std::false_type{}, gr);
+    };
+    // the first group's operands are built here, not hoisted above the query phase, where they
+    // would hold registers
+#pragma unroll
+    for (int s2 = 0; s2 < SPW; ++s2)
+#pragma unroll
+      for (int tq = 0; tq < 4; ++tq)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int w = 0; w < LW; ++w) asm volatile("" : "+v"(b0.raw[s2][tq][ks][w]));
 #pragma unroll 1
-  for (int gi = 0; gi < a.gpw; ++gi) {
-    const int64_t kb64 = wave_base + gi * kGroupKeys;
-    if (kb64 >= nv_max) break;  // wave-uniform
-    const bool full = kb64 + kGroupKeys <= nv_mini;
-    if (preload && gi == 0) {
-      // the preloaded codes enter here (the operands built from them are not hoisted above the
-      // query phase, where they would hold registers)
-#pragma unroll
-      for (int s = 0; s < SPW; ++s)
-#pragma unroll
-        for (int tq = 0; tq < 4; ++tq)
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int w = 0; w < LW; ++w) asm volatile("" : "+v"(g0.raw[s][tq][ks][w]));
-      if (full) score_group(static_cast<int>(kb64), std::true_type{}, g0);
-      else score_group(static_cast<int>(kb64), std::false_type{}, g0);
-    } else {
+    for (int gi = 0; gi < a.gpw; gi += 2) {
+      consume(gi, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(gi + 2, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(gi + 1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(gi + 3, b1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    auto group = [&](const int kb, auto full_c) {
+      GroupRaw gr;
+      // keys past a row's count read key 0 (nv_max >= 1 here) and are dropped
+      load_group(kb, std::integral_constant<bool, !decltype(full_c)::value>{}, nv_maxi, gr);
+      score_group(kb, full_c, gr);
+    };
+#pragma unroll 1
+    for (int gi = 0; gi < a.gpw; ++gi) {
+      const int64_t kb64 = wave_base + gi * kGroupKeys;
+      if (kb64 >= nv_max) break;  // wave-uniform
+      const bool full = kb64 + kGroupKeys <= nv_mini;
       if (full) group(static_cast<int>(kb64), std::true_type{});
       else group(static_cast<int>(kb64), std::false_type{});
     }
@@ -1047,6 +1109,7 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
 template <int NT, int CAP>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 512 ? 6 : 1))) void idx_mfma_final_kernel(
     MfmaIdxArgs a, int64_t* __restrict__ out_idx, float* __restrict__ out_score) {
+  touch_kernargs<sizeof(a) + 2 * sizeof(void*)>();
   select_row<NT, CAP>(a, blockIdx.x, out_idx, out_score, nullptr);
 }
 

@@ -174,45 +174,55 @@ struct AttnFrags {
   bf16x8_t qb[4];
   i32x4_t hA[4];
   bf16x8_t esel[2];
+  float sink;  // the sink of head threadIdx.x (threads below H; 0 for a split of several)
 };
 
-// The prologue's loads: the diagonal at the lane's 32 dims and the query row of its head.
+// The prologue's loads: two entries of the diagonal (dims lane and 64 + lane; the wave's ballots
+// of their signs give every lane the signs of its own dims), the query row of the lane's head, and
+// the sink the merge needs at the end (requested here so that the merge does not wait for it).
+// Each load instruction of a wave costs the CU's memory pipeline time per lane, so the diagonal
+// is not read as 32 dims per lane.
 struct PrologueRaw {
-  float4 dg[4][2];
+  float dv[2];
   uint2 lo[4], hi[4];
+  float sink;
 };
 
 __device__ __forceinline__ void prologue_loads(const QAttnMfmaArgs& a, const int64_t b, PrologueRaw& r) {
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
   // The lane's 32 dims, for every key it holds: element j of k-step ks (bf16x8) is dim
-  // 16*(2ks + (j >> 2)) + 4g + (j & 3).  Every load (the diagonal at those dims, the query row of
-  // head c16) is issued before any is used: one memory round.  Lanes past the heads read head 0's
-  // row and use zeros.
+  // 16*(2ks + (j >> 2)) + 4g + (j & 3).  Every load (the diagonal, the query row of head c16) is
+  // issued before any is used: one memory round.  Lanes past the heads read head 0's row and use
+  // zeros.
   const uint16_t* qr = a.q + (b * a.H + (c16 < a.H ? c16 : 0)) * kD + 4 * g;
+  r.dv[0] = a.diag[lane];
+  r.dv[1] = a.diag[64 + lane];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-    for (int hv = 0; hv < 2; ++hv) r.dg[ks][hv] = *reinterpret_cast<const float4*>(a.diag + 16 * (2 * ks + hv) + 4 * g);
     r.lo[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks));
     r.hi[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks + 1));
   }
+  const int th = static_cast<int>(threadIdx.x) < a.H ? static_cast<int>(threadIdx.x) : 0;
+  r.sink = a.n_split == 1 ? a.sink[th] : 0.0f;
 }
 
 template <int BITS>
 __device__ __forceinline__ void prologue_build(const QAttnMfmaArgs& a, const PrologueRaw& r, AttnFrags<BITS>& f) {
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
   const bool has_head = c16 < a.H;
-  const float4 (&dg)[4][2] = r.dg;
   const uint2 (&lo)[4] = r.lo;
   const uint2 (&hi)[4] = r.hi;
-  // dsign: the diagonal's sign bits for the lane's dims, per packed bf16 pair (dword e of k-step ks)
+  f.sink = r.sink;
+  // dsign: the diagonal's sign bits for the lane's dims, per packed bf16 pair (dword e of k-step
+  // ks), from the signs of all 128 dims (bit d of neg[d >> 6], every lane of the wave active)
+  const uint64_t neg[2] = {__builtin_amdgcn_ballot_w64(r.dv[0] < 0.0f), __builtin_amdgcn_ballot_w64(r.dv[1] < 0.0f)};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
     for (int hv = 0; hv < 2; ++hv) {
-      const float4 d = dg[ks][hv];
-      f.dsign[ks][2 * hv] = (d.x < 0.0f ? 0x8000u : 0u) | (d.y < 0.0f ? 0x80000000u : 0u);
-      f.dsign[ks][2 * hv + 1] = (d.z < 0.0f ? 0x8000u : 0u) | (d.w < 0.0f ? 0x80000000u : 0u);
+      const uint32_t nb = static_cast<uint32_t>(neg[ks >> 1] >> ((32 * (ks & 1) + 16 * hv + 4 * g) & 63));  // dims 0..3 of the four
+      f.dsign[ks][2 * hv] = ((nb & 1u) ? 0x8000u : 0u) | ((nb & 2u) ? 0x80000000u : 0u);
+      f.dsign[ks][2 * hv + 1] = ((nb & 4u) ? 0x8000u : 0u) | ((nb & 8u) ? 0x80000000u : 0u);
     }
   // queries (times the diagonal) as the B operand of S^T: lane (head c16), the lane's dims
 #pragma unroll
@@ -487,10 +497,11 @@ __device__ __forceinline__ void group_consume(const QAttnMfmaArgs& a, const Attn
 }
 
 // Merges the NW waves' states (and the sink, unless this is one split of several) and writes the
-// row's output, or its split result (max, sum, O) for the combine.
+// row's output, or its split result (max, sum, O) for the combine.  sink_h: the sink of head
+// threadIdx.x, requested with the prologue (AttnFrags::sink).
 template <int NW>
 __device__ __forceinline__ void attend_finish(const QAttnMfmaArgs& a, const int64_t b, const int split,
-                                              unsigned char* lds, const AttnState& s) {
+                                              unsigned char* lds, const AttnState& s, const float sink_h) {
   constexpr int kW = NW, kT = 64 * NW;
   using L = QLay<NW>;
   float* Ob = reinterpret_cast<float*>(lds + L::ob);    // [wave][head][kObStride]
@@ -510,10 +521,10 @@ __device__ __forceinline__ void attend_finish(const QAttnMfmaArgs& a, const int6
   // the normaliser L; the factors replace the maxima in stat, 1/L (or L for a split) is kept aside
   if (threadIdx.x < H) {
     const int h = threadIdx.x;
-    float M = a.n_split == 1 ? a.sink[h] : kNegInf;
+    float M = a.n_split == 1 ? sink_h : kNegInf;
 #pragma unroll
     for (int w = 0; w < kW; ++w) M = fmaxf(M, stat[(w * 16 + h) * 2]);
-    float Lsum = a.n_split == 1 ? __expf(a.sink[h] - M) : 0.0f;
+    float Lsum = a.n_split == 1 ? __expf(sink_h - M) : 0.0f;
 #pragma unroll
     for (int w = 0; w < kW; ++w) {
       const float mw = stat[(w * 16 + h) * 2];
@@ -610,7 +621,7 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
     }
   }
   // ---- merge the waves (and the sink, unless this is one split of several) ----
-  attend_finish<NW>(a, b, split, lds, s);
+  attend_finish<NW>(a, b, split, lds, s, f.sink);
 }
 
 
@@ -750,7 +761,7 @@ __device__ __forceinline__ void attend_dense(const QAttnMfmaArgs& a, const int64
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  attend_finish<NW>(a, b, split, lds, s);
+  attend_finish<NW>(a, b, split, lds, s, f.sink);
 }
 
 // One row (or one split of a long row) per workgroup of 64 * NW threads.
@@ -761,6 +772,7 @@ __device__ __forceinline__ void attend_dense(const QAttnMfmaArgs& a, const int64
 // i.e. whole sequences, whose code rows then stay in that XCD's L2 for all of their targets.
 template <int BITS, int NW>
 __global__ __launch_bounds__(64 * NW) void quant_attn_mfma_kernel(QAttnMfmaArgs a) {
+  touch_kernargs<sizeof(a)>();
   extern __shared__ __align__(16) unsigned char lds[];
   int64_t row = blockIdx.y, split = blockIdx.x;
   const uint32_t nx = gridDim.x, n_wg = nx * gridDim.y;
@@ -777,6 +789,7 @@ __global__ __launch_bounds__(64 * NW) void quant_attn_mfma_kernel(QAttnMfmaArgs 
 // 512 threads per (split, row).
 template <int BITS>
 __global__ __launch_bounds__(kThreads) void quant_attn_dense_kernel(QAttnMfmaArgs a) {
+  touch_kernargs<sizeof(a)>();
   extern __shared__ __align__(16) unsigned char lds[];
   const int64_t row = blockIdx.y;
   const int split = static_cast<int>(blockIdx.x);

@@ -17,6 +17,7 @@ constexpr int kMaxCombineSplits = 256;  // most source pieces per row
 // spread over as many CUs, instead of queueing their loads on a few.
 constexpr int kCombineThreads = 64;
 __global__ __launch_bounds__(kCombineThreads) void quant_attn_mfma_combine_kernel(QAttnMfmaArgs a, int64_t rows) {
+  touch_kernargs<sizeof(a) + sizeof(rows)>();
   constexpr int kChunk = 8;
   const int H = a.H, ns = a.n_split;
   const int64_t rh = static_cast<int64_t>(blockIdx.x) * (kCombineThreads / 32) + (threadIdx.x >> 5);  // row * H + head

@@ -72,7 +72,9 @@ def test_decode_step_equals_separate_entry_points(dev, B, S, H, IH, IC, W, k, kv
 
 
 @pytest.mark.parametrize("ix_bits,n_special,S", [(4, 300, 20000), (8, 300, 20000), (4, 100, 20000), (8, 100, 20000),
-                                                  (4, 100, 65536), (4, "spread", 20000), (4, "spread", 65536)])
+                                                  (4, 100, 65536), (4, "spread", 20000), (4, "spread", 65536),
+                                                  # rows of at most 16384 keys
+                                                  (8, 300, 16384), (4, 100, 16384), (4, "spread", 12000)])
 def test_decode_step_exact_ties(dev, ix_bits, n_special, S):
     # Every index key is the same code row (equal scores).  With an integer n_special, that many
     # keys get twice the scale: with 100 the k-th key is one of all the other, equal keys, so the
