@@ -838,11 +838,18 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
 #pragma unroll
   for (int w2 = 0; w2 < NW; ++w2) top = top > s_tot[w2] ? top : s_tot[w2];
   top >>= 16;
+  // slot columns r of a pass that hold a slot for some thread (workgroup-uniform): the work of
+  // the others is skipped (a row of 1024 slots uses 2 of the 8 columns of 512 threads)
+  auto columns = [&](int64_t c0) {
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(min<int64_t>(kSlotPer, (n_slots - c0 + NT - 1) / NT)));
+  };
   // bin 4095 - d holds the maxima with key >> 16 == top - d (d < 4095); bin 0 everything lower
   for (int64_t c0 = 0; c0 < n_slots; c0 += kSlotPass) {
     if (n_slots > kSlotPass) load_max(c0);  // otherwise mx still holds the only pass
+    const int n_col = columns(c0);
 #pragma unroll
     for (int r = 0; r < kSlotPer; ++r) {
+      if (r >= n_col) break;
       const uint32_t d = top - (mx[r] >> 16);
       if (c0 + tid + static_cast<int64_t>(r) * NT < n_slots)
         atomicAdd(&h[kHistBins - 1 - (d < kHistBins - 1 ? d : kHistBins - 1)], 1u);
@@ -881,11 +888,15 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
       __syncthreads();
     }
     {  // one reservation per wave for all of its slot columns
+      const int n_col = columns(c0);
       bool q[kSlotPer];
       uint64_t m[kSlotPer];
       uint32_t tot = 0u;
 #pragma unroll
       for (int r = 0; r < kSlotPer; ++r) {
+        q[r] = false;
+        m[r] = 0u;
+        if (r >= n_col) continue;
         const int64_t sl = c0 + tid + static_cast<int64_t>(r) * NT;
         q[r] = sl < n_slots && mx[r] >= tau;
         m[r] = __builtin_amdgcn_ballot_w64(q[r]);
@@ -896,6 +907,7 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
       base = __builtin_amdgcn_readfirstlane(base);
 #pragma unroll
       for (int r = 0; r < kSlotPer; ++r) {
+        if (r >= n_col) break;
         const uint32_t pos = base + static_cast<uint32_t>(mbcnt64(m[r]));
         if (q[r] && pos < static_cast<uint32_t>(kListCap)) h[pos] = static_cast<uint32_t>(tid + r * NT);
         base += static_cast<uint32_t>(__builtin_popcountll(m[r]));
