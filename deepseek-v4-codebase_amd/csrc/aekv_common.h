@@ -117,7 +117,8 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // Lane exchange with partner lane ^ HL inside a wave64, on the VALU (no LDS pipe):
 //   1, 2  DPP quad_perm [1,0,3,2] / [2,3,0,1];
 //   4     DPP row_half_mirror (i ^ 7) then quad_perm [3,2,1,0] (i ^ 3);
-//   8     DPP row_ror:8 within the 16-lane row;
+//   8     DPP row_ror:8 within the 16-lane row
+//         (every lane's source lies in its row, so these moves need no fallback value);
 //   16/32 v_permlane16_swap / v_permlane32_swap of the value with itself: the partner lands in the
 //         first result on lanes with that lane bit set and in the second on the others.
 // LDS_PIPE = true moves 4/8/16 to ds_swizzle (xor mode) and 32 to ds_bpermute instead: longer
@@ -130,14 +131,14 @@ __device__ __forceinline__ float xor_lane(float v) {
   } else if constexpr (LDS_PIPE && HL == 32) {
     i = __builtin_amdgcn_ds_bpermute(static_cast<int>(((threadIdx.x & 63) ^ 32) << 2), i);
   } else if constexpr (HL == 1) {
-    i = __builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false);
+    i = __builtin_amdgcn_mov_dpp(i, 0xB1, 0xF, 0xF, false);
   } else if constexpr (HL == 2) {
-    i = __builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false);
+    i = __builtin_amdgcn_mov_dpp(i, 0x4E, 0xF, 0xF, false);
   } else if constexpr (HL == 4) {
-    i = __builtin_amdgcn_update_dpp(0, i, 0x141, 0xF, 0xF, false);
-    i = __builtin_amdgcn_update_dpp(0, i, 0x1B, 0xF, 0xF, false);
+    i = __builtin_amdgcn_mov_dpp(i, 0x141, 0xF, 0xF, false);
+    i = __builtin_amdgcn_mov_dpp(i, 0x1B, 0xF, 0xF, false);
   } else if constexpr (HL == 8) {
-    i = __builtin_amdgcn_update_dpp(0, i, 0x128, 0xF, 0xF, false);
+    i = __builtin_amdgcn_mov_dpp(i, 0x128, 0xF, 0xF, false);
   } else if constexpr (HL == 16) {
     const auto r = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(i), static_cast<uint32_t>(i), false, false);
     i = static_cast<int>((threadIdx.x & 16) ? r[0] : r[1]);

@@ -928,12 +928,13 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
         kw[4 * q + 3] = v.w;
       }
       uint32_t c = 0;
+      const int n_in = static_cast<int>(min<int64_t>(16, nv - 16 * sl));  // the slot's visible keys
 #pragma unroll
-      for (int e = 0; e < 16; ++e) c += (16 * sl + e < nv && kw[e] >= tau) ? 1u : 0u;
+      for (int e = 0; e < 16; ++e) c += (e < n_in && kw[e] >= tau) ? 1u : 0u;
       uint32_t p = wave_reserve<5>(&s_cnt[0], c);  // c <= 16
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        if (16 * sl + e < nv && kw[e] >= tau) {
+        if (e < n_in && kw[e] >= tau) {
           if (p < static_cast<uint32_t>(CAP)) {
             ck[p] = kw[e];
             ci[p] = static_cast<uint32_t>(16 * sl + e);
@@ -961,7 +962,9 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
         for (int j = kq >> 1; j > 0; j >>= 1) {
           const uint64_t o = xor_lane_u64(w, j);
           const bool keep_min = ((lane & j) == 0) == ((lane & kq) == 0);
-          w = keep_min ? (o < w ? o : w) : (o > w ? o : w);
+          // the smaller word on keep_min lanes, the larger on the others (words are distinct but
+          // for the ~0 padding, where either is the same)
+          w = (o < w) == keep_min ? o : w;
         }
       }
     }
