@@ -751,7 +751,7 @@ __device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
 //     placed by rank.  If the candidates overflow LDS (many equal keys), the levels run over all
 //     of the row's keys, read in index order.
 // NT threads per row; CAP candidates collected in LDS; up to NT candidates sorted outright.
-// 1024 / 4096 for few rows; 512 / 1536 (37 KB of LDS, at most 128 VGPRs: two rows per CU, where
+// 1024 / 4096 for few rows; 512 / 1536 (37 KB of LDS, at most 64 VGPRs: four rows per CU, where
 // the 1024-thread instance fits one) for launches of many rows with k <= 512.
 // sel_lds (nullable): the row's output indices also go there as int32 (-1 padding), for a caller
 // that continues with them in the same workgroup.  during_wait: work of the caller's that needs no
@@ -1119,10 +1119,10 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
   return kk;
 }
 
-// The 512-thread instance serves launches of many rows: bounded to 128 VGPRs (four waves per SIMD),
-// so that two rows share a CU (bounded to 80 for three rows, it spills, and is 4% slower).
+// The 512-thread instance serves launches of many rows: bounded to 64 VGPRs (eight waves per SIMD),
+// so that four rows share a CU (it needs 57).
 template <int NT, int CAP>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 512 ? 4 : 1))) void idx_mfma_final_kernel(
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 512 ? 8 : 1))) void idx_mfma_final_kernel(
     MfmaIdxArgs a, int64_t* __restrict__ out_idx, float* __restrict__ out_score) {
   touch_kernargs<sizeof(a) + 2 * sizeof(void*)>();
   select_row<NT, CAP>(a, blockIdx.x, out_idx, out_score, nullptr);
