@@ -794,9 +794,17 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
     return 0u;
   }
   const uint32_t* krow = a.keys + static_cast<int64_t>(b) * a.ks;
-  const uint4* krow4 = reinterpret_cast<const uint4*>(krow);
   const uint32_t* mrow = a.smax + static_cast<int64_t>(b) * a.ms;
   const int64_t n_slots = (nv + 15) >> 4;
+  // The row's slot maxima and order keys are read through buffer resources whose ranges end at its
+  // last visible slot (S <= 2^24 keys: 32-bit offsets): a load past them returns 0 and touches no
+  // memory, so the loads are branch-free and the wait counts exact.  (The count is read through the
+  // vector unit; made scalar for the resources.)
+  const int n_slots_i = __builtin_amdgcn_readfirstlane(static_cast<int>(n_slots));
+  const __amdgpu_buffer_rsrc_t mrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(mrow), 0, n_slots_i * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(krow), 0, n_slots_i * 64, 0x00020000);
 
   // ---- 1. slot bound and candidates ----
   // thread tid owns slots c0 + tid + r * NT (r < kSlotPer) of each pass of 4096 slots; with
@@ -809,16 +817,10 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
     s_cnt[1] = 0u;
   }
   uint32_t mx[kSlotPer];
-  auto load_max = [&](int64_t c0) {
-    // branch-free: slots past the row read slot 0 and count as 0, so the wait counts stay exact
-    uint32_t v[kSlotPer];
+  auto load_max = [&](int64_t c0) {  // slots past the row read as 0
 #pragma unroll
-    for (int r = 0; r < kSlotPer; ++r) {
-      const int64_t sl = c0 + tid + static_cast<int64_t>(r) * NT;
-      v[r] = mrow[sl < n_slots ? sl : 0];
-    }
-#pragma unroll
-    for (int r = 0; r < kSlotPer; ++r) mx[r] = c0 + tid + static_cast<int64_t>(r) * NT < n_slots ? v[r] : 0u;
+    for (int r = 0; r < kSlotPer; ++r)
+      mx[r] = __builtin_amdgcn_raw_buffer_load_b32(mrs, static_cast<uint32_t>(c0 + tid + r * NT) * 4u, 0, 0);
   };
   // the row's largest slot max anchors the histogram
   uint32_t mloc = 0u;
@@ -851,7 +853,7 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
     for (int r = 0; r < kSlotPer; ++r) {
       if (r >= n_col) break;
       const uint32_t d = top - (mx[r] >> 16);
-      if (c0 + tid + static_cast<int64_t>(r) * NT < n_slots)
+      if (tid + r * NT < n_slots_i - static_cast<int>(c0))
         atomicAdd(&h[kHistBins - 1 - (d < kHistBins - 1 ? d : kHistBins - 1)], 1u);
     }
   }
@@ -897,8 +899,7 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
         q[r] = false;
         m[r] = 0u;
         if (r >= n_col) continue;
-        const int64_t sl = c0 + tid + static_cast<int64_t>(r) * NT;
-        q[r] = sl < n_slots && mx[r] >= tau;
+        q[r] = tid + r * NT < n_slots_i - static_cast<int>(c0) && mx[r] >= tau;
         m[r] = __builtin_amdgcn_ballot_w64(q[r]);
         tot += static_cast<uint32_t>(__builtin_popcountll(m[r]));
       }
@@ -921,11 +922,9 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
       uint32_t kw[16];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint4 v = krow4[sl * 4 + q];
-        kw[4 * q] = v.x;
-        kw[4 * q + 1] = v.y;
-        kw[4 * q + 2] = v.z;
-        kw[4 * q + 3] = v.w;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(krs, static_cast<uint32_t>(sl) * 64u + 16u * q, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kw[4 * q + e] = v[e];
       }
       uint32_t c = 0;
       const int n_in = static_cast<int>(min<int64_t>(16, nv - 16 * sl));  // the slot's visible keys
