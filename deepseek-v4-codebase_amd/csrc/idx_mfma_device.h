@@ -973,23 +973,39 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
     const int n_runs = (n + 63) >> 6;
     if (tid < n) {
       // position = number of smaller words over all runs (the own run gives the lane); the binary
-      // searches of 8 runs are interleaved so that their LDS reads overlap
-      uint32_t pos = 0u;
-      for (int r0 = 0; r0 < n_runs; r0 += 8) {
-        int lo[8];
+      // searches of up to 8 runs are interleaved so that their LDS reads overlap, and only the
+      // runs that hold candidates are searched (the run count is workgroup-uniform)
+      auto ranks = [&](auto nq_c) {
+        constexpr int NQ = decltype(nq_c)::value;
+        uint32_t pos = 0u;
+        for (int r0 = 0; r0 < n_runs; r0 += NQ) {
+          int lo[NQ];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) lo[q] = 0;
+          for (int q = 0; q < NQ; ++q) lo[q] = 0;
 #pragma unroll
-        for (int step = 32; step > 0; step >>= 1) {
+          for (int step = 32; step > 0; step >>= 1) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q)
-            if (cbuf[64 * (r0 + q) + lo[q] + step - 1] < w) lo[q] += step;
+            for (int q = 0; q < NQ; ++q)
+              if (cbuf[64 * (r0 + q) + lo[q] + step - 1] < w) lo[q] += step;
+          }
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) {  // the steps reach 63; the last compare 64
+            if (cbuf[64 * (r0 + q) + lo[q]] < w) ++lo[q];
+            pos += static_cast<uint32_t>(lo[q]);
+          }
         }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {  // the steps reach 63; the last compare 64
-          if (cbuf[64 * (r0 + q) + lo[q]] < w) ++lo[q];
-          pos += static_cast<uint32_t>(lo[q]);
-        }
+        return pos;
+      };
+      uint32_t pos;
+      switch (__builtin_amdgcn_readfirstlane(n_runs)) {
+        case 1: pos = ranks(std::integral_constant<int, 1>{}); break;
+        case 2: pos = ranks(std::integral_constant<int, 2>{}); break;
+        case 3: pos = ranks(std::integral_constant<int, 3>{}); break;
+        case 4: pos = ranks(std::integral_constant<int, 4>{}); break;
+        case 5: pos = ranks(std::integral_constant<int, 5>{}); break;
+        case 6: pos = ranks(std::integral_constant<int, 6>{}); break;
+        case 7: pos = ranks(std::integral_constant<int, 7>{}); break;
+        default: pos = ranks(std::integral_constant<int, 8>{}); break;  // 8, or two passes and more
       }
       if (pos < kk) {
         orow[pos] = static_cast<int64_t>(static_cast<uint32_t>(w & 0xffffffffu));
