@@ -162,7 +162,6 @@ __device__ __forceinline__ float row_sums_scatter(const float (&t)[4]) {
   return __builtin_bit_cast(float, x0) + __builtin_bit_cast(float, x1);
 }
 
-// 64-bit lane exchange with partner lane ^ j (j a power of two below 64, constant after unrolling).
 template <int HL>
 __device__ __forceinline__ uint32_t max_xor_u32(uint32_t v) {
   const uint32_t o = __builtin_bit_cast(uint32_t, xor_lane<HL>(__builtin_bit_cast(float, v)));
@@ -177,6 +176,7 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return max_xor_u32<32>(v);
 }
 
+// 64-bit lane exchange with partner lane ^ j (j a power of two below 64, constant after unrolling).
 __device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v, int j) {
   float lo = __builtin_bit_cast(float, static_cast<uint32_t>(v));
   float hi = __builtin_bit_cast(float, static_cast<uint32_t>(v >> 32));
@@ -671,13 +671,16 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
         uint8_t* krow = reinterpret_cast<uint8_t*>(a.keys + row[tt] * a.ks);
         uint8_t* mrow = reinterpret_cast<uint8_t*>(a.smax + row[tt] * a.ms);
         if (ok) *reinterpret_cast<uint32_t*>(krow + static_cast<uint32_t>(jo) * 4u) = key;
-        // max of the 16-key slot of lanes 16u .. 16u+15, stored by its first lane
+        // max of the 16-key slot of lanes 16u .. 16u+15: a prefix max along the row (row_shr by 1,
+        // 2, 4, 8, lanes shifted in from outside the row read 0), stored by the row's last lane
+        // when the slot's first key is visible (keys past the count are 0)
         uint32_t mx = key;
-        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<1>(__builtin_bit_cast(float, mx))));
-        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<2>(__builtin_bit_cast(float, mx))));
-        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<4>(__builtin_bit_cast(float, mx))));
-        mx = max(mx, __builtin_bit_cast(uint32_t, xor_lane<8>(__builtin_bit_cast(float, mx))));
-        if ((lane & 15) == 0 && ok) *reinterpret_cast<uint32_t*>(mrow + static_cast<uint32_t>(jo >> 4) * 4u) = mx;
+        mx = max(mx, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mx), 0x111, 0xF, 0xF, true)));
+        mx = max(mx, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mx), 0x112, 0xF, 0xF, true)));
+        mx = max(mx, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mx), 0x114, 0xF, 0xF, true)));
+        mx = max(mx, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mx), 0x118, 0xF, 0xF, true)));
+        if ((lane & 15) == 15 && (FULL || jo - 15 < nvi[tt]))
+          *reinterpret_cast<uint32_t*>(mrow + static_cast<uint32_t>(jo >> 4) * 4u) = mx;
       }
     }
   };
