@@ -208,15 +208,25 @@ __device__ __forceinline__ void load_bins(const uint32_t* h, int tid, uint32_t (
   }
 }
 
-// Inclusive suffix sum over the lanes of a wave (lane 63 holds the highest bins).
+// DPP move of x (lanes without a source, or in rows outside RMASK, read 0).
+template <int CTRL, int RMASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_or_zero(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, RMASK, 0xF, true));
+}
+
+// Inclusive suffix sum over the lanes of a wave (lane 63 holds the highest bins): the inclusive
+// prefix sum by DPP (row_shr 1, 2, 4, 8 within the 16-lane rows, then row_bcast:15 into rows 1
+// and 3 and row_bcast:31 into rows 2 and 3), subtracted from the total.
 __device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t y = __shfl_down(x, off, 64);
-    if (lane + off < 64) x += y;
-  }
-  return x;
+  uint32_t p = x;
+  p += dpp_or_zero<0x111>(p);
+  p += dpp_or_zero<0x112>(p);
+  p += dpp_or_zero<0x114>(p);
+  p += dpp_or_zero<0x118>(p);
+  p += dpp_or_zero<0x142, 0xA>(p);
+  p += dpp_or_zero<0x143, 0xC>(p);
+  const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(p), 63));
+  return total - p + x;
 }
 
 // The lane whose bins hold the crossing walks them from the top.
