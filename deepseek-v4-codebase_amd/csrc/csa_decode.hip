@@ -97,7 +97,7 @@ __global__ __launch_bounds__(kFusedThreads) void csa_decode_fused_kernel(idx::Mf
     qattn::group_consume<KV_BITS, false>(qa, f, in, st);
   }
   if (win_pending) window();  // a wave without a selected group
-  qattn::attend_finish<NW>(qa, b, 0, lds, st, f.sink);
+  qattn::attend_finish<NW>(qa, b, 0, lds, st, f.sink, f.neg);
 }
 
 }  // namespace

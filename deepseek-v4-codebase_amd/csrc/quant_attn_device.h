@@ -175,6 +175,7 @@ struct AttnFrags {
   i32x4_t hA[4];
   bf16x8_t esel[2];
   float sink;  // the sink of head threadIdx.x (threads below H; 0 for a split of several)
+  uint64_t neg[2];  // the diagonal's sign bits: bit d of neg[d >> 6] (wave-uniform)
 };
 
 // The prologue's loads: two entries of the diagonal (dims lane and 64 + lane; the wave's ballots
@@ -216,6 +217,8 @@ __device__ __forceinline__ void prologue_build(const QAttnMfmaArgs& a, const Pro
   // dsign: the diagonal's sign bits for the lane's dims, per packed bf16 pair (dword e of k-step
   // ks), from the signs of all 128 dims (bit d of neg[d >> 6], every lane of the wave active)
   const uint64_t neg[2] = {__builtin_amdgcn_ballot_w64(r.dv[0] < 0.0f), __builtin_amdgcn_ballot_w64(r.dv[1] < 0.0f)};
+  f.neg[0] = neg[0];
+  f.neg[1] = neg[1];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -498,10 +501,12 @@ __device__ __forceinline__ void group_consume(const QAttnMfmaArgs& a, const Attn
 
 // Merges the NW waves' states (and the sink, unless this is one split of several) and writes the
 // row's output, or its split result (max, sum, O) for the combine.  sink_h: the sink of head
-// threadIdx.x, requested with the prologue (AttnFrags::sink).
+// threadIdx.x, requested with the prologue (AttnFrags::sink); neg: the diagonal's sign bits
+// (AttnFrags::neg), so that the diagonal comes off the output without a memory round.
 template <int NW>
 __device__ __forceinline__ void attend_finish(const QAttnMfmaArgs& a, const int64_t b, const int split,
-                                              unsigned char* lds, const AttnState& s, const float sink_h) {
+                                              unsigned char* lds, const AttnState& s, const float sink_h,
+                                              const uint64_t (&neg)[2]) {
   constexpr int kW = NW, kT = 64 * NW;
   using L = QLay<NW>;
   float* Ob = reinterpret_cast<float*>(lds + L::ob);    // [wave][head][kObStride]
@@ -551,8 +556,14 @@ __device__ __forceinline__ void attend_finish(const QAttnMfmaArgs& a, const int6
       const f32x4_t o = *reinterpret_cast<const f32x4_t*>(Ob + (w * 16 + h) * kObStride + d4);
       acc = f32x4_t{fmaf(f, o[0], acc[0]), fmaf(f, o[1], acc[1]), fmaf(f, o[2], acc[2]), fmaf(f, o[3], acc[3])};
     }
-    const float4 dg = *reinterpret_cast<const float4*>(a.diag + d4);
-    acc = f32x4_t{acc[0] * dg.x, acc[1] * dg.y, acc[2] * dg.z, acc[3] * dg.w};
+    // times the +-1 diagonal: a sign flip of dims d4 .. d4 + 3 (exact)
+    // (a select, not an index: a runtime index into the array would put the fragments in scratch)
+    const uint32_t sg = static_cast<uint32_t>((d4 < 64 ? neg[0] : neg[1]) >> (d4 & 63));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x = acc[e];  // (a bit cast of the vector element itself would read element 0)
+      acc[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) ^ (((sg >> e) & 1u) << 31));
+    }
     if (a.n_split == 1) {
       const float r = inv[h];
       const uint2 v = make_uint2(pack_bf16x2(acc[0] * r, acc[1] * r), pack_bf16x2(acc[2] * r, acc[3] * r));
@@ -621,7 +632,7 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
     }
   }
   // ---- merge the waves (and the sink, unless this is one split of several) ----
-  attend_finish<NW>(a, b, split, lds, s, f.sink);
+  attend_finish<NW>(a, b, split, lds, s, f.sink, f.neg);
 }
 
 
@@ -761,7 +772,7 @@ __device__ __forceinline__ void attend_dense(const QAttnMfmaArgs& a, const int64
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  attend_finish<NW>(a, b, split, lds, s, f.sink);
+  attend_finish<NW>(a, b, split, lds, s, f.sink, f.neg);
 }
 
 // One row (or one split of a long row) per workgroup of 64 * NW threads.
