@@ -41,17 +41,17 @@ __device__ __forceinline__ void load_elems(const void* base, int64_t off, bool o
         a[e] = DT == AEKV_BF16 ? bf16_to_f32(u) : f16_to_f32(u);
       }
     }
-  } else {  // fp32, EPL == 8: two 16-byte loads
-    Bytes<16> r0 = reinterpret_cast<const Bytes<16>*>(p)[0];
-    Bytes<16> r1 = reinterpret_cast<const Bytes<16>*>(p)[1];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      uint32_t u0, u1;
-      __builtin_memcpy(&u0, r0.b + 4 * e, 4);
-      __builtin_memcpy(&u1, r1.b + 4 * e, 4);
-      a[e] = __builtin_bit_cast(float, u0);
-      a[e + 4] = __builtin_bit_cast(float, u1);
-    }
+  } else {  // fp32, EPL == 8: two 16-byte loads (as vectors: byte arrays copied out of end up in scratch)
+    const float4 r0 = reinterpret_cast<const float4*>(p)[0];
+    const float4 r1 = reinterpret_cast<const float4*>(p)[1];
+    a[0] = r0.x;
+    a[1] = r0.y;
+    a[2] = r0.z;
+    a[3] = r0.w;
+    a[4] = r1.x;
+    a[5] = r1.y;
+    a[6] = r1.z;
+    a[7] = r1.w;
   }
 }
 
