@@ -174,7 +174,7 @@ struct AttnFrags {
   bf16x8_t qb[4];
   i32x4_t hA[4];
   bf16x8_t esel[2];
-  float sink;  // the sink of head threadIdx.x (threads below H; 0 for a split of several)
+  float sink;  // the sink of head threadIdx.x / 8 (threads below 8H; 0 for a split of several)
   uint64_t neg[2];  // the diagonal's sign bits: bit d of neg[d >> 6] (wave-uniform)
 };
 
@@ -203,7 +203,7 @@ __device__ __forceinline__ void prologue_loads(const QAttnMfmaArgs& a, const int
     r.lo[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks));
     r.hi[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks + 1));
   }
-  const int th = static_cast<int>(threadIdx.x) < a.H ? static_cast<int>(threadIdx.x) : 0;
+  const int th = static_cast<int>(threadIdx.x >> 3) < a.H ? static_cast<int>(threadIdx.x >> 3) : 0;
   r.sink = a.n_split == 1 ? a.sink[th] : 0.0f;
 }
 
@@ -501,7 +501,7 @@ __device__ __forceinline__ void group_consume(const QAttnMfmaArgs& a, const Attn
 
 // Merges the NW waves' states (and the sink, unless this is one split of several) and writes the
 // row's output, or its split result (max, sum, O) for the combine.  sink_h: the sink of head
-// threadIdx.x, requested with the prologue (AttnFrags::sink); neg: the diagonal's sign bits
+// threadIdx.x / 8, requested with the prologue (AttnFrags::sink); neg: the diagonal's sign bits
 // (AttnFrags::neg), so that the diagonal comes off the output without a memory round.
 template <int NW>
 __device__ __forceinline__ void attend_finish(const QAttnMfmaArgs& a, const int64_t b, const int split,
@@ -522,27 +522,33 @@ __device__ __forceinline__ void attend_finish(const QAttnMfmaArgs& a, const int6
     stat[(wv * 16 + c16) * 2 + 1] = s.l_run;
   }
   __syncthreads();
-  // per head (one thread each): M = max(sink, wave maxima), the waves' factors e^{m_w - M}, and
-  // the normaliser L; the factors replace the maxima in stat, 1/L (or L for a split) is kept aside
-  if (threadIdx.x < H) {
-    const int h = threadIdx.x;
-    float M = a.n_split == 1 ? sink_h : kNegInf;
-#pragma unroll
-    for (int w = 0; w < kW; ++w) M = fmaxf(M, stat[(w * 16 + h) * 2]);
-    float Lsum = a.n_split == 1 ? __expf(sink_h - M) : 0.0f;
-#pragma unroll
-    for (int w = 0; w < kW; ++w) {
-      const float mw = stat[(w * 16 + h) * 2];
-      const float f = mw == kNegInf ? 0.0f : __expf(mw - M);
-      Lsum = fmaf(f, stat[(w * 16 + h) * 2 + 1], Lsum);
-      stat[(w * 16 + h) * 2] = f;
-    }
-    if (a.n_split == 1) {
-      inv[h] = M == kNegInf ? 0.0f : 1.0f / Lsum;  // no source and sink -inf: 0
-    } else {
-      float* dst = a.part + ((b * a.n_split + split) * H + h) * kPartStride;
-      dst[0] = M;
-      dst[1] = Lsum;
+  // per head: M = max(sink, wave maxima), the waves' factors e^{m_w - M}, and the normaliser L;
+  // the factors replace the maxima in stat, 1/L (or L for a split) is kept aside.  Thread 8h + w of
+  // the first two waves takes head h and wave w, and the 8 lanes of a head reduce by lane exchanges.
+  if (threadIdx.x < 128) {  // wave-uniform
+    const int h = threadIdx.x >> 3, w = threadIdx.x & 7;
+    const bool valid = h < H && w < kW;
+    const float mw = valid ? stat[(w * 16 + h) * 2] : kNegInf;
+    const float lw = valid ? stat[(w * 16 + h) * 2 + 1] : 0.0f;
+    float M = a.n_split == 1 ? fmaxf(mw, sink_h) : mw;
+    M = fmaxf(M, xor_lane<1>(M));
+    M = fmaxf(M, xor_lane<2>(M));
+    M = fmaxf(M, xor_lane<4>(M));
+    const float f = mw == kNegInf ? 0.0f : __expf(mw - M);
+    float L = f * lw;
+    L += xor_lane<1>(L);
+    L += xor_lane<2>(L);
+    L += xor_lane<4>(L);
+    if (a.n_split == 1) L += __expf(sink_h - M);
+    if (valid) stat[(w * 16 + h) * 2] = f;
+    if (w == 0 && h < H) {
+      if (a.n_split == 1) {
+        inv[h] = M == kNegInf ? 0.0f : 1.0f / L;  // no source and sink -inf: 0
+      } else {
+        float* dst = a.part + ((b * a.n_split + split) * H + h) * kPartStride;
+        dst[0] = M;
+        dst[1] = L;
+      }
     }
   }
   __syncthreads();
