@@ -413,6 +413,43 @@ def csa_step_bytes(B, S, bits, k=256, H=12, D=128, W=128, IH=4, IC=64):
     return B * (S * ix_bytes + k * row_bytes + W * D * 2 + H * D * 2 * 2 + IH * IC * 4 + IH * 4 + k * 8)
 
 
+def scan_ceiling(args, layers, B, S, bits, dev):
+    """The score pass's streaming ceiling, cold like the step (one probe launch per layer's index
+    cache in one graph): aekv_scan_probe reads every key's codes and scale in the score kernel's
+    groups, and writes 4 bytes per key and per 16-key slot as its order keys and slot maxima, or
+    only reads."""
+    import aetherkv._lib as L
+
+    plib = ctypes.CDLL(str(Path(L.__file__).with_name("libaetherkv_probe.so")))
+    plib.aekv_scan_probe.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    plib.aekv_scan_probe.restype = ctypes.c_int
+    keys = torch.empty(B * S, dtype=torch.int32, device=dev)
+    smax = torch.empty(B * S // 16, dtype=torch.int32, device=dev)
+    row_bytes = 64 if bits == 8 else 32
+
+    def probe(x, kp):
+        cp, sp, mp = L.ptr(x["ix_codes"]), L.ptr(x["ix_scale"]), L.ptr(smax)
+
+        def run():
+            if plib.aekv_scan_probe(cp, sp, B * S, row_bytes, kp, mp, L.stream_of(smax)) != 0:
+                raise RuntimeError("aekv_scan_probe rejected its arguments or failed to launch")
+        return run
+
+    ms_rw = timed_graph_layers([probe(x, L.ptr(keys)) for x in layers], args.steps, args.warmup)
+    ms_r = timed_graph_layers([probe(x, None) for x in layers], args.steps, args.warmup)
+    ix = B * S * (row_bytes + 4)
+    out = {"read_write_ms": round(ms_rw, 5), "read_only_ms": round(ms_r, 5), "bytes_read": ix,
+           "bytes_written": B * S * 4 + B * S // 16 * 4,
+           "what": "aekv_scan_probe over the same layers' index caches, cold: the score pass's reads (codes + "
+                   "scales, 128 keys per wave) and writes (4 B per key, 4 B per 16-key slot), no arithmetic; "
+                   "read_only: the reads alone"}
+    log(f"score pass ceiling: {ms_rw * 1e3:.1f} us with its writes, {ms_r * 1e3:.1f} us reads only "
+        f"({ix / ms_r / 1e6:.0f} GB/s)")
+    del keys, smax
+    return out
+
+
 def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
     from aetherkv.decode import (attention_workspace, csa_decode_step, csa_indexer_topk_quant, decode_workspace,
                                  indexer_workspace, quant_sink_attention)
@@ -469,6 +506,7 @@ def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
                                        kv_quant=pq, index_quant=pq, workspace=ws_s, out_idx=idx, out=out)
 
     ms = timed_graph_layers([layer_step(li) for li in range(n_layers)], args.steps, args.warmup)
+    scan = scan_ceiling(args, layers, B, S, bits, dev)
     res = {"B": B, "S": S, "bits": bits, "ms_per_step": round(ms, 5), "tokens_per_s": round(B / ms * 1e3, 1),
            "hbm_frac": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes_per_step": step_bytes,
            "timing": f"cold: {n_layers} layers' distinct caches ({n_layers * step_bytes / 2 ** 20:.0f} MiB touched "
@@ -484,6 +522,7 @@ def bench_csa(args, dev, B, S, bits, seed, outliers, name, cpu_rows=0):
     log(f"{name}: cold {ms * 1e3:.1f} us/step ({n_layers} layers) -> {res['tokens_per_s']:.0f} tok/s, "
         f"{res['hbm_frac'] * 100:.1f}% of HBM peak; warm {ms_warm * 1e3:.1f} (eager {ms_eager * 1e3:.1f}); separate "
         f"kernels warm {ms_sep * 1e3:.1f} ({ms_i * 1e3:.1f} indexer + {ms_a * 1e3:.1f} attention)")
+    res["score_pass_ceiling"] = scan
     if cpu:
         res["cpu_baseline"] = cpu
     del inp, layers

@@ -1,5 +1,5 @@
-// Streaming ceiling for the cfg2 encode's traffic shape: a measurement utility for bench.py with
-// no counterpart in the reference, built into its own library (libaetherkv_probe.so, declared in
+// Streaming ceilings for the traffic of two kernels: measurement utilities for bench.py with no
+// counterpart in the reference, built into their own library (libaetherkv_probe.so, declared in
 // include/aetherkv_probe.h) so that the product library exports only the path's entry points.
 //
 // stream_probe_kernel moves exactly the encode's bytes with the encode's access pattern and
@@ -40,7 +40,57 @@ __global__ __launch_bounds__(256) void stream_probe_kernel(const uint4* __restri
   }
 }
 
+// scan_probe_kernel: the CSA score pass's traffic with no arithmetic.  One wave per group of 128
+// keys of one row (the score kernel's decode group at 4 bits): the group's code bytes (128 x RB,
+// 16 bytes per lane and load) and its 128 scales (8 bytes per lane) are read, and, with keys set, 4
+// bytes per key (8 per lane) and 4 per 16-key slot are written, as the order keys and slot maxima.
+// The written values are xor folds of the loaded ones, so no load can be dropped.
+template <int RB>
+__global__ __launch_bounds__(256) void scan_probe_kernel(const uint4* __restrict__ codes, const uint2* __restrict__ scale,
+                                                         int64_t n_groups, uint2* __restrict__ keys,
+                                                         uint32_t* __restrict__ smax) {
+  constexpr int kLoads = 128 * RB / 16 / 64;  // 16-byte loads per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t grp = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (grp >= n_groups) return;
+  const uint4* c = codes + grp * (128 * RB / 16);
+  uint4 t[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) t[i] = c[64 * i + lane];
+  const uint2 sc = scale[grp * 64 + lane];
+  uint32_t x = sc.x, y = sc.y;
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    x ^= t[i].x ^ t[i].z;
+    y ^= t[i].y ^ t[i].w;
+  }
+  if (keys) {
+    keys[grp * 64 + lane] = make_uint2(x, y);
+    if ((lane & 7) == 0) smax[grp * 8 + (lane >> 3)] = x + y;
+  } else if (x == 0x9e3779b9u && y == 0x7f4a7c15u) {
+    smax[0] = x;  // (never in practice: keeps the loads live)
+  }
+}
+
 }  // namespace
+
+extern "C" int aekv_scan_probe(const void* codes, const float* scale, int64_t n_keys, int32_t row_bytes, void* keys,
+                               uint32_t* smax, void* stream) {
+  auto aligned = [](const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; };
+  if (n_keys < 0 || n_keys % 128 != 0 || (row_bytes != 32 && row_bytes != 64)) return AEKV_PROBE_ERR_ARGS;
+  if (n_keys == 0) return AEKV_PROBE_OK;
+  if (!codes || !scale || !smax || !aligned(codes, 16) || !aligned(scale, 8) || (keys && !aligned(keys, 8)) ||
+      !aligned(smax, 4))
+    return AEKV_PROBE_ERR_ARGS;
+  const int64_t n_groups = n_keys / 128;
+  const int64_t blocks = (n_groups + 3) / 4;
+  if (blocks > 0x7fffffff) return AEKV_PROBE_ERR_ARGS;
+  auto fn = row_bytes == 32 ? scan_probe_kernel<32> : scan_probe_kernel<64>;
+  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const uint4*>(codes), reinterpret_cast<const uint2*>(scale), n_groups,
+                     static_cast<uint2*>(keys), smax);
+  return hipGetLastError() == hipSuccess ? AEKV_PROBE_OK : AEKV_PROBE_ERR_LAUNCH;
+}
 
 extern "C" int aekv_stream_probe(const void* x, int64_t n_vec, void* codes, float* scale, void* stream) {
   auto aligned = [](const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; };

@@ -41,24 +41,31 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_probe_library_exports_its_header_and_nothing_leaks_into_the_product():
-    """bench.py's streaming probe lives in libaetherkv_probe.so (include/aetherkv_probe.h), not in
-    the product library, and rejects bad arguments before enqueuing anything."""
+    """bench.py's streaming probes live in libaetherkv_probe.so (include/aetherkv_probe.h), not in
+    the product library, and reject bad arguments before enqueuing anything."""
     text = (ROOT / "include" / "aetherkv_probe.h").read_text()
     names = sorted(set(re.findall(r"^\s*int\s+(aekv_\w+)\(", text, flags=re.M)))
-    assert names == ["aekv_stream_probe"]
+    assert names == ["aekv_scan_probe", "aekv_stream_probe"]
     path = L.LIB_PATH.with_name("libaetherkv_probe.so")
     if not path.exists():
         pytest.fail("libaetherkv_probe.so is not built (run __graft_entry__.build())")
     plib = ctypes.CDLL(str(path))
     for n in names:
         assert hasattr(plib, n), n
-    assert "aekv_stream_probe" not in L.SYMBOLS
+    assert "aekv_stream_probe" not in L.SYMBOLS and "aekv_scan_probe" not in L.SYMBOLS
     plib.aekv_stream_probe.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_void_p]
     assert plib.aekv_stream_probe(None, -1, None, None, None) == 1
     assert plib.aekv_stream_probe(None, 0, None, None, None) == 0
     assert plib.aekv_stream_probe(None, 16, None, None, None) == 1
     assert plib.aekv_stream_probe(ctypes.c_void_p(0x10008), 16, FAKE, FAKE, None) == 1  # x not 16-byte aligned
+    plib.aekv_scan_probe.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    assert plib.aekv_scan_probe(None, None, 0, 32, None, None, None) == 0
+    assert plib.aekv_scan_probe(FAKE, FAKE, 100, 32, None, FAKE, None) == 1  # not a multiple of 128 keys
+    assert plib.aekv_scan_probe(FAKE, FAKE, 128, 48, None, FAKE, None) == 1  # row bytes neither 32 nor 64
+    assert plib.aekv_scan_probe(None, FAKE, 128, 32, None, FAKE, None) == 1
+    assert plib.aekv_scan_probe(ctypes.c_void_p(0x10008), FAKE, 128, 64, None, FAKE, None) == 1  # codes misaligned
 
 
 def test_version_and_limits(lib):
