@@ -44,6 +44,9 @@ COMMON_FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # the leading scalar kernel arguments arrive in registers at dispatch (a kernel's first loads then
+    # do not wait for its argument block); byval struct arguments are still read from memory
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     f"-I{INCLUDE}",
     f"-I{CSRC}",

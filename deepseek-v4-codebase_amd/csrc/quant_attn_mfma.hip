@@ -12,37 +12,55 @@ constexpr int kMaxCombineSplits = 256;  // most source pieces per row
 // Split combine: M = max(sink, split maxima), L = e^{sink-M} + sum_s e^{m_s-M} l_s,
 // out = sum_s e^{m_s-M} acc_s / L (the sink counted once, aether_pipeline/serving.py:125-129).  32
 // threads per (row, head), 4 dims each; the splits' (m, l, acc) are loaded in chunks of 8 whose
-// loads are all issued together and merged online, so a row takes one memory round per 8 splits.
-// Workgroups of kCombineThreads (two (row, head) pairs): a decode step's few hundred pairs then
-// spread over as many CUs, instead of queueing their loads on a few.
+// loads are all issued together (the first chunk's with the sink's) and merged online, so a row
+// takes one memory round per 8 splits.  Workgroups of kCombineThreads (two (row, head) pairs): a
+// decode step's few hundred pairs then spread over as many CUs, instead of queueing their loads on
+// a few.  The arguments are plain scalars, which the dispatch preloads into registers (the
+// library is built with kernel-argument preloading), so the first loads do not wait for the
+// argument block.
 constexpr int kCombineThreads = 64;
-__global__ __launch_bounds__(kCombineThreads) void quant_attn_mfma_combine_kernel(QAttnMfmaArgs a, int64_t rows) {
-  touch_kernargs<sizeof(a) + sizeof(rows)>();
+__global__ __launch_bounds__(kCombineThreads) void quant_attn_mfma_combine_kernel(const float* __restrict__ part,
+                                                                                  const float* __restrict__ sink,
+                                                                                  uint16_t* __restrict__ out,
+                                                                                  int rows_heads, int H, int ns) {
   constexpr int kChunk = 8;
-  const int H = a.H, ns = a.n_split;
-  const int64_t rh = static_cast<int64_t>(blockIdx.x) * (kCombineThreads / 32) + (threadIdx.x >> 5);  // row * H + head
-  if (rh >= rows * H) return;
-  const int64_t b = rh / H;
-  const int h = static_cast<int>(rh - b * H), j = threadIdx.x & 31;
-  const float* part = a.part + (b * ns * H + h) * kPartStride;  // split s at + s * H * kPartStride
-  const float sk = a.sink[h];
+  const int rh = static_cast<int>(blockIdx.x) * (kCombineThreads / 32) + (static_cast<int>(threadIdx.x) >> 5);
+  if (rh >= rows_heads) return;
+  const int b = rh / H, h = rh - b * H, j = threadIdx.x & 31;
+  // split s of (row b, head h) at prow + s H kPartStride; a split past ns reads split 0 (always
+  // present) and is replaced by the empty state (max -inf, sum 0, acc 0)
+  const float* prow = part + (static_cast<int64_t>(b) * ns * H + h) * kPartStride;
+  float m[kChunk], l[kChunk];
+  f32x4_t o[kChunk];
+  // the chunk's loads all precede the empty asm that takes their values, so every load is issued
+  // before the first wait (the compiler would otherwise move loads into the branches that use
+  // them, each with its own wait)
+  auto load_chunk = [&](const int s0, float* sk) {
+    float2 ml[kChunk];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      const float* ps = prow + static_cast<int64_t>(s0 + i < ns ? s0 + i : 0) * H * kPartStride;
+      ml[i] = *reinterpret_cast<const float2*>(ps);
+      o[i] = *reinterpret_cast<const f32x4_t*>(ps + 4 + 4 * j);
+    }
+    if (sk) *sk = sink[h];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) asm volatile("" : "+v"(ml[i].x), "+v"(ml[i].y), "+v"(o[i]));
+    if (sk) asm volatile("" : "+v"(*sk));
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      const bool in = s0 + i < ns;
+      m[i] = in ? ml[i].x : kNegInf;
+      l[i] = in ? ml[i].y : 0.0f;
+      o[i] = in ? o[i] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
+  float sk;
+  load_chunk(0, &sk);
   float M = sk, den = sk == kNegInf ? 0.0f : 1.0f;
   f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   for (int s0 = 0; s0 < ns; s0 += kChunk) {
-    float m[kChunk], l[kChunk];
-    f32x4_t o[kChunk];
-#pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-      m[i] = kNegInf;
-      l[i] = 0.0f;
-      o[i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      if (s0 + i < ns) {
-        const float* ps = part + static_cast<int64_t>(s0 + i) * H * kPartStride;
-        m[i] = ps[0];
-        l[i] = ps[1];
-        o[i] = *reinterpret_cast<const f32x4_t*>(ps + 4 + 4 * j);
-      }
-    }
+    if (s0 > 0) load_chunk(s0, nullptr);
     float cm = M;
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) cm = fmaxf(cm, m[i]);
@@ -59,7 +77,7 @@ __global__ __launch_bounds__(kCombineThreads) void quant_attn_mfma_combine_kerne
     }
   }
   const float r = den > 0.0f ? 1.0f / den : 0.0f;
-  *reinterpret_cast<uint2*>(a.out + rh * kD + 4 * j) =
+  *reinterpret_cast<uint2*>(out + static_cast<int64_t>(rh) * kD + 4 * j) =
       make_uint2(pack_bf16x2(acc[0] * r, acc[1] * r), pack_bf16x2(acc[2] * r, acc[3] * r));
 }
 
@@ -142,8 +160,8 @@ int launch_quant_attn_mfma_rows(const void* q, const void* codes, const float* s
   if (int rc = check_launch(who)) return rc;
   if (n_split > 1) {
     const int64_t n_wg = ceil_div(rows * H, kCombineThreads / 32);
-    hipLaunchKernelGGL(quant_attn_mfma_combine_kernel, dim3(static_cast<uint32_t>(n_wg)), dim3(kCombineThreads), 0, st, a,
-                       rows);
+    hipLaunchKernelGGL(quant_attn_mfma_combine_kernel, dim3(static_cast<uint32_t>(n_wg)), dim3(kCombineThreads), 0, st,
+                       static_cast<const float*>(a.part), a.sink, a.out, static_cast<int>(rows * H), a.H, a.n_split);
     return check_launch(who);
   }
   return AEKV_OK;
