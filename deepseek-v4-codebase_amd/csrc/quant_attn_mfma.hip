@@ -15,9 +15,9 @@ constexpr int kMaxCombineSplits = 256;  // most source pieces per row
 // loads are all issued together (the first chunk's with the sink's) and merged online, so a row
 // takes one memory round per 8 splits.  Workgroups of kCombineThreads (two (row, head) pairs): a
 // decode step's few hundred pairs then spread over as many CUs, instead of queueing their loads on
-// a few.  The arguments are plain scalars, which the dispatch preloads into registers (the
-// library is built with kernel-argument preloading), so the first loads do not wait for the
-// argument block.
+// a few.  The arguments are plain scalars, which the dispatch preloads into registers (this file
+// is built with kernel-argument preloading), so the first loads do not wait for the argument
+// block.
 constexpr int kCombineThreads = 64;
 __global__ __launch_bounds__(kCombineThreads) void quant_attn_mfma_combine_kernel(const float* __restrict__ part,
                                                                                   const float* __restrict__ sink,
