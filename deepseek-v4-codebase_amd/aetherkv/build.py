@@ -61,12 +61,15 @@ def sources():
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
-# Per-source flags.  quant_attn_mfma.hip: the split combine's scalar arguments arrive in registers
-# at dispatch (its one memory round then does not wait for the argument block; byval struct
-# arguments are not preloaded).  Measured per kernel: it helps the combine (HCA decode) and left
-# the codec kernels within noise or up to 1.7% slower, so it is not applied library-wide.
+# Per-source flags.  quant_attn_mfma.hip, sink_attention_mfma.hip: the split combines' scalar
+# arguments arrive in registers at dispatch (their one memory round then does not wait for the
+# argument block; byval struct arguments, as the other kernels there take, are not preloaded).
+# Measured per kernel: it helps the combine (HCA decode) and left the codec kernels within noise or
+# up to 1.7% slower, so it is not applied library-wide.
+_PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
 SOURCE_FLAGS = {
-    "quant_attn_mfma.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+    "quant_attn_mfma.hip": _PRELOAD,
+    "sink_attention_mfma.hip": _PRELOAD,
 }
 
 

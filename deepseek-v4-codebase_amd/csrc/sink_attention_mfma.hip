@@ -276,31 +276,46 @@ __global__ __launch_bounds__(64 * NW) void gather_attn_kernel(GatherArgs a) {
 template <int DT, int NT>
 __global__ __launch_bounds__(NT) void sink_attn_combine_kernel(const float* __restrict__ part, int n_split,
                                                                const uint16_t* __restrict__ sink, int sink_scalar,
-                                                               int H, int64_t rows, uint16_t* __restrict__ out) {
+                                                               int H, int rows, uint16_t* __restrict__ out) {
   using E = Elem<DT>;
   constexpr int kChunk = 8;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (NT / 32) + (threadIdx.x >> 5);
+  const int row = static_cast<int>(blockIdx.x) * (NT / 32) + (static_cast<int>(threadIdx.x) >> 5);
   if (row >= rows) return;
   const int j = threadIdx.x & 31;
-  const float* p = part + row * n_split * kPartStride;
-  const float sk = E::to_f32(sink[sink_scalar ? 0 : row % H]) * kLog2e;
+  const float* p = part + static_cast<int64_t>(row) * n_split * kPartStride;
+  float m[kChunk], l[kChunk];
+  f32x4_t o[kChunk];
+  // A chunk's loads (and the sink's, with the first) all precede the empty asm that takes their
+  // values, so every load is issued before the first wait (the compiler would otherwise wait for
+  // the sink first, and move loads into the branches that use them, each with its own wait).  A
+  // piece past n_split reads piece 0 and is replaced by the empty state.
+  auto load_chunk = [&](const int s0, uint32_t* skb) {
+    float2 ml[kChunk];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      const float* ps = p + (s0 + i < n_split ? s0 + i : 0) * kPartStride;
+      ml[i] = *reinterpret_cast<const float2*>(ps);
+      o[i] = *reinterpret_cast<const f32x4_t*>(ps + 4 + 4 * j);
+    }
+    if (skb) *skb = sink[sink_scalar ? 0 : row % H];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) asm volatile("" : "+v"(ml[i].x), "+v"(ml[i].y), "+v"(o[i]));
+    if (skb) asm volatile("" : "+v"(*skb));
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+      const bool in = s0 + i < n_split;
+      m[i] = in ? ml[i].x : kNegInf;
+      l[i] = in ? ml[i].y : 0.0f;
+      o[i] = in ? o[i] : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
+  uint32_t skb;
+  load_chunk(0, &skb);
+  const float sk = E::to_f32(skb) * kLog2e;
   float M = sk, den = sk == kNegInf ? 0.0f : 1.0f;
   f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   for (int s0 = 0; s0 < n_split; s0 += kChunk) {
-    float m[kChunk], l[kChunk];
-    f32x4_t o[kChunk];
-#pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-      m[i] = kNegInf;
-      l[i] = 0.0f;
-      o[i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      if (s0 + i < n_split) {
-        const float* ps = p + (s0 + i) * kPartStride;
-        m[i] = ps[0];
-        l[i] = ps[1];
-        o[i] = *reinterpret_cast<const f32x4_t*>(ps + 4 + 4 * j);
-      }
-    }
+    if (s0 > 0) load_chunk(s0, nullptr);
     float cm = M;
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) cm = fmaxf(cm, m[i]);
@@ -317,7 +332,7 @@ __global__ __launch_bounds__(NT) void sink_attn_combine_kernel(const float* __re
     }
   }
   const float r = den > 0.0f ? 1.0f / den : 0.0f;
-  *reinterpret_cast<uint2*>(out + row * kD + 4 * j) =
+  *reinterpret_cast<uint2*>(out + static_cast<int64_t>(row) * kD + 4 * j) =
       make_uint2(E::pack(acc[0] * r, acc[1] * r), E::pack(acc[2] * r, acc[3] * r));
 }
 
@@ -426,13 +441,13 @@ int sink_attention_mfma(const void* q, const void* kv, const void* idx, int idx_
   const int64_t n = rows * H;
   const int nt = ceil_div(n, int64_t(8)) >= 256 ? 256 : 64;
   const int64_t n_wg = ceil_div(n, static_cast<int64_t>(nt / 32));
-  if (n_wg > 0x7fffffffLL) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many rows", who);
+  if (n > 0x7fffffffLL) return fail(AEKV_ERR_UNSUPPORTED, "%s: too many rows", who);
   const dim3 grid(static_cast<uint32_t>(n_wg));
   const uint16_t* sk = static_cast<const uint16_t*>(sink);
   uint16_t* o = static_cast<uint16_t*>(out);
   const int hh = static_cast<int>(H);
   auto launch = [&](auto kern) {
-    hipLaunchKernelGGL(kern, grid, dim3(nt), 0, st, part, p.n_split, sk, sink_scalar, hh, n, o);
+    hipLaunchKernelGGL(kern, grid, dim3(nt), 0, st, part, p.n_split, sk, sink_scalar, hh, static_cast<int>(n), o);
   };
   if (dtype == AEKV_BF16) {
     if (nt == 256) launch(sink_attn_combine_kernel<AEKV_BF16, 256>);
