@@ -548,7 +548,9 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
   if constexpr (TT == 1) {
     row[0] = blockIdx.y;
     rok[0] = true;
-    kr = row[0] / a.T;
+    // (32-bit: row < 65536, 1 <= T; a 64-bit division is a long emulated sequence ahead of the
+    // first loads)
+    kr = static_cast<uint32_t>(row[0]) / static_cast<uint32_t>(a.T);
   } else {
     // prefill: the linear workgroup ids are renumbered so that XCD x (linear id L runs on XCD
     // L % 8, each XCD with its own L2) runs the consecutive range [x n/8, (x+1) n/8) of (row group,
@@ -563,8 +565,9 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
       bx = w % nx;
     }
     const int64_t ngt = (a.T + TT - 1) / TT;
-    kr = by / ngt;
-    const int64_t t0 = (by % ngt) * TT;
+    const uint32_t by32 = static_cast<uint32_t>(by), ngt32 = static_cast<uint32_t>(ngt);  // both < 65536
+    kr = by32 / ngt32;
+    const int64_t t0 = static_cast<int64_t>(by32 - static_cast<uint32_t>(kr) * ngt32) * TT;
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
       rok[tt] = t0 + tt < a.T;

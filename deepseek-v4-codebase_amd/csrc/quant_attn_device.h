@@ -128,7 +128,7 @@ __device__ __forceinline__ RowSources attend_sources(const QAttnMfmaArgs& a, con
                                                      RowSel<NW>* sv) {
   constexpr int kT = 64 * NW;
   RowSources r;
-  r.cb = b / a.T;
+  r.cb = static_cast<uint32_t>(b) / static_cast<uint32_t>(a.T);  // (32-bit: b < 65536, 1 <= T)
   // the per-row counts are requested together, before any is used (one memory round)
   // (absent counts: all n_comp blocks, window from 0 to its end)
   const int32_t vis = load_or(a.vis, b, a.q, 0x7fffffff), ws = load_or(a.wstart, b, a.q, 0);

@@ -93,7 +93,7 @@ __global__ __launch_bounds__(64 * NW) void gather_attn_kernel(GatherArgs a) {
   const int64_t bt = blockIdx.x;  // b * T + t
   const int h0 = 16 * static_cast<int>(blockIdx.y);
   const int nh = min(16, a.H - h0);
-  const int64_t b = bt / a.T;
+  const int64_t b = static_cast<uint32_t>(bt) / static_cast<uint32_t>(a.T);  // (32-bit: bt < 2^31, 1 <= T)
   const int64_t K = a.K, S = a.S;
 
   // the target's queries as the B operand: lane (head c16), k-step ks = dims 32 ks + 8 g .. + 7
