@@ -199,7 +199,7 @@ def workspace(nbytes: int, device: torch.device, stream: int) -> Optional[torch.
 def require_device(name: str, *tensors: Optional[torch.Tensor]) -> None:
     """The product path runs on HIP devices only; CPU tensors are rejected loudly."""
     for t in tensors:
-        if t is not None and t.device.type != "cuda":
+        if t is not None and not t.is_cuda:  # (is_cuda: no device object built per tensor)
             raise RuntimeError(f"{name} must be a HIP device tensor (got {t.device}); aetherkv has no CPU path")
 
 

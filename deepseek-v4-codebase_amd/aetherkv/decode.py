@@ -33,8 +33,41 @@ def _check_out(name: str, t: torch.Tensor, dtype: torch.dtype, numel: int, devic
         raise RuntimeError(f"{name} must hold {numel} elements, got shape {tuple(t.shape)}")
     if not t.is_contiguous():
         raise RuntimeError(f"{name} must be contiguous")
-    if t.device != torch.device(device):
+    if t.device != (device if isinstance(device, torch.device) else torch.device(device)):
         raise RuntimeError(f"{name} must be on {device}, got {t.device}")
+
+
+# The decode entry points are called once per layer and token, so their host cost counts: a tensor
+# conversion or view builds a new tensor object (≈ 0.5–0.7 us each) even when it changes nothing,
+# so inputs already in the kernels' form are passed as they are.
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    """t as contiguous fp32 (t itself when it already is)."""
+    if t.dtype != torch.float32:
+        t = t.to(torch.float32)
+    return t.contiguous()
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    """t as contiguous int32 (t itself when it already is)."""
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    return t.contiguous()
+
+
+def _sink_f32(sink: torch.Tensor, H: int) -> torch.Tensor:
+    """The per-head sink as H contiguous fp32 values (a scalar is broadcast)."""
+    sk = _f32(sink)
+    n = sk.numel()
+    if n == 1 and H != 1:
+        return sk.reshape(1).expand(H).contiguous()
+    if n != H:
+        raise RuntimeError("sink must be a scalar or a [num_heads] tensor")
+    return sk
+
+
+def _like_q(out: torch.Tensor, q: torch.Tensor) -> torch.Tensor:
+    """The output in q's shape (a view only when the caller's buffer has another)."""
+    return out if out.dim() == q.dim() else out.view(q.shape)
 
 
 def _iptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -43,7 +76,7 @@ def _iptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 def _scale_2d(scale: torch.Tensor, B: int, S: int) -> torch.Tensor:
-    s = scale.to(torch.float32).contiguous()
+    s = _f32(scale)
     if s.numel() != B * S:
         raise RuntimeError(f"scale must hold B*S = {B * S} values, got shape {tuple(scale.shape)}")
     return s
@@ -133,11 +166,12 @@ def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tens
     _lib.require_device("q", q, codes, scale, sel, window, sink)
     if q.dtype != torch.bfloat16:
         raise RuntimeError(f"q must be bfloat16, got {q.dtype}")
-    squeeze = q.dim() == 4
-    q3 = q.reshape(q.size(0), q.size(-2), q.size(-1)) if squeeze else q
-    if squeeze and q.size(1) != 1:
+    qs = q.shape
+    if len(qs) == 4 and qs[1] != 1:
         raise RuntimeError("quant_sink_attention expects one target token per row")
-    B, H, D = q3.shape
+    if len(qs) not in (3, 4):
+        raise RuntimeError(f"q must be [B, 1, H, D] or [B, H, D], got {tuple(qs)}")
+    B, H, D = qs[0], qs[-2], qs[-1]
     S = codes.size(1)
     bits = quant.bits
     want = torch.int8 if bits == 8 else torch.uint8
@@ -145,8 +179,8 @@ def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tens
         raise RuntimeError(f"{bits}-bit codes must be {want}, got {codes.dtype}")
     if codes.size(-1) * (1 if bits == 8 else 2) != D or codes.size(0) != B:
         raise RuntimeError(f"codes shape {tuple(codes.shape)} does not match q {tuple(q.shape)}")
-    qc = q3.contiguous()
-    s64 = None if sel is None else sel.to(torch.int64).contiguous()
+    qc = q.contiguous()
+    s64 = None if sel is None else (sel if sel.dtype == torch.int64 else sel.to(torch.int64)).contiguous()
     K = -1 if s64 is None else s64.size(1)  # n_sel < 0: every block (HCA)
     stride = _prefix_rows(codes, scale) if s64 is None and not codes.is_contiguous() else None
     if stride is not None:
@@ -161,27 +195,23 @@ def quant_sink_attention(q: torch.Tensor, codes: torch.Tensor, scale: torch.Tens
         W = win.size(1)
     else:
         win, W = None, 0
-    sk = sink.to(torch.float32).reshape(-1).contiguous()
-    if sk.numel() == 1:
-        sk = sk.expand(H).contiguous()
-    if sk.numel() != H:
-        raise RuntimeError("sink must be a scalar or a [num_heads] tensor")
+    sk = _sink_f32(sink, H)
     diag = quant._diag(D, q.device)
     n_comp = K if K >= 0 else S
     if workspace is None:
         workspace = attention_workspace(B, H, D, n_comp, W, q.device)
-    if out is None:
-        out = torch.empty((B, H, D), dtype=torch.bfloat16, device=q.device)
-    else:
-        _check_out("out", out, torch.bfloat16, B * H * D, q.device)
     dev = q.device
+    if out is None:
+        out = torch.empty(qs, dtype=torch.bfloat16, device=dev)
+    else:
+        _check_out("out", out, torch.bfloat16, B * H * D, dev)
     with _lib.on_device(dev):
         rc = _lib.hot("aekv_quant_sink_attention")(
             qc.data_ptr(), cc.data_ptr(), sc.data_ptr(), _iptr(s64), _iptr(win), sk.data_ptr(), diag.data_ptr(), B, H,
             D, S if stride is None else stride, K, W, bits, float(softmax_scale), workspace.data_ptr(),
             workspace.numel(), out.data_ptr(), _lib.raw_stream(dev))
     _lib.check(rc, "aekv_quant_sink_attention")
-    return out.view(B, 1, H, D) if squeeze else out
+    return _like_q(out, q)
 
 
 def decode_workspace(B: int, S: int, k: int, H: int, D: int, W: int, device) -> torch.Tensor:
@@ -207,11 +237,13 @@ def csa_decode_step(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.
         raise ValueError(f"mode must be one of {sorted(_lib.INDEX_MODES)}, got {mode!r}")
     if q.dtype != torch.bfloat16:
         raise RuntimeError(f"q must be bfloat16, got {q.dtype}")
-    squeeze = q.dim() == 4
-    if squeeze and q.size(1) != 1:
+    qs = q.shape
+    if len(qs) == 4 and qs[1] != 1:
         raise RuntimeError("csa_decode_step expects one target token per row")
-    q3 = (q.reshape(q.size(0), q.size(-2), q.size(-1)) if squeeze else q).contiguous()
-    B, H, D = q3.shape
+    if len(qs) not in (3, 4):
+        raise RuntimeError(f"q must be [B, 1, H, D] or [B, H, D], got {tuple(qs)}")
+    q3 = q.contiguous()
+    B, H, D = qs[0], qs[-2], qs[-1]
     IB, IH, IC = index_q.shape
     S = kv_codes.size(1)
     if index_codes.size(1) != S or IB != B:
@@ -230,18 +262,14 @@ def csa_decode_step(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.
         W = win.size(1)
     else:
         win, W = None, 0
-    sk = sink.to(torch.float32).reshape(-1).contiguous()
-    if sk.numel() == 1:
-        sk = sk.expand(H).contiguous()
-    if sk.numel() != H:
-        raise RuntimeError("sink must be a scalar or a [num_heads] tensor")
-    iq = index_q.to(torch.float32).contiguous()
-    iw = index_weight.to(torch.float32).contiguous()
+    sk = _sink_f32(sink, H)
+    iq = _f32(index_q)
+    iw = _f32(index_weight)
     ic = index_codes.contiguous()
     isc = _scale_2d(index_scale, B, S)
     kc = _lib.aligned(kv_codes, 16)
     ksc = _scale_2d(kv_scale, B, S)
-    v = None if valid is None else valid.to(torch.int32).contiguous()
+    v = None if valid is None else _i32(valid)
     dev = q.device
     idiag = index_quant._diag(IC, dev)
     kdiag = kv_quant._diag(D, dev)
@@ -252,7 +280,7 @@ def csa_decode_step(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.
         _check_out("out_idx", out_idx, torch.int64, B * k, dev)
     scores = torch.empty((B, k), dtype=torch.float32, device=dev) if return_scores else None
     if out is None:
-        out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
+        out = torch.empty(qs, dtype=torch.bfloat16, device=dev)
     else:
         _check_out("out", out, torch.bfloat16, B * H * D, dev)
     if workspace is None:
@@ -264,7 +292,7 @@ def csa_decode_step(q: torch.Tensor, index_q: torch.Tensor, index_weight: torch.
             sk.data_ptr(), kdiag.data_ptr(), H, D, W, kv_quant.bits, float(softmax_scale), workspace.data_ptr(),
             workspace.numel(), out_idx.data_ptr(), _iptr(scores), out.data_ptr(), _lib.raw_stream(dev))
     _lib.check(rc, "aekv_csa_decode_quant")
-    o = out.view(B, 1, H, D) if squeeze else out
+    o = _like_q(out, q)
     return (o, out_idx, scores) if return_scores else (o, out_idx)
 
 
