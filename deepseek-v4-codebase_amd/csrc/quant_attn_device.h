@@ -727,10 +727,12 @@ __device__ __forceinline__ void dense_fetch(const QAttnMfmaArgs& a, const DenseR
 
 // One split [src0, src1) of decode row b over every block then every window entry (T = 1, no
 // selection, no counts).  The query's and the wave's first group's rows are requested together.
-// Without window entries in the split (!WIN), the second group's rows are requested once the query
-// fragments are built (their registers are free then) and each group is decoded while the group
-// after next is requested (two buffers, no copies).  A split with window entries (WIN: 64 more
-// bytes per lane and block) keeps one buffer: a group's successor is requested after it is decoded.
+// Without window entries in the split (!WIN), the second group's rows are requested in the same
+// round (the registers allow it: 196, two waves per SIMD either way; a wave that waited for the
+// query fragments before requesting them could stall on them after its first group) and each group
+// is decoded while the group after next is requested (two buffers, no copies).  A split with window
+// entries (WIN: 64 more bytes per lane and block) keeps one buffer: a group's successor is
+// requested after it is decoded.
 template <int BITS, int NW, bool WIN>
 __device__ __forceinline__ void attend_dense(const QAttnMfmaArgs& a, const int64_t b, const int split,
                                              unsigned char* lds) {
@@ -745,9 +747,13 @@ __device__ __forceinline__ void attend_dense(const QAttnMfmaArgs& a, const int64
   PrologueRaw praw;
   prologue_loads(a, b, praw);
   __builtin_amdgcn_sched_barrier(0);
-  GroupIn<BITS, WIN> in0;
+  GroupIn<BITS, WIN> in0, in1;
   dense_fetch<BITS, WIN>(a, rs, src0, src1, wv, in0);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (!WIN) {
+    dense_fetch<BITS, WIN>(a, rs, src0, src1, wv + kW, in1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   AttnFrags<BITS> f;
   prologue_build<BITS>(a, praw, f);
   AttnState s;
@@ -759,10 +765,6 @@ __device__ __forceinline__ void attend_dense(const QAttnMfmaArgs& a, const int64
       dense_fetch<BITS, WIN>(a, rs, src0, src1, G + kW, in0);
     }
   } else {
-    GroupIn<BITS, WIN> in1;
-    __builtin_amdgcn_sched_barrier(0);
-    dense_fetch<BITS, WIN>(a, rs, src0, src1, wv + kW, in1);
-    __builtin_amdgcn_sched_barrier(0);
     // Both buffers are decoded on every pass, so that no load is used only under a branch (the
     // compiler would move it there, after the wait it was meant to overlap).  A group past the split
     // has no sources and changes nothing (all keys masked: the state's factor is exactly 1).
