@@ -266,13 +266,6 @@ __device__ __forceinline__ void prologue_build(const QAttnMfmaArgs& a, const Pro
   }
 }
 
-template <int BITS>
-__device__ __forceinline__ void attend_prologue(const QAttnMfmaArgs& a, const int64_t b, AttnFrags<BITS>& f) {
-  PrologueRaw r;
-  prologue_loads(a, b, r);
-  prologue_build<BITS>(a, r, f);
-}
-
 // ---- one 32-source group of a wave: its rows requested, then decoded and attended -------------
 // A group is two blocks of 16 keys; lane (key c16 of block kb) holds its source's row: a code row
 // (kind 1, block id blk of cache row cb), a window row (kind 2, entry wrow) or nothing (kind 0).
@@ -580,13 +573,15 @@ __device__ __forceinline__ void attend_finish(const QAttnMfmaArgs& a, const int6
   }
 }
 
-// The row's attention over its sources (after attend_sources and attend_prologue).  win_lds
-// (nullable): the cache row's window entries 0 .. Wt-1 staged in LDS (win_chunk layout) instead of
-// read from global memory.  PIPE: a wave requests its next group's rows before decoding the
-// current one (the 4-wave prefill instance, whose register budget has room for them).
+// The row's attention over its sources (after attend_sources and the prologue's loads).  The query
+// fragments are built from praw once the wave's first group's rows are requested, so that the
+// gather does not wait for them.  win_lds (nullable): the cache row's window entries 0 .. Wt-1
+// staged in LDS (win_chunk layout) instead of read from global memory.  PIPE: a wave requests its
+// next group's rows before decoding the current one (the 4-wave prefill instance, whose register
+// budget has room for them).
 template <int BITS, int NW, bool PIPE = false>
 __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_t b, const int split,
-                                            unsigned char* lds, const AttnFrags<BITS>& f, const RowSources& rs,
+                                            unsigned char* lds, const PrologueRaw& praw, const RowSources& rs,
                                             const unsigned char* win_lds) {
   constexpr int kW = NW;
   using L = QLay<NW>;
@@ -618,10 +613,13 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
     }
     group_fetch<BITS>(a, cb, src, win_lds, in);
   };
+  AttnFrags<BITS> f;
   if constexpr (PIPE) {
     // the next group's rows are requested before this group is decoded
     GroupIn<BITS> cur, nxt;
     if (wv < n_groups) fetch(wv, cur);
+    __builtin_amdgcn_sched_barrier(0);
+    prologue_build<BITS>(a, praw, f);
 #pragma unroll 1
     for (int G = wv; G < n_groups; G += kW) {
       const bool more = G + kW < n_groups;  // wave-uniform
@@ -630,29 +628,36 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
       if (more) cur = nxt;
     }
   } else {
+    bool built = false;  // wave-uniform
 #pragma unroll 1
     for (int G = wv; G < n_groups; G += kW) {
       GroupIn<BITS> in;
       fetch(G, in);
+      if (!built) {
+        __builtin_amdgcn_sched_barrier(0);
+        prologue_build<BITS>(a, praw, f);
+        built = true;
+      }
       group_consume<BITS>(a, f, in, s);
     }
+    if (!built) prologue_build<BITS>(a, praw, f);  // (a wave without a group)
   }
   // ---- merge the waves (and the sink, unless this is one split of several) ----
   attend_finish<NW>(a, b, split, lds, s, f.sink, f.neg);
 }
 
 
-// attend_sources + attend_prologue + store_sel + attend_main: the row's counts, its selected block
+// attend_sources + prologue_loads + store_sel + attend_main: the row's counts, its selected block
 // ids and the prologue's loads are requested in one memory round.
 template <int BITS, int NW>
 __device__ __forceinline__ void attend_row(const QAttnMfmaArgs& a, const int64_t b, const int split,
                                            unsigned char* lds) {
   RowSel<NW> sv;
   const RowSources rs = attend_sources<NW>(a, b, split, a.sel ? &sv : nullptr);
-  AttnFrags<BITS> f;
-  attend_prologue<BITS>(a, b, f);
+  PrologueRaw praw;
+  prologue_loads(a, b, praw);
   if (a.sel) store_sel<NW>(a, rs, sv, lds);
-  attend_main<BITS, NW, NW == 4>(a, b, split, lds, f, rs, nullptr);
+  attend_main<BITS, NW, NW == 4>(a, b, split, lds, praw, rs, nullptr);
 }
 
 // ---- rows that attend every block, without per-row counts (the decode step's HCA call) ----
