@@ -942,20 +942,23 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
 #pragma unroll
         for (int e = 0; e < 4; ++e) kw[4 * q + e] = v[e];
       }
-      uint32_t c = 0;
       const int n_in = static_cast<int>(min<int64_t>(16, nv - 16 * sl));  // the slot's visible keys
+      uint32_t qm = 0u;  // the slot's keys >= tau (about one per listed slot)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) c += (e < n_in && kw[e] >= tau) ? 1u : 0u;
-      uint32_t p = wave_reserve<5>(&s_cnt[0], c);  // c <= 16
+      for (int e = 0; e < 16; ++e) qm |= (e < n_in && kw[e] >= tau) ? (1u << e) : 0u;
+      uint32_t p = wave_reserve<5>(&s_cnt[0], static_cast<uint32_t>(__builtin_popcount(qm)));  // <= 16
+      // only the qualifying keys are visited (a loop over the set bits, not over all 16)
+      while (qm != 0u) {
+        const int e = __builtin_ctz(qm);
+        qm &= qm - 1u;
+        uint32_t ke = kw[0];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        if (e < n_in && kw[e] >= tau) {
-          if (p < static_cast<uint32_t>(CAP)) {
-            ck[p] = kw[e];
-            ci[p] = static_cast<uint32_t>(16 * sl + e);
-          }
-          ++p;
+        for (int e2 = 1; e2 < 16; ++e2) ke = e == e2 ? kw[e2] : ke;  // (a select: no runtime index)
+        if (p < static_cast<uint32_t>(CAP)) {
+          ck[p] = ke;
+          ci[p] = static_cast<uint32_t>(16 * sl + e);
         }
+        ++p;
       }
     }
   }
