@@ -29,7 +29,7 @@ constexpr int kFusedMaxK = 512;     // largest k the 512-thread select sorts out
 constexpr int kFusedMaxW = 128;     // window rows: 16 per wave
 using FusedLay = qattn::QLay<8>;
 
-template <int KV_BITS>
+template <int KV_BITS, int COLS>
 __global__ __launch_bounds__(kFusedThreads) void csa_decode_fused_kernel(idx::MfmaIdxArgs ia, qattn::QAttnMfmaArgs qa,
                                                                        int64_t* __restrict__ out_idx,
                                                                        float* __restrict__ out_score) {
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(kFusedThreads) void csa_decode_fused_kernel(idx::Mf
     qattn::prologue_build<KV_BITS>(qa, praw, f);
     built = true;
   };
-  const uint32_t kk = idx::select_row<kFusedThreads, kFusedCap>(ia, b, out_idx, out_score, sel_lds, build);
+  const uint32_t kk = idx::select_row<kFusedThreads, kFusedCap, COLS>(ia, b, out_idx, out_score, sel_lds, build);
   if (!built) build();  // a row with no visible block skips the select's memory rounds
   __syncthreads();      // sel_lds
   auto window = [&]() {
@@ -167,10 +167,14 @@ extern "C" int aekv_csa_decode_quant(const float* index_q, const float* index_we
   qa.sm_scale = softmax_scale;
   qa.wscale = wht_scale(qattn::kD);
   qa.out = static_cast<uint16_t*>(out);
-  auto fn = kv_bits == 8 ? csa_decode_fused_kernel<8> : csa_decode_fused_kernel<4>;
+  // rows of at most 16384 keys: the select loads 2 slot columns per thread instead of 8
+  constexpr int kWide = idx::kHistBins / kFusedThreads;
+  const bool few = idx::slot_cols_fit(S, kFusedThreads, 2);
+  auto fn = kv_bits == 8 ? (few ? csa_decode_fused_kernel<8, 2> : csa_decode_fused_kernel<8, kWide>)
+                         : (few ? csa_decode_fused_kernel<4, 2> : csa_decode_fused_kernel<4, kWide>);
   const size_t lds = FusedLay::bytes;
-  static std::once_flag once[2];
-  std::call_once(once[kv_bits == 8 ? 1 : 0], [&] {
+  static std::once_flag once[4];
+  std::call_once(once[(kv_bits == 8 ? 2 : 0) + (few ? 1 : 0)], [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                               static_cast<int>(lds));
   });

@@ -94,11 +94,16 @@ int launch_mfma_indexer(const float* q, const float* w, const void* codes, const
   if (int rc = launch_mfma_score(a, q, w, codes, kscale, diag, valid, B, T, S, IH, IC, bits, k, mode, ws, st, who))
     return rc;
   const uint32_t by = static_cast<uint32_t>(B);
-  if (B >= 1024 && k <= 512)
-    hipLaunchKernelGGL((idx_mfma_final_kernel<512, 1536>), dim3(by), dim3(512), 0, st, a, out_idx, out_score);
-  else
-    hipLaunchKernelGGL((idx_mfma_final_kernel<kSelThreads, kCandCap>), dim3(by), dim3(kSelThreads), 0, st, a, out_idx,
-                       out_score);
+  // rows of at most 16384 keys load 2 (512 threads) or 1 (1024 threads) slot columns per thread
+  const bool few_slots = slot_cols_fit(S, 512, 2);
+  if (B >= 1024 && k <= 512) {
+    auto fn = few_slots ? idx_mfma_final_kernel<512, 1536, 2> : idx_mfma_final_kernel<512, 1536, kHistBins / 512>;
+    hipLaunchKernelGGL(fn, dim3(by), dim3(512), 0, st, a, out_idx, out_score);
+  } else {
+    auto fn = few_slots ? idx_mfma_final_kernel<kSelThreads, kCandCap, 1>
+                        : idx_mfma_final_kernel<kSelThreads, kCandCap, kHistBins / kSelThreads>;
+    hipLaunchKernelGGL(fn, dim3(by), dim3(kSelThreads), 0, st, a, out_idx, out_score);
+  }
   return check_launch(who);
 }
 

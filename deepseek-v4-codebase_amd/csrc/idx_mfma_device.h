@@ -773,12 +773,16 @@ __device__ __forceinline__ uint64_t sort_word(uint32_t key, uint32_t idx) {
 // that continues with them in the same workgroup.  during_wait: work of the caller's that needs no
 // result of the select, run once, with the first slot maxima requested and not yet used (every
 // thread of the workgroup calls it at the same point; rows with no visible block skip it).
+// COLS: slot maxima each thread loads per pass (a pass covers COLS * NT slots); launches whose
+// rows have at most 16 * COLS * NT keys take the smallest COLS that covers them, so that no thread
+// issues loads that only fall past the row (each is an instruction through the CU's address unit
+// in the workgroup's first memory round, and a register held until the list is built).
 // Returns kk = min(k, visible count).
 struct NoHook {
   __device__ void operator()() const {}
 };
 
-template <int NT, int CAP, typename Hook = NoHook>
+template <int NT, int CAP, int COLS = kHistBins / NT, typename Hook = NoHook>
 __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b, int64_t* __restrict__ out_idx,
                                                float* __restrict__ out_score, int32_t* __restrict__ sel_lds,
                                                Hook&& during_wait = Hook{}) {
@@ -823,9 +827,10 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(krow), 0, n_slots_i * 64, 0x00020000);
 
   // ---- 1. slot bound and candidates ----
-  // thread tid owns slots c0 + tid + r * NT (r < kSlotPer) of each pass of 4096 slots; with
-  // n_slots <= 4096 (S <= 65536) the maxima loaded for the histogram are reused for the scan
-  constexpr int kSlotPer = kHistBins / NT;  // one pass over the slot maxima for S <= 65536
+  // thread tid owns slots c0 + tid + r * NT (r < kSlotPer) of each pass of kSlotPass slots; with
+  // n_slots <= kSlotPass the maxima loaded for the histogram are reused for the scan
+  static_assert(COLS >= 1 && COLS <= kHistBins / NT, "slot columns: 1 .. kHistBins / NT");
+  constexpr int kSlotPer = COLS;  // one pass over the slot maxima for S <= 16 * COLS * NT
   constexpr int64_t kSlotPass = static_cast<int64_t>(kSlotPer) * NT;
   for (int i = tid; i < kHistBins; i += NT) h[i] = 0u;
   if (tid == 0) {
@@ -1155,11 +1160,17 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
 
 // The 512-thread instance serves launches of many rows: bounded to 64 VGPRs (eight waves per SIMD),
 // so that four rows share a CU (it needs 57).
-template <int NT, int CAP>
+template <int NT, int CAP, int COLS>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 512 ? 8 : 1))) void idx_mfma_final_kernel(
     MfmaIdxArgs a, int64_t* __restrict__ out_idx, float* __restrict__ out_score) {
   touch_kernargs<sizeof(a) + 2 * sizeof(void*)>();
-  select_row<NT, CAP>(a, blockIdx.x, out_idx, out_score, nullptr);
+  select_row<NT, CAP, COLS>(a, blockIdx.x, out_idx, out_score, nullptr);
+}
+
+// Whether every 16-key slot of rows of at most S keys lies within `cols` slot columns of NT
+// threads (the select instance with COLS = cols then makes one pass over them).
+__host__ __device__ constexpr bool slot_cols_fit(int64_t S, int NT, int cols) {
+  return (S + 15) / 16 <= static_cast<int64_t>(cols) * NT;
 }
 
 // Launch set-up shared by the indexer and the fused CSA decode step: fills the kernel arguments
