@@ -185,24 +185,38 @@ struct AttnFrags {
 // is not read as 32 dims per lane.
 struct PrologueRaw {
   float dv[2];
-  uint2 lo[4], hi[4];
+  uint4 qw[4];
   float sink;
 };
+
+// A bf16 row of kD dims held by the lane pair l, l ^ 16 (lane groups g, g ^ 1: one 16-lane column)
+// as one 16-byte piece per lane and k-step: dims 16 (2 ks + (g & 1)) + 8 (g >> 1) + 0..7.  The
+// operands want, per lane, dims 32 ks + 4 g + 0..3 (lo) and 32 ks + 16 + 4 g + 0..3 (hi); a lane's
+// piece holds its own lo (g even) or hi (g odd) and its partner's other half, so one
+// permlane16_swap per dword pair (odd rows of the first operand swapped with even rows of the
+// second) hands each half to its lane.  Both lanes of a pair must run it.  Loading 16-byte pieces
+// halves the load instructions of a row (each one a pass through the CU's address unit).
+__device__ __forceinline__ int pair_piece_dims(int g) { return 16 * (g & 1) + 8 * (g >> 1); }
+
+__device__ __forceinline__ void pair_halves(const uint4& p, uint2& lo, uint2& hi) {
+  const auto sx = __builtin_amdgcn_permlane16_swap(p.x, p.z, false, false);
+  const auto sy = __builtin_amdgcn_permlane16_swap(p.y, p.w, false, false);
+  const uint32_t lx = sx[0], hx = sx[1], ly = sy[0], hy = sy[1];  // (elements copied out first)
+  lo = make_uint2(lx, ly);
+  hi = make_uint2(hx, hy);
+}
 
 __device__ __forceinline__ void prologue_loads(const QAttnMfmaArgs& a, const int64_t b, PrologueRaw& r) {
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
   // The lane's 32 dims, for every key it holds: element j of k-step ks (bf16x8) is dim
-  // 16*(2ks + (j >> 2)) + 4g + (j & 3).  Every load (the diagonal, the query row of head c16) is
-  // issued before any is used: one memory round.  Lanes past the heads read head 0's row and use
-  // zeros.
-  const uint16_t* qr = a.q + (b * a.H + (c16 < a.H ? c16 : 0)) * kD + 4 * g;
+  // 16*(2ks + (j >> 2)) + 4g + (j & 3); the query row of head c16 arrives as pair pieces
+  // (pair_halves).  Every load (the diagonal, the query row) is issued before any is used: one
+  // memory round.  Lanes past the heads read head 0's row and use zeros.
+  const uint16_t* qr = a.q + (b * a.H + (c16 < a.H ? c16 : 0)) * kD + pair_piece_dims(g);
   r.dv[0] = a.diag[lane];
   r.dv[1] = a.diag[64 + lane];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    r.lo[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks));
-    r.hi[ks] = *reinterpret_cast<const uint2*>(qr + 16 * (2 * ks + 1));
-  }
+  for (int ks = 0; ks < 4; ++ks) r.qw[ks] = *reinterpret_cast<const uint4*>(qr + 32 * ks);
   const int th = static_cast<int>(threadIdx.x >> 3) < a.H ? static_cast<int>(threadIdx.x >> 3) : 0;
   r.sink = a.n_split == 1 ? a.sink[th] : 0.0f;
 }
@@ -211,8 +225,9 @@ template <int BITS>
 __device__ __forceinline__ void prologue_build(const QAttnMfmaArgs& a, const PrologueRaw& r, AttnFrags<BITS>& f) {
   const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
   const bool has_head = c16 < a.H;
-  const uint2 (&lo)[4] = r.lo;
-  const uint2 (&hi)[4] = r.hi;
+  uint2 lo[4], hi[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) pair_halves(r.qw[ks], lo[ks], hi[ks]);
   f.sink = r.sink;
   // dsign: the diagonal's sign bits for the lane's dims, per packed bf16 pair (dword e of k-step
   // ks), from the signs of all 128 dims (bit d of neg[d >> 6], every lane of the wave active)
@@ -275,7 +290,7 @@ struct GroupIn {
   int kind[2];
   uint32_t cw[2][2][BITS == 8 ? 4 : 2];
   float sraw[2];
-  uint2 wv2[WIN ? 2 : 1][4][2];
+  uint4 wq[WIN ? 2 : 1][4];  // window rows as pair pieces (pair_halves)
 };
 
 // The lane's source of block kb: kind and block id (kind 1) or window entry (kind 2).
@@ -322,21 +337,18 @@ __device__ __forceinline__ void group_fetch(const QAttnMfmaArgs& a, const int64_
     if (WIN && src[kb].kind == 2) {
       const int64_t wrow = src[kb].at;
       if (win_lds) {
-        // dims 32ks + 4g (+16): chunk 4ks + g/2 (+2), bytes 8(g & 1) .. +8 of it
+        // the pair piece of k-step ks, dims 16 (2ks + (g & 1)) + 8 (g >> 1): 16-byte chunk
+        // 4ks + 2 (g & 1) + (g >> 1) of the row
         const int r = static_cast<int>(wrow);
-        const unsigned char* rp = win_lds + 2 * kD * r + 8 * (g & 1);
+        const unsigned char* rp = win_lds + 2 * kD * r;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          in.wv2[WIN ? kb : 0][ks][0] = *reinterpret_cast<const uint2*>(rp + 16 * win_chunk(r, 4 * ks + (g >> 1)));
-          in.wv2[WIN ? kb : 0][ks][1] = *reinterpret_cast<const uint2*>(rp + 16 * win_chunk(r, 4 * ks + 2 + (g >> 1)));
-        }
+        for (int ks = 0; ks < 4; ++ks)
+          in.wq[WIN ? kb : 0][ks] =
+              *reinterpret_cast<const uint4*>(rp + 16 * win_chunk(r, 4 * ks + 2 * (g & 1) + (g >> 1)));
       } else {
-        const uint16_t* wr = a.win + (cb * a.Wt + wrow) * kD + 4 * g;
+        const uint16_t* wr = a.win + (cb * a.Wt + wrow) * kD + pair_piece_dims(g);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          in.wv2[WIN ? kb : 0][ks][0] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks));
-          in.wv2[WIN ? kb : 0][ks][1] = *reinterpret_cast<const uint2*>(wr + 16 * (2 * ks + 1));
-        }
+        for (int ks = 0; ks < 4; ++ks) in.wq[WIN ? kb : 0][ks] = *reinterpret_cast<const uint4*>(wr + 32 * ks);
       }
     }
   }
@@ -370,7 +382,7 @@ __device__ __forceinline__ void group_consume(const QAttnMfmaArgs& a, const Attn
   const int (&kind)[2] = in.kind;
   const auto& cw = in.cw;
   const float (&sraw)[2] = in.sraw;
-  const auto& wv2 = in.wv2;
+  const auto& wq = in.wq;
   // a group with no source at all (past the end of a piece) changes nothing
   if (__builtin_amdgcn_ballot_w64(kind[0] != 0 || kind[1] != 0) == 0) return;
   const float kscale_unit = (BITS == 4 ? 1.0f / 16.0f : 1.0f) * a.wscale;
@@ -403,12 +415,15 @@ __device__ __forceinline__ void group_consume(const QAttnMfmaArgs& a, const Attn
     for (int ks = 0; ks < 4; ++ks) {
       uint32_t w4[4];
       if (WIN && kind[kb] == 2) {
-        constexpr int kw = 0;  // (wv2 has one block without window rows)
+        constexpr int kw = 0;  // (wq has one block without window rows)
         const int wb = WIN ? kb : kw;
-        w4[0] = wv2[wb][ks][0].x ^ dsign[ks][0];
-        w4[1] = wv2[wb][ks][0].y ^ dsign[ks][1];
-        w4[2] = wv2[wb][ks][1].x ^ dsign[ks][2];
-        w4[3] = wv2[wb][ks][1].y ^ dsign[ks][3];
+        // (the lane pair of a window row shares its kind: kinds depend on the column c16 only)
+        uint2 lo, hi;
+        pair_halves(wq[wb][ks], lo, hi);
+        w4[0] = lo.x ^ dsign[ks][0];
+        w4[1] = lo.y ^ dsign[ks][1];
+        w4[2] = hi.x ^ dsign[ks][2];
+        w4[3] = hi.y ^ dsign[ks][3];
       } else {
         float v[8];
 #pragma unroll
@@ -718,13 +733,12 @@ __device__ __forceinline__ void dense_fetch(const QAttnMfmaArgs& a, const DenseR
     in.sraw[kb] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                 rs.scale, is_code ? static_cast<uint32_t>(si) * 4 : kPastRange, 0, 0));
     if constexpr (WIN) {
-      const uint32_t wo = is_win ? static_cast<uint32_t>(si - n_comp) * (2 * kD) + 8 * g : kPastRange;
+      const uint32_t wo =
+          is_win ? static_cast<uint32_t>(si - n_comp) * (2 * kD) + 2 * pair_piece_dims(g) : kPastRange;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const auto w0 = __builtin_amdgcn_raw_buffer_load_b64(rs.win, wo + 64 * ks, 0, 0);
-        const auto w1 = __builtin_amdgcn_raw_buffer_load_b64(rs.win, wo + 64 * ks + 32, 0, 0);
-        in.wv2[kb][ks][0] = make_uint2(w0[0], w0[1]);
-        in.wv2[kb][ks][1] = make_uint2(w1[0], w1[1]);
+        const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs.win, wo + 64 * ks, 0, 0);
+        in.wq[kb][ks] = make_uint4(w[0], w[1], w[2], w[3]);
       }
     }
   }
