@@ -41,34 +41,29 @@ __global__ __launch_bounds__(kFusedThreads) void csa_decode_fused_kernel(idx::Mf
   const int lane = threadIdx.x & 63, c16 = lane & 15;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = static_cast<int>(qa.Wt);
-  // first memory round (with the select's count): the wave's window entries 16 wv .. 16 wv + 15 as
-  // block 0 of a group (lanes past W read entry 0 and are masked), and the query and diagonal
+  // first memory round: the query and diagonal, then the row's visible count (a scalar load: the
+  // select's slot ranges wait for it alone), then the select's slot maxima
   const bool has_win = 16 * wv < W;  // wave-uniform
   const bool wok = 16 * wv + c16 < W;
-  qattn::GroupIn<KV_BITS> win_in;
-  if (has_win) {
-    qattn::SrcRef wsrc[2];
-    wsrc[0].kind = 2;
-    wsrc[0].at = wok ? 16 * wv + c16 : 0;
-    wsrc[1].kind = 0;
-    wsrc[1].at = -1;
-    qattn::group_fetch<KV_BITS>(qa, b, wsrc, nullptr, win_in);
-  }
   qattn::PrologueRaw praw;
   qattn::prologue_loads(qa, b, praw);
+  const int64_t nv = idx::visible(ia, b);
   qattn::AttnFrags<KV_BITS> f;
   qattn::AttnState st;
   qattn::attn_state_init(st);
-  // the query fragments are built while the select waits for its slot maxima (they arrive with the
-  // query); the window rows, which arrive then too, are attended after the select, while the
-  // wave's first group of selected rows is requested, so that the select starts as soon as its
-  // maxima are in
+  // While the select waits for its maxima: the wave's window entries 16 wv .. 16 wv + 15 are
+  // requested (block 0 of a group, entries past W no source) and the query fragments built.  The
+  // window rows are requested after the maxima because loads complete in order: ahead of them they
+  // delay the select, and they are only attended after it, while the wave's first group of
+  // selected rows is requested.
+  qattn::GroupIn<KV_BITS> win_in;
   bool built = false;
   auto build = [&]() {
+    qattn::window_fetch<KV_BITS>(qa, b, 16 * wv + c16, win_in);
     qattn::prologue_build<KV_BITS>(qa, praw, f);
     built = true;
   };
-  const uint32_t kk = idx::select_row<kFusedThreads, kFusedCap, COLS>(ia, b, out_idx, out_score, sel_lds, build);
+  const uint32_t kk = idx::select_row<kFusedThreads, kFusedCap, COLS>(ia, b, nv, out_idx, out_score, sel_lds, build);
   if (!built) build();  // a row with no visible block skips the select's memory rounds
   __syncthreads();      // sel_lds
   auto window = [&]() {

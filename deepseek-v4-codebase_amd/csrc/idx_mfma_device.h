@@ -123,8 +123,15 @@ inline WsLayout layout(int64_t B, int64_t S) {
   return l;
 }
 
+// Row b's visible count (b uniform over the workgroup; S without counts).  The count is read
+// through the constant address space, which makes it a scalar load: the wait for it (where the
+// null check's branch joins) leaves the vector memory counter alone, so it does not wait for
+// vector requests issued before it (a vector load here had made that wait cover the caller's
+// whole first memory round).  Integer compares: min<int64_t> lowers through doubles here.
 __device__ __forceinline__ int64_t visible(const MfmaIdxArgs& a, int b) {
-  return a.valid ? min<int64_t>(a.S, max(0, a.valid[b])) : a.S;
+  if (!a.valid) return a.S;
+  const int32_t v = *(const __attribute__((address_space(4))) int32_t*)(a.valid + b);
+  return v <= 0 ? 0 : (v < a.S ? v : a.S);
 }
 
 // digit position -> index c of the key element for lane group g, byte position p of k-step ks
@@ -782,10 +789,12 @@ struct NoHook {
   __device__ void operator()() const {}
 };
 
+// nv: the row's visible count, visible(a, b), read by the caller (after requests of its own that
+// do not depend on it).
 template <int NT, int CAP, int COLS = kHistBins / NT, typename Hook = NoHook>
-__device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b, int64_t* __restrict__ out_idx,
-                                               float* __restrict__ out_score, int32_t* __restrict__ sel_lds,
-                                               Hook&& during_wait = Hook{}) {
+__device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b, const int64_t nv,
+                                               int64_t* __restrict__ out_idx, float* __restrict__ out_score,
+                                               int32_t* __restrict__ sel_lds, Hook&& during_wait = Hook{}) {
   constexpr bool kHook = !std::is_same<std::decay_t<Hook>, NoHook>::value;
   constexpr int NW = NT / 64;
   __shared__ uint64_t cbuf[CAP];  // candidates: keys ck[] then indices ci[], or sort words
@@ -795,7 +804,6 @@ __device__ __forceinline__ uint32_t select_row(const MfmaIdxArgs& a, const int b
   uint32_t* ck = reinterpret_cast<uint32_t*>(cbuf);
   uint32_t* ci = ck + CAP;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int64_t nv = visible(a, b);
   const int k = a.k;
   const uint32_t kk = static_cast<uint32_t>(min<int64_t>(k, nv));
   int64_t* orow = out_idx + static_cast<int64_t>(b) * k;
@@ -1164,7 +1172,7 @@ template <int NT, int CAP, int COLS>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 512 ? 8 : 1))) void idx_mfma_final_kernel(
     MfmaIdxArgs a, int64_t* __restrict__ out_idx, float* __restrict__ out_score) {
   touch_kernargs<sizeof(a) + 2 * sizeof(void*)>();
-  select_row<NT, CAP, COLS>(a, blockIdx.x, out_idx, out_score, nullptr);
+  select_row<NT, CAP, COLS>(a, blockIdx.x, visible(a, blockIdx.x), out_idx, out_score, nullptr);
 }
 
 // Whether every 16-key slot of rows of at most S keys lies within `cols` slot columns of NT

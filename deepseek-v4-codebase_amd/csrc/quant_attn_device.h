@@ -354,6 +354,37 @@ __device__ __forceinline__ void group_fetch(const QAttnMfmaArgs& a, const int64_
   }
 }
 
+constexpr uint32_t kPastRange = 0x80000000u; // an offset past every range (ranges are < 2^31 bytes)
+
+// Window entry e (< Wt, else no source) of decode row b as block 0 of lane column c16's group
+// (block 1 empty), its row as pair pieces, through a buffer resource over the row's Wt entries: the
+// loads are unconditional (a branch around them would make the compiler copy their registers, and
+// so wait for them, where the branch joins) and an entry past Wt reads zeros without a memory
+// access.  Rows of Wt * kD * 2 < 2^31 bytes.
+template <int BITS>
+__device__ __forceinline__ void window_fetch(const QAttnMfmaArgs& a, const int64_t b, const int e, GroupIn<BITS>& in) {
+  const int g = (threadIdx.x & 63) >> 4;
+  const bool ok = e < a.Wt;
+  in.kind[0] = ok ? 2 : 0;
+  in.kind[1] = 0;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int i = 0; i < (BITS == 8 ? 4 : 2); ++i) in.cw[kb][hh][i] = 0u;
+    in.sraw[kb] = 0.0f;
+  }
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.win + b * a.Wt * kD), 0, static_cast<int>(a.Wt * kD * 2), 0x00020000);
+  const uint32_t o = ok ? static_cast<uint32_t>(e) * (2 * kD) + 2 * pair_piece_dims(g) : kPastRange;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, o + 64 * ks, 0, 0);
+    in.wq[0][ks] = make_uint4(v[0], v[1], v[2], v[3]);
+  }
+}
+
 // Online-softmax state and output of head c16 (replicated over the four lane groups).
 struct AttnState {
   float m_run, l_run;
@@ -682,7 +713,6 @@ __device__ __forceinline__ void attend_row(const QAttnMfmaArgs& a, const int64_t
 // compiler leaves where they are written (it may merge or move plain loads that feed a loop
 // variable down to their first use, which undoes a prefetch).
 constexpr uint32_t kBufWord3 = 0x00020000u;  // 32-bit data, raw (unswizzled) addressing
-constexpr uint32_t kPastRange = 0x80000000u; // an offset past every range (ranges are < 2^31 bytes)
 
 struct DenseRsrc {
   __amdgpu_buffer_rsrc_t codes, scale, win;
