@@ -120,32 +120,56 @@ struct RowSel {
   int64_t v[kSplitSrc / (64 * NW)];
 };
 
-// The row's source ranges.  With sv, the selected block ids of the workgroup's piece are requested
-// as well, over the whole piece of the row's selection (in bounds; entries past the visible count
-// are never read), so that they need not wait for the counts; store_sel puts them in LDS.
+// A row's raw per-row counts (visible blocks, window start and length), as loaded.
+struct RowCounts {
+  int32_t vis, ws, wl;
+};
+
+// The row's loads that set its sources: the per-row counts and the selected block ids of the
+// workgroup's piece (which do not depend on the counts).  Only requests: the caller issues its
+// other first-round loads before anything reads these (attend_ranges), so that one memory round
+// covers them all (vector loads complete in order, and a count used early, or a load under a
+// branch, is waited for before the later requests are issued).  The id loads are unconditional,
+// through a buffer resource over the piece's ids (past it, or without a selection: 0 without a
+// memory access); store_sel reads only ids below the row's selected count, which lie in the piece.
+// (absent counts: all n_comp blocks, window from 0 to its end)
 template <int NW>
-__device__ __forceinline__ RowSources attend_sources(const QAttnMfmaArgs& a, const int64_t b, const int split,
-                                                     RowSel<NW>* sv) {
+__device__ __forceinline__ void attend_requests(const QAttnMfmaArgs& a, const int64_t b, const int split,
+                                                RowCounts& c, RowSel<NW>& sv) {
   constexpr int kT = 64 * NW;
+  // scalar loads (b is uniform; through the constant address space): a vector load of a uniform
+  // value is moved to a scalar register right where it is loaded, which waits for it there
+  auto count = [&](const int32_t* p, int32_t dflt) {
+    const int32_t v = *(const __attribute__((address_space(4))) int32_t*)(p ? p + b : reinterpret_cast<const int32_t*>(a.q));
+    return p ? v : dflt;
+  };
+  c.vis = count(a.vis, 0x7fffffff);
+  c.ws = count(a.wstart, 0);
+  c.wl = count(a.wlen, 0x7fffffff);
+  const int64_t src0 = static_cast<int64_t>(split) * a.split_src;
+  const int64_t rest = a.sel ? a.K - src0 : 0;
+  const int n_piece = static_cast<int>(rest < a.split_src ? rest : a.split_src);  // <= kSplitSrc
+  const __amdgpu_buffer_rsrc_t ids = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int64_t*>(a.sel ? a.sel + b * a.K + src0 : a.sel), 0, n_piece > 0 ? 8 * n_piece : 0, 0x00020000);
+#pragma unroll
+  for (int j = 0; j < kSplitSrc / kT; ++j) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(ids, (threadIdx.x + j * kT) * 8u, 0, 0);
+    sv.v[j] = static_cast<int64_t>((static_cast<uint64_t>(v[1]) << 32) | v[0]);
+  }
+}
+
+// The row's source ranges from its counts.  Integer clamps (min<int64_t> lowers through doubles).
+__device__ __forceinline__ RowSources attend_ranges(const QAttnMfmaArgs& a, const int64_t b, const int split,
+                                                    const RowCounts& c) {
+  auto clamp = [](int64_t x, int64_t hi) { return x <= 0 ? int64_t{0} : (x < hi ? x : hi); };
   RowSources r;
   r.cb = static_cast<uint32_t>(b) / static_cast<uint32_t>(a.T);  // (32-bit: b < 65536, 1 <= T)
-  // the per-row counts are requested together, before any is used (one memory round)
-  // (absent counts: all n_comp blocks, window from 0 to its end)
-  const int32_t vis = load_or(a.vis, b, a.q, 0x7fffffff), ws = load_or(a.wstart, b, a.q, 0);
-  const int32_t wl = load_or(a.wlen, b, a.q, 0x7fffffff);
-  r.n_comp = min<int64_t>(max(vis, 0), a.n_comp);
-  r.w0 = min<int64_t>(max(ws, 0), a.Wt);
-  r.wl = min<int64_t>(max(wl, 0), a.Wt - r.w0);
+  r.n_comp = clamp(c.vis, a.n_comp);
+  r.w0 = clamp(c.ws, a.Wt);
+  r.wl = clamp(c.wl, a.Wt - r.w0);
   r.src0 = static_cast<int64_t>(split) * a.split_src;
-  if (sv) {
-    const int64_t n_piece = min<int64_t>(a.K - r.src0, a.split_src);
-#pragma unroll
-    for (int j = 0; j < kSplitSrc / kT; ++j) {
-      const int64_t i = threadIdx.x + static_cast<int64_t>(j) * kT;
-      sv->v[j] = i < n_piece ? a.sel[b * a.K + r.src0 + i] : -1;
-    }
-  }
-  r.src1 = min<int64_t>(r.n_comp + r.wl, r.src0 + a.split_src);
+  const int64_t end = r.src0 + a.split_src;
+  r.src1 = r.n_comp + r.wl < end ? r.n_comp + r.wl : end;
   return r;
 }
 
@@ -619,7 +643,7 @@ __device__ __forceinline__ void attend_finish(const QAttnMfmaArgs& a, const int6
   }
 }
 
-// The row's attention over its sources (after attend_sources and the prologue's loads).  The query
+// The row's attention over its sources (after attend_ranges and the prologue's loads).  The query
 // fragments are built from praw once the wave's first group's rows are requested, so that the
 // gather does not wait for them.  win_lds (nullable): the cache row's window entries 0 .. Wt-1
 // staged in LDS (win_chunk layout) instead of read from global memory.  PIPE: a wave requests its
@@ -693,15 +717,18 @@ __device__ __forceinline__ void attend_main(const QAttnMfmaArgs& a, const int64_
 }
 
 
-// attend_sources + prologue_loads + store_sel + attend_main: the row's counts, its selected block
-// ids and the prologue's loads are requested in one memory round.
+// attend_requests + prologue_loads + attend_ranges + store_sel + attend_main: the row's counts, its
+// selected block ids and the prologue's loads are requested in one memory round.
 template <int BITS, int NW>
 __device__ __forceinline__ void attend_row(const QAttnMfmaArgs& a, const int64_t b, const int split,
                                            unsigned char* lds) {
   RowSel<NW> sv;
-  const RowSources rs = attend_sources<NW>(a, b, split, a.sel ? &sv : nullptr);
+  RowCounts cnt;
+  attend_requests<NW>(a, b, split, cnt, sv);
   PrologueRaw praw;
   prologue_loads(a, b, praw);
+  __builtin_amdgcn_sched_barrier(0);  // every request above is issued before a count is read
+  const RowSources rs = attend_ranges(a, b, split, cnt);
   if (a.sel) store_sel<NW>(a, rs, sv, lds);
   attend_main<BITS, NW, NW == 4>(a, b, split, lds, praw, rs, nullptr);
 }
