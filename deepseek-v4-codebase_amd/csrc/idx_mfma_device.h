@@ -123,6 +123,10 @@ inline WsLayout layout(int64_t B, int64_t S) {
   return l;
 }
 
+// Counts read in place of a row's when a target lies past T (none) or a launch has no counts (all).
+__device__ const int32_t kCountNone = 0;
+__device__ const int32_t kCountAll = 0x7fffffff;
+
 // Row b's visible count (b uniform over the workgroup; S without counts).  The count is read
 // through the constant address space, which makes it a scalar load: the wait for it (where the
 // null check's branch joins) leaves the vector memory counter alone, so it does not wait for
@@ -584,9 +588,21 @@ idx_mfma_score_kernel(MfmaIdxArgs a) {
   int64_t nv[TT], nv_max = 0;
 #pragma unroll
   for (int tt = 0; tt < TT; ++tt) {
-    // (unconditional loads, requested with the query's: absent counts give all S)
-    nv[tt] = rok[tt] ? min<int64_t>(S, max(0, load_or(a.valid, row[tt], a.q, 0x7fffffff))) : 0;
-    nv_max = max(nv_max, nv[tt]);
+    // Prefill rows: unconditional scalar loads (uniform addresses, through the constant address
+    // space), requested with the query's.  No select acts on a loaded value (the compiler turns such a
+    // select into a branch around the load and waits for it where the branch joins, one target
+    // after the other): the pointer is selected instead, a target past T reading kCountNone and a
+    // launch without counts kCountAll.  Integer clamps (min<int64_t> lowers through doubles).
+    // Decode rows (TT = 1) keep one vector load beside the query's (its address falls back on the
+    // query's without counts; the constants' scalar load measured 0.1 us slower there).
+    if constexpr (TT > 1) {
+      const int32_t* vp = !rok[tt] ? &kCountNone : (a.valid ? a.valid + row[tt] : &kCountAll);
+      const int32_t v = *(const __attribute__((address_space(4))) int32_t*)vp;
+      nv[tt] = v <= 0 ? int64_t{0} : (v < S ? int64_t{v} : S);
+    } else {
+      nv[tt] = rok[tt] ? min<int64_t>(S, max(0, load_or(a.valid, row[tt], a.q, 0x7fffffff))) : 0;
+    }
+    nv_max = nv_max > nv[tt] ? nv_max : nv[tt];
   }
 
   __shared__ int8_t dig[4][16][IC];
