@@ -8,9 +8,10 @@
 // Two kernels instead of three: the wide score kernel (idx_mfma_device.h) writes every visible
 // key's order key and the 16-key slot maxima; then one workgroup per row selects the row's top-k
 // (select_row) and, in the same workgroup, attends the window and the selected blocks.  The window
-// does not depend on the selection: each wave requests its 16 window rows with the query in the
-// workgroup's first memory round, and attends them after the select while its group of 32 selected
-// blocks (k <= 256) is being gathered, so that neither the select nor the gather waits for it.  Fusing
+// does not depend on the selection: each wave requests its 16 window rows while the select waits
+// for its slot maxima (after them: loads complete in order), and attends them after the select
+// while its group of 32 selected blocks (k <= 256) is being gathered, so that neither the select
+// nor the gather waits for it.  Fusing
 // the two per-row stages also removes a kernel boundary and the global round trip of the selected
 // indices between them; the selection is that of the separate kernels, and the attention that of
 // the separate attention kernel up to the order in which the sources are summed (the entry point
